@@ -1,0 +1,107 @@
+/*
+ * C ABI of the MI355X (gfx950) WKV library, libwkv_hip.so.
+ *
+ * Plain pointers and sizes only; every entry point launches asynchronously on
+ * the HIP stream it is given (pass torch.cuda.current_stream().cuda_stream)
+ * and never allocates, frees or synchronises.  Tensors are contiguous,
+ * row-major: [B, T, C] with channels fastest, and their base addresses are
+ * 16-byte aligned (the kernels use vector loads and stores).  Return value: 0 on success,
+ * otherwise a nonzero code whose text wkv_last_error_string() gives (the
+ * message is thread-local).
+ *
+ * The reference runs this path as Triton kernels behind torch.library ops; the
+ * comment on each entry point names the reference interface it replaces.
+ */
+#ifndef WKV_HIP_H
+#define WKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of the [B,T,C] tensors (k, v, y, grad_y, grad_k, grad_v).
+ * Parameters (time_decay, time_first, w, u) and gradient sums are float32. */
+enum wkv_dtype {
+  WKV_DTYPE_F32 = 0,
+  WKV_DTYPE_BF16 = 1,
+  WKV_DTYPE_F16 = 2
+};
+
+enum wkv_status {
+  WKV_OK = 0,
+  WKV_ERR_INVALID_ARGUMENT = 1,
+  WKV_ERR_LAUNCH = 2,
+  WKV_ERR_WORKSPACE_TOO_SMALL = 3
+};
+
+/* RWKV-4 / SpikeGPT WKV forward.
+ *
+ * Replaces the kernel launch inside myelin::wkv_forward
+ * (src/spikegpt/wkv_triton.py:147-158) and myelin::wkv_forward_bf16io
+ * (src/spikegpt/wkv_bf16.py:143-154): y[b,t,c] from k, v [B,T,C] in `dtype`
+ * with fp32 recurrence state.  Unlike the Triton kernel (which takes the
+ * transformed w = -exp(time_decay) computed by the host wrapper), this entry
+ * point takes the raw fp32 time_decay [C] and time_first [C] and applies
+ * w = -exp(time_decay) itself, saving the wrapper's extra launch. */
+int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
+                 void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream);
+
+/* Bytes of device workspace wkv4_backward needs for these sizes (chunk
+ * checkpoints of the forward state plus per-batch parameter-gradient
+ * partials).  Replaces the reference's three [B,T,C] fp32 replay buffers
+ * (src/spikegpt/wkv_triton.py:170-172, wkv_bf16.py:167-169). */
+size_t wkv4_backward_workspace_bytes(int64_t B, int64_t T, int64_t C, int dtype);
+
+/* RWKV-4 / SpikeGPT WKV backward.
+ *
+ * Replaces the kernel launch and the batch sums inside myelin::wkv_backward
+ * (src/spikegpt/wkv_triton.py:164-194) and myelin::wkv_backward_bf16io
+ * (src/spikegpt/wkv_bf16.py:160-191).  Inputs: grad_y, k, v [B,T,C] in
+ * `dtype`; w = -exp(time_decay) and u = time_first, fp32 [C] (the op's own
+ * argument convention).  Outputs: grad_k, grad_v [B,T,C] in `dtype`;
+ * grad_time_decay [C] (already multiplied by w, the chain rule through
+ * w = -exp(time_decay)) and grad_time_first [C], both fp32 and summed over
+ * the batch.  `workspace` must hold wkv4_backward_workspace_bytes() bytes. */
+int wkv4_backward(const void* grad_y, const float* w, const float* u, const void* k, const void* v,
+                  void* grad_k, void* grad_v, float* grad_time_decay, float* grad_time_first,
+                  void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                  int dtype, void* stream);
+
+/* Single-token WKV decode step for generation.
+ *
+ * Replaces the eager WKV arithmetic of SpikeTimeMix.step
+ * (src/spikegpt/language.py:989-1012), which has no op in the reference.
+ * k, v [B,C] in `dtype`; time_decay, time_first fp32 [C]; state
+ * (numerator, denominator, log_scale) fp32 [B,C], natural-log units as in the
+ * reference.  Writes y [B,C] in `dtype` and the next state to
+ * num_out/den_out/log_scale_out (which may alias the inputs). */
+int wkv4_decode_step(const void* k, const void* v, const float* time_decay, const float* time_first,
+                     const float* num, const float* den, const float* log_scale, void* y,
+                     float* num_out, float* den_out, float* log_scale_out, int64_t B, int64_t C,
+                     int dtype, void* stream);
+
+/* RWKV-7 DPLR recurrence forward, per (batch, head) with head size N = 64:
+ *   S_t = S_{t-1} (diag(w_t) + a_t b_t^T) + v_t k_t^T,   y_t = S_t r_t
+ * r, w, k, v, a, b, y: [B,T,H,64] in `dtype`; S is [N_v=64, N_k=64] fp32.
+ * s0 (optional, may be NULL = zeros) and s_out (optional, may be NULL):
+ * [B,H,64,64] fp32.  The reference's RWKV-7 code was deleted
+ * (benchmarks/results/optimizer_wkv_experiments_5090.md:3); this op has no
+ * surviving counterpart there. */
+int wkv7_forward(const void* r, const void* w, const void* k, const void* v, const void* a,
+                 const void* b, const float* s0, void* y, float* s_out, int64_t B, int64_t T,
+                 int64_t H, int64_t N, int dtype, void* stream);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* wkv_last_error_string(void);
+
+/* Library version string. */
+const char* wkv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WKV_HIP_H */

@@ -1,0 +1,83 @@
+"""CPU oracle for the RWKV-7 DPLR recurrence (test infrastructure).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()``
+and ``bench.py``'s baseline leg; never by the product package.
+
+Recurrence, per (batch, head), head size N, state S [N_v, N_k]::
+
+    S_t = S_{t-1} (diag(w_t) + a_t b_t^T) + v_t k_t^T,    y_t = S_t r_t
+
+(the formula of the benchmark configuration; the reference's own RWKV-7 code
+was deleted, ``benchmarks/results/optimizer_wkv_experiments_5090.md:3``, and
+its arithmetic lived in the unpinned external ``fla`` package).  PARITY
+UNPINNED against the reference: there is no reference implementation, test or
+fixture to compare with.  What pins this restatement is mathematics only
+(``tests/test_oracle_wkv7.py``): with a = b = 0 it must equal causal
+(decayed) linear attention computed as a masked matrix product, autograd
+through it must agree with central finite differences, and the state carried
+across a split of the sequence must reproduce the unsplit run.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+
+def wkv7_loop(
+    r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor, state: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """Sequential recurrence in the inputs' dtype.
+
+    Inputs ``[B, T, H, N]``; ``state`` ``[B, H, N, N]`` (rows: value index,
+    columns: key index) or None for zeros.  Returns ``(y [B,T,H,N], S_T)``.
+    """
+    bsz, steps, heads, n = r.shape
+    dt = r.dtype
+    s = torch.zeros((bsz, heads, n, n), dtype=dt) if state is None else state.to(dt).clone()
+    ys = []
+    for t in range(steps):
+        rt, wt, kt, vt, at, bt = (x[:, t] for x in (r, w, k, v, a, b))  # [B, H, N]
+        sa = torch.einsum("bhij,bhj->bhi", s, at)
+        s = s * wt[:, :, None, :] + sa[..., :, None] * bt[:, :, None, :] + vt[..., :, None] * kt[:, :, None, :]
+        ys.append(torch.einsum("bhij,bhj->bhi", s, rt))
+    y = torch.stack(ys, dim=1) if steps else r.new_empty(r.shape)
+    return y, s
+
+
+def linear_attention(r: Tensor, w: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """Closed form of the a = b = 0 case as a masked matrix product.
+
+    ``y_t[i] = sum_{s<=t} v_s[i] * sum_j k_s[j] r_t[j] prod_{s<u<=t} w_u[j]``,
+    evaluated with cumulative log-decays (requires w > 0).
+    """
+    logw = torch.log(w)
+    cum = torch.cumsum(logw, dim=1)  # [B,T,H,N]: sum_{u<=t} log w_u
+    # decay from step s (exclusive) to t (inclusive): exp(cum_t - cum_s)
+    dec = torch.exp(cum[:, :, None] - cum[:, None, :])  # [B, t, s, H, N]
+    steps = r.shape[1]
+    mask = torch.tril(torch.ones(steps, steps, dtype=torch.bool))
+    scores = torch.einsum("bthj,btshj,bshj->bhts", r, dec, k)
+    scores = scores.masked_fill(~mask[None, None], 0.0)
+    return torch.einsum("bhts,bshi->bthi", scores, v)
+
+
+def make_inputs(batch: int, steps: int, heads: int, n: int = 64, *, seed: int, dtype=torch.float32):
+    """Seeded inputs with the benchmark distributions, drawn in this order:
+    x ~ N(-0.5, 1) -> w = exp(-exp(x)); r, k, v ~ N(0, 1); kappa ~ N(0, 1)
+    L2-normalised over each head's N channels; iclr = sigmoid(N(0, 1));
+    a = -kappa, b = kappa * iclr.  Returns ``(r, w, k, v, a, b)`` in ``dtype``.
+    """
+    g = torch.Generator().manual_seed(seed)
+    shape = (batch, steps, heads, n)
+    x = torch.randn(shape, generator=g) - 0.5
+    w = torch.exp(-torch.exp(x))
+    r = torch.randn(shape, generator=g)
+    k = torch.randn(shape, generator=g)
+    v = torch.randn(shape, generator=g)
+    kappa = torch.randn(shape, generator=g)
+    kappa = kappa / kappa.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    iclr = torch.sigmoid(torch.randn(shape, generator=g))
+    a = -kappa
+    b = kappa * iclr
+    return tuple(t.to(dtype) for t in (r, w, k, v, a, b))

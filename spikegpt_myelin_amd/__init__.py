@@ -1,0 +1,34 @@
+"""MI355X (gfx950) WKV time-mixing recurrence for SpikeGPT.
+
+Importing the package registers the ``myelin::`` custom ops backed by the HIP
+library ``libwkv_hip.so`` (built in-tree by ``python -m
+spikegpt_myelin_amd.build``):
+
+* ``myelin::wkv_forward`` / ``myelin::wkv_backward`` (fp32 I/O) and
+  ``myelin::wkv_forward_bf16io`` / ``myelin::wkv_backward_bf16io`` (16-bit
+  I/O) -- the reference's op names and schemas;
+* ``myelin::wkv_decode_step`` -- one-token WKV state update for generation;
+* ``myelin::wkv7_forward`` -- RWKV-7 DPLR recurrence.
+"""
+
+from .decode import initial_wkv_state, wkv_decode_step
+from .language import validate_wkv_inputs, weighted_key_value
+from .wkv import (
+    weighted_key_value_hip,
+    weighted_key_value_hip_bf16io,
+    weighted_key_value_triton,
+    weighted_key_value_triton_bf16io,
+)
+from .wkv7 import wkv7_forward
+
+__all__ = [
+    "initial_wkv_state",
+    "validate_wkv_inputs",
+    "weighted_key_value",
+    "weighted_key_value_hip",
+    "weighted_key_value_hip_bf16io",
+    "weighted_key_value_triton",
+    "weighted_key_value_triton_bf16io",
+    "wkv7_forward",
+    "wkv_decode_step",
+]

@@ -1,0 +1,116 @@
+"""ctypes binding of libwkv_hip.so (the C ABI declared in include/wkv_hip.h).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime
+torch already loaded (both carry the soname ``libamdhip64.so.7``); the stream
+handles torch hands out are then valid in the library.  There is no fallback:
+if the shared library is missing the first call raises ``RuntimeError`` naming
+the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  -- must load torch's HIP runtime first
+
+LIB_PATH = Path(__file__).resolve().parent / "libwkv_hip.so"
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+DTYPE_F16 = 2
+
+_TORCH_TO_CODE = {
+    torch.float32: DTYPE_F32,
+    torch.bfloat16: DTYPE_BF16,
+    torch.float16: DTYPE_F16,
+}
+
+# Every exported entry point: name -> (restype, argtypes).
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_SZ = ctypes.c_size_t
+SIGNATURES = {
+    "wkv4_forward": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
+    "wkv4_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _INT]),
+    "wkv4_backward": (
+        _INT,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P],
+    ),
+    "wkv4_decode_step": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
+    "wkv7_forward": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]),
+    "wkv_last_error_string": (ctypes.c_char_p, []),
+    "wkv_version": (ctypes.c_char_p, []),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library with typed entry points."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m spikegpt_myelin_amd.build` "
+                "(the WKV ops have no non-HIP implementation)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _TORCH_TO_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"WKV kernels take float32, bfloat16 or float16 tensors; got {dtype}") from None
+
+
+def check(rc: int, what: str) -> None:
+    """Map a nonzero C ABI status to ``RuntimeError`` with the library's message."""
+    if rc != 0:
+        msg = load().wkv_last_error_string().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def aligned(t: torch.Tensor) -> torch.Tensor:
+    """``t`` contiguous with a 16-byte-aligned base address (copied if not)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The calling thread's current HIP stream on ``t``'s device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    """The ops run only on a HIP device; there is no CPU implementation."""
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "myelin WKV ops run on the GPU (HIP) only; got a tensor on "
+                f"{t.device}. Move inputs to the GPU."
+            )
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on one device; got {dev} and {t.device}")

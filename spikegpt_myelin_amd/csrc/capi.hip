@@ -1,0 +1,169 @@
+// C ABI entry points of libwkv_hip.so (declared in include/wkv_hip.h).
+//
+// Argument checks happen here, on the host, before any launch: a kernel is
+// only launched on shapes its grid and indexing were written for.  Nothing in
+// this file allocates, frees or synchronises.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <initializer_list>
+#include <string>
+
+#include "../../include/wkv_hip.h"
+#include "wkv_common.h"
+
+namespace wkv_host {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  set_error(msg);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    return fail(WKV_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(err));
+  }
+  return WKV_OK;
+}
+
+// Channels per lane of the RWKV-4 kernels: 2 (one 32-bit bf16 pair / one
+// 64-bit fp32 pair per lane per step) when that still gives every CU a row
+// (B * ceil(C/128) >= 256 workgroups), else 1 for twice as many rows.
+// WKV_VEC=1|2 in the environment overrides the choice (tuning only).
+int pick_vec(int64_t B, int64_t C) {
+  if (C % 2 != 0) return 1;
+  static const int env = [] {
+    const char* s = getenv("WKV_VEC");
+    return s ? atoi(s) : 0;
+  }();
+  if (env == 1 || env == 2) return env;
+  const int64_t rows2 = B * ((C + 127) / 128);
+  return rows2 >= 256 ? 2 : 1;
+}
+
+// Parses "vec,L,W" from an environment variable (tile tuning only).
+bool env_cfg(const char* name, int& vec, int& L, int& W) {
+  const char* s = getenv(name);
+  if (!s) return false;
+  return sscanf(s, "%d,%d,%d", &vec, &L, &W) == 3;
+}
+
+int wkv4_forward_impl(const void*, const void*, const float*, const float*, void*, int, int, int,
+                      int, hipStream_t);
+int wkv4_backward_impl(const void*, const float*, const float*, const void*, const void*, void*,
+                       void*, float*, float*, float*, int, int, int, int, hipStream_t);
+size_t wkv4_bwd_workspace_bytes_impl(int64_t, int64_t, int64_t, int);
+int wkv4_zero_param_grads(float*, float*, int, hipStream_t);
+int wkv4_decode_impl(const void*, const void*, const float*, const float*, const float*,
+                     const float*, const float*, void*, float*, float*, float*, int, int, int,
+                     hipStream_t);
+int wkv7_forward_impl(const void*, const void*, const void*, const void*, const void*,
+                      const void*, const float*, void*, float*, int, int, int, int, hipStream_t);
+
+static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }
+
+// Tensors are read and written with vector instructions of up to 16 bytes.
+static bool aligned16(std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+  return true;
+}
+
+// Every index the kernels form is int32 per dimension and size_t overall.
+static bool dims_ok(int64_t B, int64_t T, int64_t C) {
+  const int64_t lim = int64_t(1) << 31;
+  return B >= 0 && T >= 0 && C >= 0 && B < lim && T < lim && C < lim && B * T < lim * 64;
+}
+
+}  // namespace wkv_host
+
+using namespace wkv_host;
+
+extern "C" {
+
+int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
+                 void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: bad sizes");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!k || !v || !time_decay || !time_first || !y)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: null pointer");
+  if (!aligned16({k, v, y}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: k, v, y must be 16-byte aligned");
+  return wkv4_forward_impl(k, v, time_decay, time_first, y, int(B), int(T), int(C), dtype,
+                           static_cast<hipStream_t>(stream));
+}
+
+size_t wkv4_backward_workspace_bytes(int64_t B, int64_t T, int64_t C, int dtype) {
+  if (!dtype_ok(dtype) || !dims_ok(B, T, C)) return 0;
+  return wkv4_bwd_workspace_bytes_impl(B, T, C, dtype);
+}
+
+int wkv4_backward(const void* grad_y, const float* w, const float* u, const void* k, const void* v,
+                  void* grad_k, void* grad_v, float* grad_time_decay, float* grad_time_first,
+                  void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                  int dtype, void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: bad sizes");
+  if (C == 0) return WKV_OK;
+  if (!grad_time_decay || !grad_time_first)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0 || T == 0) return wkv4_zero_param_grads(grad_time_decay, grad_time_first, int(C), s);
+  if (!grad_y || !w || !u || !k || !v || !grad_k || !grad_v || !workspace)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: null pointer");
+  const size_t need = wkv4_bwd_workspace_bytes_impl(B, T, C, dtype);
+  if (workspace_bytes < need)
+    return fail(WKV_ERR_WORKSPACE_TOO_SMALL,
+                "wkv4_backward: workspace too small (need " + std::to_string(need) + " bytes)");
+  if (!aligned16({grad_y, k, v, grad_k, grad_v, workspace}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv4_backward: grad_y, k, v, grad_k, grad_v, workspace must be 16-byte aligned");
+  return wkv4_backward_impl(grad_y, w, u, k, v, grad_k, grad_v, grad_time_decay, grad_time_first,
+                            static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
+}
+
+int wkv4_decode_step(const void* k, const void* v, const float* time_decay, const float* time_first,
+                     const float* num, const float* den, const float* log_scale, void* y,
+                     float* num_out, float* den_out, float* log_scale_out, int64_t B, int64_t C,
+                     int dtype, void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_decode_step: unknown dtype");
+  if (!dims_ok(B, 1, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_decode_step: bad sizes");
+  if (B == 0 || C == 0) return WKV_OK;
+  if (!k || !v || !time_decay || !time_first || !num || !den || !log_scale || !y || !num_out ||
+      !den_out || !log_scale_out)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_decode_step: null pointer");
+  if (!aligned16({k, v, num, den, log_scale, y, num_out, den_out, log_scale_out}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_decode_step: tensors must be 16-byte aligned");
+  return wkv4_decode_impl(k, v, time_decay, time_first, num, den, log_scale, y, num_out, den_out,
+                          log_scale_out, int(B), int(C), dtype, static_cast<hipStream_t>(stream));
+}
+
+int wkv7_forward(const void* r, const void* w, const void* k, const void* v, const void* a,
+                 const void* b, const float* s0, void* y, float* s_out, int64_t B, int64_t T,
+                 int64_t H, int64_t N, int dtype, void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: unknown dtype");
+  if (N != 64) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: head size must be 64");
+  if (!dims_ok(B, T, H * N)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: bad sizes");
+  if (B == 0 || H == 0) return WKV_OK;
+  if (T > 0 && (!r || !w || !k || !v || !a || !b || !y))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: null pointer");
+  if (T == 0 && !s_out) return WKV_OK;
+  return wkv7_forward_impl(r, w, k, v, a, b, s0, y, s_out, int(B), int(T), int(H), dtype,
+                           static_cast<hipStream_t>(stream));
+}
+
+const char* wkv_last_error_string(void) { return g_last_error.c_str(); }
+
+const char* wkv_version(void) { return "wkv_hip 0.1.0 gfx950"; }
+
+}  // extern "C"

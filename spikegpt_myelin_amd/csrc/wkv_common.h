@@ -1,0 +1,185 @@
+// Shared device helpers for the gfx950 WKV kernels: element I/O for
+// fp32/bf16/fp16 tensors, base-2 transcendentals, and the host-side error
+// channel of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace wkv {
+
+// log2(e): every kernel keeps exponents in base 2 so that exp(x) is one
+// v_exp_f32 of x * log2(e) folded into the operands once per element.
+constexpr float kLog2e = 1.4426950408889634f;
+// "Minus infinity" log-scale of an empty state, the value the reference
+// kernels start from (wkv_triton.py:43), expressed in base-2 units.
+constexpr float kNegHuge = -1e38f;
+
+// ---------------------------------------------------------------- math ----
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// ----------------------------------------------------------- element I/O --
+// Element tags; storage is raw bits for the 16-bit types so that the kernels
+// control conversions (bf16 widening is a shift; narrowing is round to
+// nearest even via the hardware converter).
+struct F32 { using raw = float; };
+struct BF16 { using raw = uint16_t; };
+struct F16 { using raw = uint16_t; };
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float x) {
+  __bf16 h = static_cast<__bf16>(x);  // RNE, NaN-preserving
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16));
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ uint16_t float_to_f16_bits(float x) {
+  _Float16 h = static_cast<_Float16>(x);  // RNE
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Vector of VEC consecutive channels as loaded by one lane in one
+// instruction: raw bits held in 32-bit words.
+template <typename E, int VEC> struct Pack;
+
+template <int VEC> struct Pack<F32, VEC> {
+  float x[VEC];
+  __device__ __forceinline__ void load(const float* p) {
+    if constexpr (VEC == 1) {
+      x[0] = *p;
+    } else if constexpr (VEC == 2) {
+      float2 t = *reinterpret_cast<const float2*>(p);
+      x[0] = t.x; x[1] = t.y;
+    } else {
+      static_assert(VEC == 4, "VEC");
+      float4 t = *reinterpret_cast<const float4*>(p);
+      x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[c] = 0.f;
+  }
+  __device__ __forceinline__ float get(int c) const { return x[c]; }
+};
+
+template <int VEC> struct Pack<BF16, VEC> {
+  static constexpr int W = (VEC + 1) / 2;
+  uint32_t u[W];
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    if constexpr (VEC == 1) {
+      u[0] = *p;
+    } else if constexpr (VEC == 2) {
+      u[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else {
+      static_assert(VEC == 4, "VEC");
+      uint2 t = *reinterpret_cast<const uint2*>(p);
+      u[0] = t.x; u[1] = t.y;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < W; ++i) u[i] = 0u;
+  }
+  __device__ __forceinline__ float get(int c) const {
+    const uint32_t w = u[c >> 1];
+    return (c & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  }
+};
+
+template <int VEC> struct Pack<F16, VEC> {
+  static constexpr int W = (VEC + 1) / 2;
+  uint32_t u[W];
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    if constexpr (VEC == 1) {
+      u[0] = *p;
+    } else if constexpr (VEC == 2) {
+      u[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else {
+      static_assert(VEC == 4, "VEC");
+      uint2 t = *reinterpret_cast<const uint2*>(p);
+      u[0] = t.x; u[1] = t.y;
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < W; ++i) u[i] = 0u;
+  }
+  __device__ __forceinline__ float get(int c) const {
+    const uint32_t w = u[c >> 1];
+    return f16_bits_to_float((c & 1) ? (w >> 16) : (w & 0xffffu));
+  }
+};
+
+// Store VEC floats as one vector store of the element type.
+template <typename E, int VEC>
+__device__ __forceinline__ void store_vec(typename E::raw* p, const float (&x)[VEC]) {
+  if constexpr (sizeof(typename E::raw) == 4) {
+    if constexpr (VEC == 1) {
+      *p = x[0];
+    } else if constexpr (VEC == 2) {
+      *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+    } else {
+      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+  } else {
+    uint16_t h[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      if constexpr (__is_same(E, BF16)) {
+        h[c] = float_to_bf16_bits(x[c]);
+      } else {
+        h[c] = float_to_f16_bits(x[c]);
+      }
+    }
+    if constexpr (VEC == 1) {
+      *p = h[0];
+    } else if constexpr (VEC == 2) {
+      *reinterpret_cast<uint32_t*>(p) = uint32_t(h[0]) | (uint32_t(h[1]) << 16);
+    } else {
+      *reinterpret_cast<uint2*>(p) = make_uint2(uint32_t(h[0]) | (uint32_t(h[1]) << 16),
+                                                uint32_t(h[2]) | (uint32_t(h[3]) << 16));
+    }
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ float load_scalar(const typename E::raw* p) {
+  if constexpr (__is_same(E, F32)) {
+    return *p;
+  } else if constexpr (__is_same(E, BF16)) {
+    return bf16_bits_to_float(*p);
+  } else {
+    return f16_bits_to_float(*p);
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ void store_scalar(typename E::raw* p, float x) {
+  if constexpr (__is_same(E, F32)) {
+    *p = x;
+  } else if constexpr (__is_same(E, BF16)) {
+    *p = float_to_bf16_bits(x);
+  } else {
+    *p = float_to_f16_bits(x);
+  }
+}
+
+}  // namespace wkv
+
+// ------------------------------------------------------------ host side ---
+namespace wkv_host {
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+}  // namespace wkv_host

@@ -1,0 +1,295 @@
+"""GPU parity of the RWKV-4 WKV ops against the float64 CPU oracle.
+
+Tolerances (written per test):
+* fp32 I/O: elementwise ``rtol=1e-5`` with ``atol=1e-5 * max|ref|`` and a
+  normwise relative error below 1e-5, against the float64 oracle evaluated on
+  the same fp32 inputs;
+* bf16/fp16 I/O: ``rtol=2e-2, atol=1e-2`` against the float64 oracle on the
+  same (already rounded) 16-bit inputs;
+* the 16-bit-I/O op must equal the fp32 op's output rounded to the 16-bit
+  type bit for bit whenever both use the same tile configuration (the
+  widening is exact and both round once at the store).
+
+Shapes mirror the reference's tests (tests/test_wkv_triton.py: B=3, C=96,
+T in {1, 7, 64}; C=70) plus the benchmark shapes and edge cases.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import wkv4 as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _lib_ops():
+    import spikegpt_myelin_amd  # noqa: F401  -- registers the ops
+
+    return torch.ops.myelin
+
+
+def _close(got, ref, *, rtol, atol_scale, norm_tol=None, what=""):
+    got = got.double().cpu()
+    ref = ref.double().cpu()
+    scale = float(ref.abs().max()) if ref.numel() else 0.0
+    atol = atol_scale * max(scale, 1e-30)
+    ok = torch.allclose(got, ref, rtol=rtol, atol=atol)
+    err = (got - ref).abs().max().item() if ref.numel() else 0.0
+    assert ok, f"{what}: max abs err {err:.3e} (atol {atol:.3e}, rtol {rtol})"
+    if norm_tol is not None and ref.numel():
+        rel = ((got - ref).norm() / ref.norm().clamp_min(1e-300)).item()
+        assert rel < norm_tol, f"{what}: normwise rel err {rel:.3e} >= {norm_tol}"
+
+
+def _grads(fn, k0, v0, td0, tf0, gy):
+    """The reference test's helper (tests/test_wkv_triton.py:21-32)."""
+    k = k0.clone().requires_grad_(True)
+    v = v0.clone().requires_grad_(True)
+    td = td0.clone().requires_grad_(True)
+    tf = tf0.clone().requires_grad_(True)
+    y = fn(k, v, td, tf)
+    y.backward(gy)
+
+    def z(grad, ref):
+        return torch.zeros_like(ref) if grad is None else grad
+
+    return y.detach(), z(k.grad, k), z(v.grad, v), z(td.grad, td), z(tf.grad, tf)
+
+
+def _oracle64(k, v, td, tf, gy):
+    """float64 oracle on exactly the inputs the GPU saw."""
+    return O.autograd_grads(k.cpu().double(), v.cpu().double(), td.cpu().double(), tf.cpu().double(),
+                            gy.cpu().double())
+
+
+def _oracle64_fast(k, v, td, tf, gy):
+    """Same values via the loop + the pinned explicit backward (no autograd
+    graph), for benchmark-sized inputs."""
+    k64, v64, td64, tf64, gy64 = (x.cpu().double() for x in (k, v, td, tf, gy))
+    y = O.wkv_loop(k64, v64, td64, tf64)
+    gk, gv, gtd, gtf = O.reference_backward(gy64, -torch.exp(td64), tf64, k64, v64)
+    return y, gk, gv, gtd, gtf
+
+
+FP32_TOL = dict(rtol=1e-5, atol_scale=1e-5, norm_tol=1e-5)
+BF16_TOL = dict(rtol=2e-2, atol_scale=1e-2)
+
+
+@pytest.mark.parametrize("steps", [1, 7, 64])
+def test_fp32_op_forward_and_backward_match_oracle(steps):
+    from spikegpt_myelin_amd import weighted_key_value_hip
+
+    torch.manual_seed(steps)
+    b, c = 3, 96
+    k0 = torch.randn(b, steps, c, device=DEV)
+    v0 = torch.randn(b, steps, c, device=DEV)
+    td0 = torch.randn(c, device=DEV)
+    tf0 = torch.randn(c, device=DEV)
+    gy = torch.randn(b, steps, c, device=DEV)
+    got = _grads(weighted_key_value_hip, k0, v0, td0, tf0, gy)
+    ref = _oracle64(k0, v0, td0, tf0, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        assert g.dtype == torch.float32
+        _close(g, r, what=f"T={steps} {name}", **FP32_TOL)
+
+
+def test_fp32_op_channels_not_multiple_of_block():
+    from spikegpt_myelin_amd import weighted_key_value_hip
+
+    torch.manual_seed(0)
+    b, t, c = 2, 16, 70
+    k0, v0 = torch.randn(b, t, c, device=DEV), torch.randn(b, t, c, device=DEV)
+    td0, tf0 = torch.randn(c, device=DEV), torch.randn(c, device=DEV)
+    gy = torch.randn(b, t, c, device=DEV)
+    got = _grads(weighted_key_value_hip, k0, v0, td0, tf0, gy)
+    ref = _oracle64(k0, v0, td0, tf0, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"C=70 {name}", **FP32_TOL)
+
+
+@pytest.mark.parametrize(
+    "b,t,c,seed",
+    [(2, 128, 512, 0), (3, 300, 96, 1), (2, 513, 64, 2), (1, 5, 33, 3), (4, 1000, 130, 4)],
+)
+def test_fp32_op_benchmark_distributions(b, t, c, seed):
+    # config distributions: td ~ U(-5, 1), tf ~ N(0, 0.5), k clamped to +-30.
+    ops = _lib_ops()
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=seed)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    y = ops.wkv_forward(kd, vd, tdd, tfd)
+    w = -torch.exp(tdd)
+    gk, gv, gtd, gtf = ops.wkv_backward(gyd, w, tfd, kd, vd)
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"{(b, t, c)} {name}", **FP32_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,t,c,seed", [(3, 96, 96, 5), (2, 257, 512, 6), (4, 64, 70, 7)])
+def test_16bit_io_op_matches_oracle(dtype, b, t, c, seed):
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=seed, dtype=dtype)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    got = _grads(weighted_key_value_hip_bf16io, kd, vd, tdd, tfd, gyd)
+    assert got[0].dtype == dtype and got[1].dtype == dtype and got[3].dtype == torch.float32
+    ref = _oracle64(k, v, td, tf, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"{dtype} {(b, t, c)} {name}", **BF16_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_16bit_io_equals_fp32_op_rounded(dtype):
+    # wkv_bf16.py:11-14: same arithmetic on exactly widened inputs, one
+    # rounding at the store.  Small B keeps both ops on one tile config.
+    ops = _lib_ops()
+    k, v, td, tf, gy = O.make_inputs(2, 200, 128, seed=8, dtype=dtype)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    y16 = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
+    y32 = ops.wkv_forward(kd.float(), vd.float(), tdd, tfd)
+    assert torch.equal(y16, y32.to(dtype))
+    w = -torch.exp(tdd)
+    g16 = ops.wkv_backward_bf16io(gyd, w, tfd, kd, vd)
+    g32 = ops.wkv_backward(gyd.float(), w, tfd, kd.float(), vd.float())
+    assert torch.equal(g16[0], g32[0].to(dtype))
+    assert torch.equal(g16[1], g32[1].to(dtype))
+    assert torch.equal(g16[2], g32[2]) and torch.equal(g16[3], g32[3])
+
+
+def test_fp32_op_with_bf16_inputs_returns_bf16_like_reference():
+    # wkv_triton.py:158: fp32 math, y.to(key.dtype).
+    ops = _lib_ops()
+    k, v, td, tf, _ = O.make_inputs(2, 50, 64, seed=9, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd = (x.to(DEV) for x in (k, v, td, tf))
+    y = ops.wkv_forward(kd, vd, tdd, tfd)
+    assert y.dtype == torch.bfloat16
+    ref = ops.wkv_forward(kd.float(), vd.float(), tdd, tfd).to(torch.bfloat16)
+    assert torch.equal(y, ref)
+
+
+def test_bf16_benchmark_shape_full_size():
+    # B=64, T=1024, C=512 bf16 (the headline workload) against the fp64 oracle,
+    # plus size-independent gradient invariants.
+    ops = _lib_ops()
+    b, t, c = 64, 1024, 512
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=1, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
+    gk, gv, gtd, gtf = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
+    torch.cuda.synchronize()
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"full {name}", **BF16_TOL)
+    # Per lane: sum_t gk = 0 and sum_t gv = sum_t gy exactly in real
+    # arithmetic; each bf16 output carries a relative rounding error <= 2^-8,
+    # which bounds the residual by 2^-8 * sum_t |g|.
+    gk64, gv64 = gk.double().cpu(), gv.double().cpu()
+    bound_k = gk64.abs().sum(1) * 2.0**-8 + 1e-6
+    bound_v = gv64.abs().sum(1) * 2.0**-8 + 1e-6
+    assert bool((gk64.sum(1).abs() <= bound_k).all())
+    assert bool(((gv64.sum(1) - gy.double().sum(1)).abs() <= bound_v).all())
+
+
+def test_long_context_shape_against_oracle():
+    # B=24, T=3072, C=512 bf16 (the long-context workload), 4 batch rows.
+    ops = _lib_ops()
+    k, v, td, tf, gy = O.make_inputs(4, 3072, 512, seed=2, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
+    gk, gv, gtd, gtf = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"T=3072 {name}", **BF16_TOL)
+
+
+@pytest.mark.parametrize("kind", ["wide_keys", "large_time_first", "one_bad_channel"])
+def test_out_of_range_inputs_take_the_exact_path(kind):
+    # Keys spanning > 96 base-2 exponents inside one segment, or |u| > 16,
+    # are outside the shared-frame range; such rows are recomputed with the
+    # running-max recurrence and must still match the oracle.
+    ops = _lib_ops()
+    b, t, c = 2, 200, 64
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=10)
+    if kind == "wide_keys":
+        k[:, ::7] = 80.0
+        k[:, 3::7] = -80.0
+    elif kind == "large_time_first":
+        tf[:] = 30.0
+    else:
+        k[1, 50, 5] = 120.0
+        k[1, 51, 5] = -40.0
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    y = ops.wkv_forward(kd, vd, tdd, tfd)
+    gk, gv, gtd, gtf = ops.wkv_backward(gyd, -torch.exp(tdd), tfd, kd, vd)
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
+        assert torch.isfinite(g).all(), f"{kind} {name} not finite"
+        _close(g, r, rtol=1e-4, atol_scale=1e-5, what=f"{kind} {name}")
+
+
+def test_empty_sequence_and_batch():
+    ops = _lib_ops()
+    for shape in [(2, 0, 8), (0, 5, 8)]:
+        k = torch.randn(shape, device=DEV)
+        y = ops.wkv_forward(k, k, torch.zeros(8, device=DEV), torch.zeros(8, device=DEV))
+        assert y.shape == shape
+        gk, gv, gtd, gtf = ops.wkv_backward(k, torch.zeros(8, device=DEV), torch.zeros(8, device=DEV), k, k)
+        assert gk.shape == shape and torch.equal(gtd.cpu(), torch.zeros(8))
+        assert torch.equal(gtf.cpu(), torch.zeros(8))
+
+
+def test_deterministic():
+    ops = _lib_ops()
+    k, v, td, tf, gy = O.make_inputs(8, 512, 256, seed=11, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    w = -torch.exp(tdd)
+    a = ops.wkv_backward_bf16io(gyd, w, tfd, kd, vd)
+    bb = ops.wkv_backward_bf16io(gyd, w, tfd, kd, vd)
+    for x, y in zip(a, bb):
+        assert torch.equal(x, y)
+    assert torch.equal(ops.wkv_forward_bf16io(kd, vd, tdd, tfd), ops.wkv_forward_bf16io(kd, vd, tdd, tfd))
+
+
+def test_all_tile_configurations_agree(monkeypatch):
+    # Every compiled tile configuration computes the same function.  The
+    # library reads WKV_FWD_CFG / WKV_BWD_CFG ("vec,L,W") at each call.
+    ops = _lib_ops()
+    inputs = O.make_inputs(3, 700, 256, seed=12, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in inputs)
+    ref = _oracle64_fast(*inputs)
+    cfgs = [("1,8,16", "1,8,16"), ("2,8,16", "2,4,16"), ("2,8,8", "2,8,8"), ("1,16,8", "1,16,8"),
+            ("1,8,16", "1,4,16")]
+    for fc, bc in cfgs:
+        monkeypatch.setenv("WKV_FWD_CFG", fc)
+        monkeypatch.setenv("WKV_BWD_CFG", bc)
+        print(f"tile config fwd={fc} bwd={bc}", flush=True)
+        y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
+        g = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
+        for got, r, name in zip((y, *g), ref, ("y", "gk", "gv", "gtd", "gtf")):
+            _close(got, r, what=f"cfg {fc}/{bc} {name}", **BF16_TOL)
+
+
+def test_compiles_without_graph_breaks():
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    def f(k, v, td, tf):
+        return weighted_key_value_hip_bf16io(k, v, td, tf) * 2.0
+
+    k, v, td, tf, _ = O.make_inputs(2, 40, 64, seed=13, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd = (x.to(DEV) for x in (k, v, td, tf))
+    cf = torch.compile(f, backend="aot_eager", fullgraph=True)
+    assert torch.equal(cf(kd, vd, tdd, tfd), f(kd, vd, tdd, tfd))
+
+
+def test_language_entry_point_dispatch_and_validation():
+    from spikegpt_myelin_amd import weighted_key_value
+
+    k, v, td, tf, _ = O.make_inputs(2, 30, 32, seed=14, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd = (x.to(DEV) for x in (k, v, td, tf))
+    assert torch.equal(weighted_key_value(kd, vd, tdd, tfd), torch.ops.myelin.wkv_forward_bf16io(kd, vd, tdd, tfd))
+    with pytest.raises(ValueError, match="same shape"):
+        weighted_key_value(kd, vd[..., :16], tdd, tfd)
