@@ -1,0 +1,296 @@
+"""Benchmark of the WKV time-mixing recurrence on one MI355X.
+
+Default workload (one JSON line on stdout): RWKV-4 / SpikeGPT WKV forward +
+backward, bf16 I/O with fp32 state, B=64, T=1024, C=512 -- the 41M SpikeGPT
+training shape.  A "step" is one pass of the op path over one batch that is
+already resident in HBM: ``y = myelin::wkv_forward_bf16io(k, v, td, tf)``
+then ``torch.autograd.grad(y, (k, v, td, tf), dy)`` (the registered autograd,
+which calls ``myelin::wkv_backward_bf16io``).
+
+Reported beside the throughput:
+* ``roofline`` -- the dominant launch (the backward, whose C-ABI call issues
+  the main kernel plus the small batch-sum kernel), timed live with HIP events
+  recorded on the launch stream around every call inside the timed region;
+  algorithmic bytes = 10 B per [B,T,C] element (k, v, dy read, dk, dv
+  written); peak 8 TB/s.  ``traffic`` comes from the committed rocprofv3 PMC
+  summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters
+  on a copy of known size) when present, else null.
+* ``cpu_baseline`` -- the reference's CPU WKV path restated in eager PyTorch
+  (the sequential loop of src/spikegpt/language.py:399-449 in fp32, backward
+  by autograd) on a bounded sample of the same workload, on this host's cores.
+
+Other workloads (``--workload``): ``long`` (B=24, T=3072, C=512), ``216m``
+(B=16, T=1024, C=768, 18 layers), ``decode`` (B=256, C=768, 18 layers, fp32
+state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward), ``c0`` (fp32
+forward B=2, T=128, C=512).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0
+FP32_VALU_PEAK_TFLOPS = 157.3
+METRIC = "WKV fwd+bwd tokens/sec & HBM GB/s (% of peak), B=64 T=1024 C=512 bf16"
+
+WORKLOADS = {
+    "wkv4": dict(B=64, T=1024, C=512, dtype=torch.bfloat16, layers=1),
+    "long": dict(B=24, T=3072, C=512, dtype=torch.bfloat16, layers=1),
+    "216m": dict(B=16, T=1024, C=768, dtype=torch.bfloat16, layers=18),
+    "c0": dict(B=2, T=128, C=512, dtype=torch.float32, layers=1),
+}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(B: int, T: int, C: int, sample_batch: int, fwd_only: bool = False) -> dict:
+    """The reference CPU path (eager loop, fp32, autograd) on a batch sample."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import wkv4 as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    bs = min(B, sample_batch)
+    k, v, td, tf, dy = O.make_inputs(bs, T, C, seed=0, dtype=torch.bfloat16)
+    k, v, dy = k.float(), v.float(), dy.float()  # the reference upcasts (language.py:483-485)
+
+    def once():
+        if fwd_only:
+            with torch.no_grad():
+                O.wkv_loop(k, v, td, tf)
+            return
+        leaves = [x.clone().requires_grad_(True) for x in (k, v, td, tf)]
+        y = O.wkv_loop(*leaves)
+        torch.autograd.grad(y, leaves, dy)
+
+    once()  # warmup
+    times = []
+    budget = time.perf_counter() + 20.0
+    while len(times) < 3 and (not times or time.perf_counter() < budget):
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": bs * T / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"B={bs} of {B}, T={T}, C={C}, fp32 eager loop "
+                   f"{'forward' if fwd_only else 'forward+autograd backward'}, "
+                   f"median of {len(times)} after 1 warmup; host {_cpu_model()}, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def read_traffic(path: Path, kernel: str) -> int | None:
+    """HBM bytes per dispatch of ``kernel`` from a committed PMC summary.
+
+    The summary lists ``traffic_bytes <kernel> <N>`` lines (FETCH_SIZE +
+    WRITE_SIZE scaled by a copy-kernel calibration)."""
+    if not path.exists():
+        return None
+    m = re.search(rf"^traffic_bytes\s+{re.escape(kernel)}\s+(\d+)", path.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def bench_wkv4(args, cfg) -> dict:
+    import spikegpt_myelin_amd  # noqa: F401  -- registers the ops
+    from spikegpt_myelin_amd import _lib
+    from oracle import wkv4 as O
+
+    B, T, C, dtype, layers = cfg["B"], cfg["T"], cfg["C"], cfg["dtype"], cfg["layers"]
+    dev = torch.device("cuda", 0)
+    k, v, td, tf, dy = (x.to(dev) for x in O.make_inputs(B, T, C, seed=1, dtype=dtype))
+    leaves = [x.requires_grad_(True) for x in (k, v, td, tf)]
+    fwd = torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32 else torch.ops.myelin.wkv_forward
+    fwd_only = args.workload == "c0"
+
+    def step():
+        for _ in range(layers):
+            if fwd_only:
+                with torch.no_grad():
+                    fwd(*leaves)
+            else:
+                y = fwd(*leaves)
+                torch.autograd.grad(y, leaves, dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.EVENT_LOG = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    log, _lib.EVENT_LOG = _lib.EVENT_LOG, None
+
+    esize = torch.finfo(dtype).bits // 8
+    n_elem = B * T * C * layers
+    per_launch = {}
+    for name, s, e in log:
+        per_launch.setdefault(name, []).append(s.elapsed_time(e) * 1e-3)
+    fwd_s = statistics.mean(per_launch.get("wkv4_forward", [float("nan")]))
+    tokens = B * T * args.steps
+    value = tokens / elapsed
+    step_s = elapsed / args.steps
+    alg_step = (3 * esize if fwd_only else 8 * esize) * n_elem  # fwd 3, bwd 5 tensors
+    out = {
+        "metric": METRIC if args.workload == "wkv4" else f"WKV {'fwd' if fwd_only else 'fwd+bwd'} tokens/sec "
+                                                        f"B={B} T={T} C={C} x{layers} layers",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"wkv4_{'fwd' if fwd_only else 'fwd_bwd'}", "B": B, "T": T, "C": C,
+                   "layers": layers, "io_dtype": str(dtype).replace("torch.", ""),
+                   "state_dtype": "float32", "parallelism": "single_gpu"},
+        "hbm_gbps_algorithmic": alg_step / step_s / 1e9,
+        "hbm_frac_of_peak": alg_step / step_s / 1e9 / HBM_PEAK_GBS,
+        "fwd_launch_us": fwd_s * 1e6,
+    }
+    if fwd_only:
+        dom, dom_bytes, dom_t = "wkv4_fwd_kernel", 3 * esize * B * T * C, fwd_s
+    else:
+        bwd_s = statistics.mean(per_launch["wkv4_backward"])
+        out["bwd_launch_us"] = bwd_s * 1e6
+        dom, dom_bytes, dom_t = "wkv4_bwd_kernel", 5 * esize * B * T * C, bwd_s
+    achieved = dom_bytes / dom_t / 1e9
+    traffic = read_traffic(ROOT / "profiles" / args.traffic_file, dom) if args.traffic_file else None
+    out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
+                       "algorithmic_bytes_per_launch": dom_bytes,
+                       "avg_launch_us": dom_t * 1e6}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, T, C, args.cpu_sample_batch, fwd_only=fwd_only)
+    return out
+
+
+def bench_decode(args) -> dict:
+    import spikegpt_myelin_amd  # noqa: F401
+    from spikegpt_myelin_amd import initial_wkv_state
+    from oracle import wkv4 as O
+
+    B, C, layers = 256, 768, 18
+    dev = torch.device("cuda", 0)
+    ks, vs, tds, tfs = [], [], [], []
+    for layer in range(layers):
+        k, v, td, tf, _ = O.make_inputs(B, 1, C, seed=100 + layer, with_grad=False)
+        ks.append(k[:, 0].to(dev)); vs.append(v[:, 0].to(dev)); tds.append(td.to(dev)); tfs.append(tf.to(dev))
+    states = [initial_wkv_state(B, C, dev) for _ in range(layers)]
+
+    def step():
+        for layer in range(layers):
+            y, *st = torch.ops.myelin.wkv_decode_step(ks[layer], vs[layer], tds[layer], tfs[layer], *states[layer])
+            states[layer] = st
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    per_layer = elapsed / args.steps / layers
+    alg = 36 * B * C
+    return {
+        "metric": "WKV decode state update tokens/sec, B=256 C=768 x18 layers fp32 state",
+        "value": B * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "wkv4_decode_step", "B": B, "C": C, "layers": layers},
+        "us_per_layer_step": per_layer * 1e6,
+        "hbm_gbps_algorithmic": alg / per_layer / 1e9,
+    }
+
+
+def bench_wkv7(args) -> dict:
+    import spikegpt_myelin_amd  # noqa: F401
+    from spikegpt_myelin_amd import _lib
+    from oracle import wkv7 as O7
+
+    B, T, H, N = 16, 1024, 12, 64
+    dev = torch.device("cuda", 0)
+    xs = [x.to(dev) for x in O7.make_inputs(B, T, H, N, seed=4, dtype=torch.bfloat16)]
+    for _ in range(args.warmup):
+        torch.ops.myelin.wkv7_forward(*xs, None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        torch.ops.myelin.wkv7_forward(*xs, None)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    flops = 9 * N * N * B * T * H
+    alg = 14 * N * B * T * H
+    return {
+        "metric": "RWKV-7 DPLR forward tokens/sec, B=16 T=1024 H=12 N=64 bf16 I/O fp32 state",
+        "value": B * T / step_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "wkv7_forward", "B": B, "T": T, "H": H, "N": N, "io_dtype": "bfloat16"},
+        "roofline": {"bound": "valu", "achieved": flops / step_s / 1e12, "peak": FP32_VALU_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / step_s / 1e12 / FP32_VALU_PEAK_TFLOPS,
+                     "traffic": None, "kernel": "wkv7_fwd_kernel"},
+        "hbm_gbps_algorithmic": alg / step_s / 1e9,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7"])
+    ap.add_argument("--cpu-sample-batch", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-file", default="wkv4_bwd_b64_t1024_c512_pmc.md")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build's hot path (the WKV recurrence) runs on a "
+              "single MI355X; multi-GPU runs are not part of it (see DESIGN.md for how it would "
+              "shard).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        return 2
+    sys.path.insert(0, str(ROOT))
+    if args.workload == "decode":
+        out = bench_decode(args)
+    elif args.workload == "wkv7":
+        out = bench_wkv7(args)
+    else:
+        out = bench_wkv4(args, WORKLOADS[args.workload])
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -45,6 +45,11 @@ SIGNATURES = {
     "wkv_version": (ctypes.c_char_p, []),
 }
 
+# Optional timing hook: when set to a list, every C ABI launch made through
+# ``timed`` appends (name, start_event, end_event) recorded on the launch
+# stream immediately around the call.  None (the default) costs nothing.
+EVENT_LOG: list | None = None
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -95,6 +100,21 @@ def aligned(t: torch.Tensor) -> torch.Tensor:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def timed(name: str, device: torch.device, call):
+    """Run ``call()`` (a C ABI launch); bracket it with HIP events on the
+    current stream when ``EVENT_LOG`` is a list."""
+    if EVENT_LOG is None:
+        return call()
+    stream = torch.cuda.current_stream(device)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    rc = call()
+    end.record(stream)
+    EVENT_LOG.append((name, start, end))
+    return rc
 
 
 def stream_of(t: torch.Tensor) -> int:

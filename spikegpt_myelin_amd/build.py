@@ -21,13 +21,16 @@ BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libwkv_hip.so"
 ARCH = "gfx950"
 
-# -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops
-# (v_pk_{add,mul,fma}_f32); plain fp32 arithmetic is used everywhere.
+# -packed-fp32-ops: keep the compiler from emitting packed (two-wide) fp32
+# VALU instructions; plain fp32 arithmetic is used everywhere.
+# -ffp-contract=off: every fused multiply-add is an explicit fmaf() in the
+# source, so each element type's instantiation rounds identically.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
+    "-ffp-contract=off",
     "-Wall",
     "-Wno-unused-result",
     "-Xclang",

@@ -44,6 +44,11 @@ __device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
 }
 
 __device__ __forceinline__ uint16_t float_to_f16_bits(float x) {
+  // The empty asm keeps x materialised as an fp32 value: without it the
+  // compiler may fuse the multiply that produced x into the conversion
+  // (one rounding straight to fp16), which would differ from rounding the
+  // fp32 result -- what an fp32 computation followed by a cast produces.
+  asm volatile("" : "+v"(x));
   _Float16 h = static_cast<_Float16>(x);  // RNE
   return __builtin_bit_cast(uint16_t, h);
 }

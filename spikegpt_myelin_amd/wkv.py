@@ -50,10 +50,10 @@ def _launch_forward(key: Tensor, value: Tensor, time_decay: Tensor, time_first: 
     tf = _lib.aligned(time_first.float())
     y = torch.empty_like(k)
     lib = _lib.load()
-    rc = lib.wkv4_forward(
+    rc = _lib.timed("wkv4_forward", k.device, lambda: lib.wkv4_forward(
         k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), y.data_ptr(),
         b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k),
-    )
+    ))
     _lib.check(rc, "wkv4_forward")
     return y
 
@@ -77,11 +77,11 @@ def _launch_backward(grad_y: Tensor, w: Tensor, u: Tensor, k: Tensor, v: Tensor)
     lib = _lib.load()
     nbytes = lib.wkv4_backward_workspace_bytes(b, t, c, code)
     ws = torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=k.device)
-    rc = lib.wkv4_backward(
+    rc = _lib.timed("wkv4_backward", k.device, lambda: lib.wkv4_backward(
         gy_.data_ptr(), w_.data_ptr(), u_.data_ptr(), k_.data_ptr(), v_.data_ptr(),
         gk.data_ptr(), gv.data_ptr(), gtd.data_ptr(), gtf.data_ptr(),
         ws.data_ptr(), ws.numel(), b, t, c, code, _lib.stream_of(k_),
-    )
+    ))
     _lib.check(rc, "wkv4_backward")
     if gk.dtype != out_dtype:
         gk, gv = gk.to(out_dtype), gv.to(out_dtype)

@@ -33,15 +33,18 @@ def _lib_ops():
 
 
 def _close(got, ref, *, rtol, atol_scale, norm_tol=None, what=""):
+    """allclose with ``atol = atol_scale * max(max|ref|, 1)``: the inputs are
+    O(1), so a reference that is exactly zero (gk at T=1) is compared on the
+    problem's natural unit scale rather than on zero."""
     got = got.double().cpu()
     ref = ref.double().cpu()
     scale = float(ref.abs().max()) if ref.numel() else 0.0
-    atol = atol_scale * max(scale, 1e-30)
+    atol = atol_scale * max(scale, 1.0)
     ok = torch.allclose(got, ref, rtol=rtol, atol=atol)
     err = (got - ref).abs().max().item() if ref.numel() else 0.0
     assert ok, f"{what}: max abs err {err:.3e} (atol {atol:.3e}, rtol {rtol})"
-    if norm_tol is not None and ref.numel():
-        rel = ((got - ref).norm() / ref.norm().clamp_min(1e-300)).item()
+    if norm_tol is not None and ref.numel() and float(ref.norm()) > 0.0:
+        rel = ((got - ref).norm() / ref.norm()).item()
         assert rel < norm_tol, f"{what}: normwise rel err {rel:.3e} >= {norm_tol}"
 
 
@@ -143,9 +146,11 @@ def test_16bit_io_op_matches_oracle(dtype, b, t, c, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_16bit_io_equals_fp32_op_rounded(dtype):
+def test_16bit_io_equals_fp32_op_rounded(dtype, monkeypatch):
     # wkv_bf16.py:11-14: same arithmetic on exactly widened inputs, one
-    # rounding at the store.  Small B keeps both ops on one tile config.
+    # rounding at the store -- given one tile configuration for both.
+    monkeypatch.setenv("WKV_FWD_CFG", "1,8,16")
+    monkeypatch.setenv("WKV_BWD_CFG", "1,8,16")
     ops = _lib_ops()
     k, v, td, tf, gy = O.make_inputs(2, 200, 128, seed=8, dtype=dtype)
     kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
@@ -226,9 +231,11 @@ def test_out_of_range_inputs_take_the_exact_path(kind):
     y = ops.wkv_forward(kd, vd, tdd, tfd)
     gk, gv, gtd, gtf = ops.wkv_backward(gyd, -torch.exp(tdd), tfd, kd, vd)
     ref = _oracle64_fast(k, v, td, tf, gy)
+    # fp32 rounds k*log2(e) with relative error 2^-24, i.e. an absolute error
+    # of ~|k| 2^-24 in the exponent (5e-6 at |k| = 80): tolerance 1e-4.
     for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
         assert torch.isfinite(g).all(), f"{kind} {name} not finite"
-        _close(g, r, rtol=1e-4, atol_scale=1e-5, what=f"{kind} {name}")
+        _close(g, r, rtol=1e-4, atol_scale=1e-4, what=f"{kind} {name}")
 
 
 def test_empty_sequence_and_batch():
