@@ -2,17 +2,20 @@
 
 Default workload (one JSON line on stdout): RWKV-4 / SpikeGPT WKV forward +
 backward, bf16 I/O with fp32 state, B=64, T=1024, C=512 -- the 41M SpikeGPT
-training shape.  A "step" is one pass of the op path over one batch that is
-already resident in HBM: ``y = myelin::wkv_forward_bf16io(k, v, td, tf)``
-then ``torch.autograd.grad(y, (k, v, td, tf), dy)`` (the registered autograd,
-which calls ``myelin::wkv_backward_bf16io``).
+training shape.  A "step" is one forward + backward pass of the recurrence over one batch
+that is already resident in HBM.
+
+The timed region issues that step through the C ABI on buffers allocated
+once (``wkv4_forward_checkpointed`` then ``wkv4_backward_checkpointed``, the
+two launches the autograd path makes), so the number is the kernels' own
+throughput; the same work through the torch.library op path (dispatch,
+allocation and autograd on every call) is reported as ``op_ms_per_step``.
 
 Reported beside the throughput:
-* ``roofline`` -- the dominant launch (the backward, whose C-ABI call issues
-  the main kernel plus the small batch-sum kernel), timed live with HIP events
-  recorded on the launch stream around every call inside the timed region;
-  algorithmic bytes = 10 B per [B,T,C] element (k, v, dy read, dk, dv
-  written); peak 8 TB/s.  ``traffic`` comes from the committed rocprofv3 PMC
+* ``roofline`` -- the dominant launch (the backward: the reverse-sweep kernel
+  plus the small batch-sum kernel), timed with HIP events recorded on the
+  launch stream around every call in the timed region; algorithmic bytes =
+  10 B per [B,T,C] element (k, v, dy read, dk, dv written); peak 8 TB/s.  ``traffic`` comes from the committed rocprofv3 PMC
   summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters
   on a copy of known size) when present, else null.
 * ``cpu_baseline`` -- the reference's CPU WKV path restated in eager PyTorch
@@ -116,49 +119,96 @@ def read_traffic(path: Path, kernel: str) -> int | None:
 def bench_wkv4(args, cfg) -> dict:
     import spikegpt_myelin_amd  # noqa: F401  -- registers the ops
     from spikegpt_myelin_amd import _lib
+    from spikegpt_myelin_amd.wkv import checkpoint_shape
     from oracle import wkv4 as O
 
     B, T, C, dtype, layers = cfg["B"], cfg["T"], cfg["C"], cfg["dtype"], cfg["layers"]
     dev = torch.device("cuda", 0)
     k, v, td, tf, dy = (x.to(dev) for x in O.make_inputs(B, T, C, seed=1, dtype=dtype))
-    leaves = [x.requires_grad_(True) for x in (k, v, td, tf)]
-    fwd = torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32 else torch.ops.myelin.wkv_forward
     fwd_only = args.workload == "c0"
+    lib = _lib.load()
+    code = _lib.dtype_code(dtype)
+    # Outputs and scratch allocated once: the timed region is the kernels.
+    y = torch.empty_like(k)
+    ck = torch.empty(checkpoint_shape(B, T, C), dtype=torch.float32, device=dev)
+    gk, gv = torch.empty_like(k), torch.empty_like(k)
+    gtd = torch.empty(C, dtype=torch.float32, device=dev)
+    gtf = torch.empty(C, dtype=torch.float32, device=dev)
+    ws = torch.empty(2 * B * C, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
 
-    def step():
+    def fwd():
+        _lib.check(lib.wkv4_forward_checkpointed(k.data_ptr(), v.data_ptr(), td.data_ptr(),
+                                                 tf.data_ptr(), y.data_ptr(), ck.data_ptr(),
+                                                 B, T, C, code, sp), "forward")
+
+    def bwd():
+        _lib.check(lib.wkv4_backward_checkpointed(dy.data_ptr(), td.data_ptr(), tf.data_ptr(),
+                                                  k.data_ptr(), v.data_ptr(), ck.data_ptr(),
+                                                  gk.data_ptr(), gv.data_ptr(), gtd.data_ptr(),
+                                                  gtf.data_ptr(), ws.data_ptr(), ws.numel() * 4,
+                                                  B, T, C, code, sp), "backward")
+
+    def step(events=None):
         for _ in range(layers):
-            if fwd_only:
-                with torch.no_grad():
-                    fwd(*leaves)
-            else:
-                y = fwd(*leaves)
-                torch.autograd.grad(y, leaves, dy)
+            for name, fn in (("fwd", fwd),) if fwd_only else (("fwd", fwd), ("bwd", bwd)):
+                if events is None:
+                    fn()
+                    continue
+                s_ev = torch.cuda.Event(enable_timing=True)
+                e_ev = torch.cuda.Event(enable_timing=True)
+                s_ev.record(stream)
+                fn()
+                e_ev.record(stream)
+                events.append((name, s_ev, e_ev))
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    _lib.EVENT_LOG = []
+    events: list = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        step(events)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    log, _lib.EVENT_LOG = _lib.EVENT_LOG, None
+    step_s = elapsed / args.steps
+    per = {}
+    for name, s_ev, e_ev in events:
+        per.setdefault(name, []).append(s_ev.elapsed_time(e_ev) * 1e-3)
+    fwd_s = statistics.mean(per["fwd"])
+    bwd_s = statistics.mean(per["bwd"]) if "bwd" in per else float("nan")
+
+    # The same work through the drop-in op path (torch.library dispatch,
+    # allocation and autograd on every call), for reference.
+    leaves = [x.detach().requires_grad_(True) for x in (k, v, td, tf)]
+    fwd_op = torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32 else torch.ops.myelin.wkv_forward
+
+    def op_step():
+        for _ in range(layers):
+            if fwd_only:
+                with torch.no_grad():
+                    fwd_op(*leaves)
+            else:
+                torch.autograd.grad(fwd_op(*leaves), leaves, dy)
+
+    for _ in range(args.warmup):
+        op_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        op_step()
+    torch.cuda.synchronize()
+    op_step_s = (time.perf_counter() - t0) / args.steps
 
     esize = torch.finfo(dtype).bits // 8
     n_elem = B * T * C * layers
-    per_launch = {}
-    for name, s, e in log:
-        per_launch.setdefault(name, []).append(s.elapsed_time(e) * 1e-3)
-    fwd_s = statistics.mean(per_launch.get("wkv4_forward", [float("nan")]))
     tokens = B * T * args.steps
-    value = tokens / elapsed
-    step_s = elapsed / args.steps
-    alg_step = (3 * esize if fwd_only else 8 * esize) * n_elem  # fwd 3, bwd 5 tensors
+    alg_step = (3 * esize if fwd_only else 8 * esize) * n_elem  # fwd k,v,y; bwd k,v,dy,dk,dv
     out = {
         "metric": METRIC if args.workload == "wkv4" else f"WKV {'fwd' if fwd_only else 'fwd+bwd'} tokens/sec "
                                                         f"B={B} T={T} C={C} x{layers} layers",
-        "value": value,
+        "value": tokens / elapsed,
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -171,15 +221,17 @@ def bench_wkv4(args, cfg) -> dict:
         "data": "synthetic",
         "config": {"workload": f"wkv4_{'fwd' if fwd_only else 'fwd_bwd'}", "B": B, "T": T, "C": C,
                    "layers": layers, "io_dtype": str(dtype).replace("torch.", ""),
-                   "state_dtype": "float32", "parallelism": "single_gpu"},
+                   "state_dtype": "float32", "parallelism": "single_gpu",
+                   "timing": "C-ABI launches on preallocated buffers (op path in op_ms_per_step)"},
         "hbm_gbps_algorithmic": alg_step / step_s / 1e9,
         "hbm_frac_of_peak": alg_step / step_s / 1e9 / HBM_PEAK_GBS,
+        "op_ms_per_step": op_step_s * 1e3,
+        "op_tokens_per_s": B * T / op_step_s,
         "fwd_launch_us": fwd_s * 1e6,
     }
     if fwd_only:
         dom, dom_bytes, dom_t = "wkv4_fwd_kernel", 3 * esize * B * T * C, fwd_s
     else:
-        bwd_s = statistics.mean(per_launch["wkv4_backward"])
         out["bwd_launch_us"] = bwd_s * 1e6
         dom, dom_bytes, dom_t = "wkv4_bwd_kernel", 5 * esize * B * T * C, bwd_s
     achieved = dom_bytes / dom_t / 1e9
@@ -187,7 +239,9 @@ def bench_wkv4(args, cfg) -> dict:
     out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
                        "algorithmic_bytes_per_launch": dom_bytes,
-                       "avg_launch_us": dom_t * 1e6}
+                       "avg_launch_us": dom_t * 1e6,
+                       "launch": ("wkv4_backward_checkpointed: the reverse-sweep kernel plus the "
+                                  "batch-sum kernel" if not fwd_only else "wkv4_forward_checkpointed")}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, C, args.cpu_sample_batch, fwd_only=fwd_only)
     return out

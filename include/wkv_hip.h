@@ -49,10 +49,24 @@ enum wkv_status {
 int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
                  void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream);
 
-/* Bytes of device workspace wkv4_backward needs for these sizes (chunk
- * checkpoints of the forward state plus per-batch parameter-gradient
- * partials).  Replaces the reference's three [B,T,C] fp32 replay buffers
- * (src/spikegpt/wkv_triton.py:170-172, wkv_bf16.py:167-169). */
+/* Bytes of the forward-state checkpoint records for these sizes: 5 fp32
+ * per (batch, block of 64 steps, channel) -- the state (A, B) = 2^o (p, q)
+ * at the block start and the block's largest and smallest k*log2(e), laid
+ * out [5][B][ceil(T/64)][C].  They replace the reference's three [B,T,C] fp32
+ * replay buffers (src/spikegpt/wkv_triton.py:170-172, wkv_bf16.py:167-169). */
+size_t wkv4_checkpoint_bytes(int64_t B, int64_t T, int64_t C);
+
+/* wkv4_forward that also writes the checkpoint records (y may be NULL to
+ * write the records only).  Used by the training path so that the backward
+ * reads the sequence once; no counterpart in the reference, whose autograd
+ * re-runs the forward inside the backward kernel (wkv_triton.py:85-115). */
+int wkv4_forward_checkpointed(const void* k, const void* v, const float* time_decay,
+                              const float* time_first, void* y, float* checkpoint, int64_t B,
+                              int64_t T, int64_t C, int dtype, void* stream);
+
+/* Bytes of device workspace wkv4_backward needs for these sizes (the
+ * checkpoint records it computes itself plus per-batch parameter-gradient
+ * partials). */
 size_t wkv4_backward_workspace_bytes(int64_t B, int64_t T, int64_t C, int dtype);
 
 /* RWKV-4 / SpikeGPT WKV backward.
@@ -69,6 +83,22 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
                   void* grad_k, void* grad_v, float* grad_time_decay, float* grad_time_first,
                   void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
                   int dtype, void* stream);
+
+/* Bytes of device workspace wkv4_backward_checkpointed needs (per-batch
+ * parameter-gradient partials, 2*B*C fp32). */
+size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t C);
+
+/* wkv4_backward from the records of wkv4_forward_checkpointed on the same
+ * k, v, time_decay, time_first.  Takes the raw time_decay (w = -exp(.) is
+ * applied in the kernel) and time_first; outputs as wkv4_backward.  This is
+ * the reference autograd backward (wkv_triton.py:204-216, wkv_bf16.py:201-213)
+ * without the forward replay pass. */
+int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
+                               const float* time_first, const void* k, const void* v,
+                               const float* checkpoint, void* grad_k, void* grad_v,
+                               float* grad_time_decay, float* grad_time_first, void* workspace,
+                               size_t workspace_bytes, int64_t B, int64_t T, int64_t C, int dtype,
+                               void* stream);
 
 /* Single-token WKV decode step for generation.
  *

@@ -39,6 +39,13 @@ SIGNATURES = {
         _INT,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P],
     ),
+    "wkv4_checkpoint_bytes": (_SZ, [_I64, _I64, _I64]),
+    "wkv4_forward_checkpointed": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
+    "wkv4_backward_checkpointed_workspace_bytes": (_SZ, [_I64, _I64]),
+    "wkv4_backward_checkpointed": (
+        _INT,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P],
+    ),
     "wkv4_decode_step": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
     "wkv7_forward": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]),
     "wkv_last_error_string": (ctypes.c_char_p, []),

@@ -53,11 +53,16 @@ bool env_cfg(const char* name, int& vec, int& L, int& W) {
   return sscanf(s, "%d,%d,%d", &vec, &L, &W) == 3;
 }
 
-int wkv4_forward_impl(const void*, const void*, const float*, const float*, void*, int, int, int,
-                      int, hipStream_t);
+int wkv4_forward_impl(const void*, const void*, const float*, int, const float*, void*, float*,
+                      int, int, int, int, hipStream_t);
 int wkv4_backward_impl(const void*, const float*, const float*, const void*, const void*, void*,
                        void*, float*, float*, float*, int, int, int, int, hipStream_t);
+int wkv4_backward_ck_impl(const void*, const float*, int, const float*, const void*, const void*,
+                          const float*, void*, void*, float*, float*, float*, int, int, int, int,
+                          hipStream_t);
 size_t wkv4_bwd_workspace_bytes_impl(int64_t, int64_t, int64_t, int);
+size_t wkv4_checkpoint_floats(int64_t, int64_t, int64_t);
+size_t wkv4_partials_floats(int64_t, int64_t);
 int wkv4_zero_param_grads(float*, float*, int, hipStream_t);
 int wkv4_decode_impl(const void*, const void*, const float*, const float*, const float*,
                      const float*, const float*, void*, float*, float*, float*, int, int, int,
@@ -96,8 +101,31 @@ int wkv4_forward(const void* k, const void* v, const float* time_decay, const fl
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: null pointer");
   if (!aligned16({k, v, y}))
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: k, v, y must be 16-byte aligned");
-  return wkv4_forward_impl(k, v, time_decay, time_first, y, int(B), int(T), int(C), dtype,
-                           static_cast<hipStream_t>(stream));
+  return wkv4_forward_impl(k, v, time_decay, 0, time_first, y, nullptr, int(B), int(T), int(C),
+                           dtype, static_cast<hipStream_t>(stream));
+}
+
+size_t wkv4_checkpoint_bytes(int64_t B, int64_t T, int64_t C) {
+  if (!dims_ok(B, T, C)) return 0;
+  return wkv4_checkpoint_floats(B, T, C) * sizeof(float);
+}
+
+int wkv4_forward_checkpointed(const void* k, const void* v, const float* time_decay,
+                              const float* time_first, void* y, float* checkpoint, int64_t B,
+                              int64_t T, int64_t C, int dtype, void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: unknown dtype");
+  if (!dims_ok(B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: bad sizes");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!k || !v || !time_decay || !time_first || !checkpoint)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: null pointer");
+  if (!aligned16({k, v, y, checkpoint}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv4_forward_checkpointed: tensors must be 16-byte aligned");
+  return wkv4_forward_impl(k, v, time_decay, 0, time_first, y, checkpoint, int(B), int(T), int(C),
+                           dtype, static_cast<hipStream_t>(stream));
 }
 
 size_t wkv4_backward_workspace_bytes(int64_t B, int64_t T, int64_t C, int dtype) {
@@ -128,6 +156,40 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
                 "wkv4_backward: grad_y, k, v, grad_k, grad_v, workspace must be 16-byte aligned");
   return wkv4_backward_impl(grad_y, w, u, k, v, grad_k, grad_v, grad_time_decay, grad_time_first,
                             static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
+}
+
+size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t C) {
+  if (!dims_ok(B, 1, C)) return 0;
+  return wkv4_partials_floats(B, C) * sizeof(float) + 256;
+}
+
+int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
+                               const float* time_first, const void* k, const void* v,
+                               const float* checkpoint, void* grad_k, void* grad_v,
+                               float* grad_time_decay, float* grad_time_first, void* workspace,
+                               size_t workspace_bytes, int64_t B, int64_t T, int64_t C, int dtype,
+                               void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_checkpointed: unknown dtype");
+  if (!dims_ok(B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_checkpointed: bad sizes");
+  if (C == 0) return WKV_OK;
+  if (!grad_time_decay || !grad_time_first)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_checkpointed: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0 || T == 0) return wkv4_zero_param_grads(grad_time_decay, grad_time_first, int(C), s);
+  if (!grad_y || !time_decay || !time_first || !k || !v || !checkpoint || !grad_k || !grad_v ||
+      !workspace)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_checkpointed: null pointer");
+  if (workspace_bytes < wkv4_partials_floats(B, C) * sizeof(float))
+    return fail(WKV_ERR_WORKSPACE_TOO_SMALL, "wkv4_backward_checkpointed: workspace too small");
+  if (!aligned16({grad_y, k, v, checkpoint, grad_k, grad_v, workspace}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv4_backward_checkpointed: tensors must be 16-byte aligned");
+  return wkv4_backward_ck_impl(grad_y, time_decay, 0, time_first, k, v, checkpoint, grad_k,
+                               grad_v, grad_time_decay, grad_time_first,
+                               static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
 }
 
 int wkv4_decode_step(const void* k, const void* v, const float* time_decay, const float* time_first,

@@ -18,7 +18,7 @@
 //   * all chunks of a segment share one base-2 reference frame R (the
 //     segment max of k*log2e, exchanged through LDS), so a chunk's state is
 //     (A, B) = 2^R (p, q) and joining chunks is linear: p <- p*e^{Lw} + p_j.
-//     The per-step work is then one exp2 (e^{k-R}) and one reciprocal per
+//     The per-step work is one exp2 (2^{k log2e - R}) and one reciprocal per
 //     element, with no per-step max or select;
 //   * phase 1: every wave reduces its chunk to (p_j, q_j) from a zero state;
 //     after one barrier each wave folds the segment carry and its
@@ -26,70 +26,53 @@
 //     phase 2: every wave re-runs its chunk from registers with that carry and
 //     writes y.  k and v are read from HBM exactly once and y written once.
 //
+// Checkpoints: with a checkpoint buffer the kernel also stores, at the start
+// of every block of 64 steps, the state in running-max form and the block's
+// key range: (o, p, q, max, min) with (A, B) = 2^o (p, q) and max/min the
+// extreme k*log2e of the block ([5][B][ceil(T/64)][C] fp32).  The backward
+// kernel recomputes the forward from these records instead of re-reading the
+// whole sequence; without y (y == nullptr) the kernel writes records only.
+//
 // Range guard: the shared frame is exact arithmetic re-association, valid
 // while every quantity stays inside fp32's normal range.  Each segment checks
-// (i) the spread between the frame and the smallest k*log2e it holds,
-// (ii) the jump between consecutive frames, and (iii) |u*log2e|; if any lane
-// of the workgroup is outside the bounds, the whole row is recomputed by the
-// reference's running-max recurrence, one channel per thread.  Inputs whose
-// keys stay inside +-30 (the benchmark's clamp) never take that path.
+// the spread between the frame and the smallest k*log2e it holds, the jump
+// between consecutive frames, and |u*log2e|.  Every wave derives the decision
+// from the same LDS data, so it is workgroup-uniform without another
+// barrier; a rejected row is recomputed by the reference's running-max
+// recurrence, one channel per thread.  Inputs whose keys stay inside +-30 (the
+// benchmark's clamp) never take that path.
 #include "wkv_common.h"
 
 namespace wkv {
 
-// Bounds of the shared-frame path (base-2 exponents).
-constexpr float kFwdMaxSpread = 96.f;  // frame minus smallest k*log2e in the segment
-constexpr float kFwdMaxJump = 96.f;    // previous frame minus this frame
-constexpr float kFwdMaxU = 24.f;       // |time_first * log2(e)|
-
-// Reference running-max recurrence for one channel over the whole sequence
-// (wkv_triton.py:41-58 in base-2 units).  Used for rows the range guard
-// rejects.
-template <typename E>
-__device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
-                                        const typename E::raw* __restrict__ v,
-                                        typename E::raw* __restrict__ y, float w2, float u2,
-                                        int T, int C, size_t base) {
-  float o = kNegHuge, p = 0.f, q = 0.f;
-  for (int t = 0; t < T; ++t) {
-    const size_t idx = base + size_t(t) * C;
-    const float kk = load_scalar<E>(k + idx) * kLog2e;
-    const float vv = load_scalar<E>(v + idx);
-    const float uk = u2 + kk;
-    float no = fmaxf(o, uk);
-    float a = fast_exp2(o - no);
-    float bb = fast_exp2(uk - no);
-    store_scalar<E>(y + idx, (a * p + bb * vv) / (a * q + bb));
-    const float wo = w2 + o;
-    no = fmaxf(wo, kk);
-    a = fast_exp2(wo - no);
-    bb = fast_exp2(kk - no);
-    p = a * p + bb * vv;
-    q = a * q + bb;
-    o = no;
-  }
-}
-
-template <typename E, int VEC, int L, int W>
+template <typename E, int VEC, int L, int W, bool WY>
 struct Fwd {
   using raw = typename E::raw;
   using PackT = Pack<E, VEC>;
-  static constexpr int CPW = 64 * VEC;  // channels per row
-  static constexpr int SEG = W * L;     // steps per segment
+  static constexpr int CPW = 64 * VEC;       // channels per row
+  static constexpr int SEG = W * L;          // steps per segment
+  static constexpr int CPB = kCkptBlock / L;  // chunks per checkpoint block
+  static_assert(kCkptBlock % L == 0 && SEG % kCkptBlock == 0, "segment/block layout");
 
+  // [VEC][W][64]: lane index fastest, so every LDS access of a wave is one
+  // conflict-free row of 64 dwords.
+  // mx/mn are double-buffered by segment parity so that the waves writing
+  // checkpoint records can read their block's range after the second
+  // barrier without racing the next segment's writes.
   struct Smem {
-    float mx[W][CPW];
-    float p[W][CPW];
-    float q[W][CPW];
-    float carry[2][3][CPW];  // (R, p, q) of the segment carry, by segment parity
+    float mx[2][VEC][W][64];
+    float mn[2][VEC][W][64];
+    float p[VEC][W][64];
+    float q[VEC][W][64];
+    float carry[2][3][VEC][64];  // (R, p, q) of the segment carry, by segment parity
   };
 
-  // row_base is wave-uniform (kept in SGPRs); lane_off is the lane's 32-bit
-  // element offset, so each load is one SGPR-base + VGPR-offset instruction.
+  // row_base is wave-uniform (SGPRs); lane_off is the lane's 32-bit element
+  // offset.  Steps past the end re-read step T-1 (masked in the arithmetic).
   __device__ static __forceinline__ void load_chunk(const raw* __restrict__ k,
                                                     const raw* __restrict__ v, size_t row_base,
                                                     unsigned lane_off, int t0, int T, int C,
-                                                    bool active, PackT (&kb)[L], PackT (&vb)[L]) {
+                                                    PackT (&kb)[L], PackT (&vb)[L]) {
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const size_t step = row_base + size_t(min(t0 + i, T - 1)) * C;
@@ -98,54 +81,65 @@ struct Fwd {
     }
   }
 
-  // Processes one segment.  Returns true when the range guard rejected it
-  // (workgroup-uniform).
-  __device__ static __forceinline__ bool segment(Smem& sm, int seg, int T, int C, int wave,
-                                                 int lane, bool active, size_t row_base,
-                                                 unsigned lane_off,
-                                                 raw* __restrict__ y, const PackT (&kb)[L],
-                                                 const PackT (&vb)[L], const float (&D)[VEC],
-                                                 const float (&DL)[VEC], const float (&U)[VEC],
-                                                 bool u_ok) {
+  // One segment.  FULL: every step of the segment is inside the sequence.
+  // Returns true when the range guard rejects the row (workgroup-uniform).
+  template <bool FULL>
+  __device__ static __forceinline__ bool segment(
+      Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
+      unsigned lane_off, raw* __restrict__ y, float* __restrict__ ck, size_t ck_lane,
+      size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L], const float (&D)[VEC],
+      const float (&DL)[VEC], const float (&U)[VEC], bool u_ok) {
     const int t0 = seg * SEG + wave * L;
+    // Phase 0: chunk range of k.
     float s[L][VEC];
-    float m[VEC];
+    float m[VEC], n[VEC];
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) m[c] = kNegHuge;
+    for (int c = 0; c < VEC; ++c) { m[c] = -kBig; n[c] = kBig; }
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-      const bool valid = active && (t0 + i) < T;
+      const bool valid = FULL || (t0 + i) < T;
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        s[i][c] = kb[i].get(c) * kLog2e;
+        s[i][c] = kb[i].get(c);
         m[c] = valid ? fmaxf(m[c], s[i][c]) : m[c];
+        n[c] = valid ? fminf(n[c], s[i][c]) : n[c];
       }
     }
+    const int par = seg & 1;
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) sm.mx[wave][lane * VEC + c] = m[c];
+    for (int c = 0; c < VEC; ++c) {
+      sm.mx[par][c][wave][lane] = m[c];
+      sm.mn[par][c][wave][lane] = n[c];
+    }
     __syncthreads();
 
-    // Segment frame and the carry from the previous segment.
+    // Segment frame, the carry from the previous segment and the guard.
     float R[VEC], pin[VEC], qin[VEC];
     bool bad = !u_ok;
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      float r = kNegHuge;
+      float r = -kBig, lo = kBig;
 #pragma unroll
-      for (int w = 0; w < W; ++w) r = fmaxf(r, sm.mx[w][lane * VEC + c]);
-      R[c] = (r == kNegHuge) ? 0.f : r;
+      for (int w = 0; w < W; ++w) {
+        r = fmaxf(r, sm.mx[par][c][w][lane]);
+        lo = fminf(lo, sm.mn[par][c][w][lane]);
+      }
+      const bool any = r > -kBig;
+      R[c] = any ? r * kLog2e : 0.f;
+      bad |= any && (R[c] - lo * kLog2e > kMaxSpread);
       if (seg > 0) {
-        const float Rc = sm.carry[(seg - 1) & 1][0][lane * VEC + c];
-        const float d = Rc - R[c];
-        bad |= active && (d > kFwdMaxJump);
+        const float d = sm.carry[(seg - 1) & 1][0][c][lane] - R[c];
+        bad |= active && d > kMaxJump;
         const float f = fast_exp2(d);
-        pin[c] = sm.carry[(seg - 1) & 1][1][lane * VEC + c] * f;
-        qin[c] = sm.carry[(seg - 1) & 1][2][lane * VEC + c] * f;
+        pin[c] = sm.carry[(seg - 1) & 1][1][c][lane] * f;
+        qin[c] = sm.carry[(seg - 1) & 1][2][c][lane] * f;
       } else {
         pin[c] = 0.f;
         qin[c] = 0.f;
       }
     }
+    // Identical LDS inputs in every wave: the wave vote is the workgroup's.
+    if (__any(active && bad)) return true;
 
     // Phase 1: chunk summary from a zero state, in frame R.
     float ps[VEC], qs[VEC];
@@ -153,12 +147,11 @@ struct Fwd {
     for (int c = 0; c < VEC; ++c) { ps[c] = 0.f; qs[c] = 0.f; }
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-      const bool valid = active && (t0 + i) < T;
+      const bool valid = FULL || (t0 + i) < T;
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        const float x = s[i][c] - R[c];
-        bad |= valid && (x < -kFwdMaxSpread);
-        const float e = valid ? fast_exp2(x) : 0.f;
+        float e = fast_exp2(fmaf(s[i][c], kLog2e, -R[c]));
+        if (!FULL) e = valid ? e : 0.f;
         s[i][c] = e;
         ps[c] = fmaf(ps[c], D[c], e * vb[i].get(c));
         qs[c] = fmaf(qs[c], D[c], e);
@@ -166,58 +159,125 @@ struct Fwd {
     }
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      sm.p[wave][lane * VEC + c] = ps[c];
-      sm.q[wave][lane * VEC + c] = qs[c];
+      sm.p[c][wave][lane] = ps[c];
+      sm.q[c][wave][lane] = qs[c];
     }
-    if (__syncthreads_or(bad)) return true;
+    __syncthreads();
 
     // Carry-in of this chunk: segment carry, then the earlier chunks.
     for (int w = 0; w < wave; ++w) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        pin[c] = fmaf(pin[c], DL[c], sm.p[w][lane * VEC + c]);
-        qin[c] = fmaf(qin[c], DL[c], sm.q[w][lane * VEC + c]);
+        pin[c] = fmaf(pin[c], DL[c], sm.p[c][w][lane]);
+        qin[c] = fmaf(qin[c], DL[c], sm.q[c][w][lane]);
       }
     }
-
-    // Phase 2: outputs.
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int t = t0 + i;
-      float yv[VEC];
+    if (ck != nullptr && wave % CPB == 0 && active && t0 < T) {
+      // Key range of this wave's checkpoint block (chunks wave..wave+CPB-1).
+      float bmax[VEC], bmin[VEC];
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        const float e = s[i][c];
-        const float vv = vb[i].get(c);
-        const float e1 = e * U[c];
-        const float num = fmaf(e1, vv, pin[c]);
-        const float den = qin[c] + e1;
-        yv[c] = num * fast_rcp(den);
-        // fma(e, v, p*D), not fma(p, D, e*v): keeps phase 1's e*v products
-        // from being carried live into this phase.
-        pin[c] = fmaf(e, vv, pin[c] * D[c]);
-        qin[c] = fmaf(qin[c], D[c], e);
+        float br = -kBig, bl = kBig;
+#pragma unroll
+        for (int j = 0; j < CPB; ++j) {
+          br = fmaxf(br, sm.mx[par][c][wave + j][lane]);
+          bl = fminf(bl, sm.mn[par][c][wave + j][lane]);
+        }
+        bmax[c] = br * kLog2e;
+        bmin[c] = bl * kLog2e;
       }
-      if (active && t < T) store_vec<E, VEC>((y + (row_base + size_t(t) * C)) + lane_off, yv);
+      float* rec = ck + ck_lane + size_t(t0 / kCkptBlock) * C;
+      store_vec<F32, VEC>(rec + 0 * ck_field, R);
+      store_vec<F32, VEC>(rec + 1 * ck_field, pin);
+      store_vec<F32, VEC>(rec + 2 * ck_field, qin);
+      store_vec<F32, VEC>(rec + 3 * ck_field, bmax);
+      store_vec<F32, VEC>(rec + 4 * ck_field, bmin);
     }
     if (wave == W - 1) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        sm.carry[seg & 1][0][lane * VEC + c] = R[c];
-        sm.carry[seg & 1][1][lane * VEC + c] = pin[c];
-        sm.carry[seg & 1][2][lane * VEC + c] = qin[c];
+        sm.carry[seg & 1][0][c][lane] = R[c];
+        sm.carry[seg & 1][1][c][lane] = fmaf(pin[c], DL[c], ps[c]);
+        sm.carry[seg & 1][2][c][lane] = fmaf(qin[c], DL[c], qs[c]);
+      }
+    }
+
+    // Phase 2: outputs.
+    if constexpr (WY) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        const int t = t0 + i;
+        float yv[VEC];
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+          const float e = s[i][c];
+          const float vv = vb[i].get(c);
+          const float e1 = e * U[c];
+          yv[c] = fmaf(e1, vv, pin[c]) * fast_rcp(qin[c] + e1);
+          // fma(e, v, p*D) rather than fma(p, D, e*v): keeps phase 1's e*v
+          // products from being carried live into this phase.
+          pin[c] = fmaf(e, vv, pin[c] * D[c]);
+          qin[c] = fmaf(qin[c], D[c], e);
+        }
+        if (active && (FULL || t < T)) store_vec<E, VEC>((y + (row_base + size_t(t) * C)) + lane_off, yv);
       }
     }
     return false;
   }
 };
 
-template <typename E, int VEC, int L, int W>
+// Reference running-max recurrence for one channel over the whole sequence
+// (wkv_triton.py:41-58 in base-2 units), writing y (if any) and the
+// checkpoint records (if any).  Used for rows the range guard rejects.
+template <typename E>
+__device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
+                                        const typename E::raw* __restrict__ v,
+                                        typename E::raw* __restrict__ y, float w2, float u2, int T,
+                                        int C, size_t base, float* __restrict__ ck,
+                                        size_t ck_lane, size_t ck_field) {
+  float o = kNegHuge, p = 0.f, q = 0.f;
+  for (int t = 0; t < T; ++t) {
+    const size_t idx = base + size_t(t) * C;
+    if (ck != nullptr && t % kCkptBlock == 0) {
+      float bmax = -kBig, bmin = kBig;
+      for (int j = t; j < min(T, t + kCkptBlock); ++j) {
+        const float kj = load_scalar<E>(k + base + size_t(j) * C);
+        bmax = fmaxf(bmax, kj);
+        bmin = fminf(bmin, kj);
+      }
+      float* rec = ck + ck_lane + size_t(t / kCkptBlock) * C;
+      rec[0 * ck_field] = o;
+      rec[1 * ck_field] = p;
+      rec[2 * ck_field] = q;
+      rec[3 * ck_field] = bmax * kLog2e;
+      rec[4 * ck_field] = bmin * kLog2e;
+    }
+    const float kk = load_scalar<E>(k + idx) * kLog2e;
+    const float vv = load_scalar<E>(v + idx);
+    if (y != nullptr) {
+      const float uk = u2 + kk;
+      const float no = fmaxf(o, uk);
+      const float a = fast_exp2(o - no);
+      const float bb = fast_exp2(uk - no);
+      store_scalar<E>(y + idx, (a * p + bb * vv) / (a * q + bb));
+    }
+    const float wo = w2 + o;
+    const float no = fmaxf(wo, kk);
+    const float a = fast_exp2(wo - no);
+    const float bb = fast_exp2(kk - no);
+    p = a * p + bb * vv;
+    q = a * q + bb;
+    o = no;
+  }
+}
+
+// decay: time_decay (decay_is_w == 0, w = -exp(decay)) or w itself.
+template <typename E, int VEC, int L, int W, bool WY>
 __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
     const typename E::raw* __restrict__ k, const typename E::raw* __restrict__ v,
-    const float* __restrict__ time_decay, const float* __restrict__ time_first,
-    typename E::raw* __restrict__ y, int T, int C) {
-  using F = Fwd<E, VEC, L, W>;
+    const float* __restrict__ decay, int decay_is_w, const float* __restrict__ time_first,
+    typename E::raw* __restrict__ y, float* __restrict__ ck, int T, int C) {
+  using F = Fwd<E, VEC, L, W, WY>;
   using PackT = typename F::PackT;
   __shared__ typename F::Smem sm;
 
@@ -231,48 +291,59 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
   // Lanes past the last channel read channel 0 of the row (never stored).
   const unsigned lane_off = active ? unsigned(lane * VEC) : 0u;
+  const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
+  const size_t ck_field = size_t(gridDim.x / n_cg) * nblk * C;  // B * nblk * C
+  const size_t ck_lane = size_t(b) * nblk * C + (active ? c0 : 0);
 
   float D[VEC], DL[VEC], U[VEC];
   bool u_ok = true;
 #pragma unroll
   for (int c = 0; c < VEC; ++c) {
-    const float td = active ? time_decay[c0 + c] : 0.f;
+    const float dv = active ? decay[c0 + c] : 0.f;
     const float tf = active ? time_first[c0 + c] : 0.f;
-    const float w2 = -expf(td) * kLog2e;
+    const float w2 = (decay_is_w ? dv : -expf(dv)) * kLog2e;
     const float u2 = tf * kLog2e;
     D[c] = fast_exp2(w2);
     DL[c] = fast_exp2(w2 * float(L));
     U[c] = fast_exp2(u2);
-    u_ok &= fabsf(u2) <= kFwdMaxU;
+    u_ok &= fabsf(u2) <= kMaxU;
   }
 
   const int nseg = (T + F::SEG - 1) / F::SEG;
+  const int nfull = T / F::SEG;
   PackT kA[L], vA[L], kB[L], vB[L];
   bool bad = false;
-  F::load_chunk(k, v, row_base, lane_off, wave * L, T, C, active, kA, vA);
+  F::load_chunk(k, v, row_base, lane_off, wave * L, T, C, kA, vA);
   for (int seg = 0; seg < nseg; seg += 2) {
     if (seg + 1 < nseg)
-      F::load_chunk(k, v, row_base, lane_off, (seg + 1) * F::SEG + wave * L, T, C, active, kB, vB);
-    if (F::segment(sm, seg, T, C, wave, lane, active, row_base, lane_off, y, kA, vA, D, DL, U, u_ok)) {
-      bad = true;
-      break;
-    }
-    if (seg + 1 >= nseg) break;
+      F::load_chunk(k, v, row_base, lane_off, (seg + 1) * F::SEG + wave * L, T, C, kB, vB);
+    bad = seg < nfull
+              ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, lane_off, y,
+                                          ck, ck_lane, ck_field, kA, vA, D, DL, U, u_ok)
+              : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, lane_off,
+                                           y, ck, ck_lane, ck_field, kA, vA, D, DL, U, u_ok);
+    if (bad || seg + 1 >= nseg) break;
     if (seg + 2 < nseg)
-      F::load_chunk(k, v, row_base, lane_off, (seg + 2) * F::SEG + wave * L, T, C, active, kA, vA);
-    if (F::segment(sm, seg + 1, T, C, wave, lane, active, row_base, lane_off, y, kB, vB, D, DL, U, u_ok)) {
-      bad = true;
-      break;
-    }
+      F::load_chunk(k, v, row_base, lane_off, (seg + 2) * F::SEG + wave * L, T, C, kA, vA);
+    bad = seg + 1 < nfull
+              ? F::template segment<true>(sm, seg + 1, T, C, wave, lane, active, row_base,
+                                          lane_off, y, ck, ck_lane, ck_field, kB, vB, D, DL, U,
+                                          u_ok)
+              : F::template segment<false>(sm, seg + 1, T, C, wave, lane, active, row_base,
+                                           lane_off, y, ck, ck_lane, ck_field, kB, vB, D, DL, U,
+                                           u_ok);
+    if (bad) break;
   }
   if (bad) {
     // Workgroup-uniform: recompute the row with the running-max recurrence.
+    __syncthreads();
     for (int ch = threadIdx.x; ch < F::CPW; ch += blockDim.x) {
       const int c = cg * F::CPW + ch;
       if (c >= C) continue;
-      const float w2 = -expf(time_decay[c]) * kLog2e;
+      const float w2 = (decay_is_w ? decay[c] : -expf(decay[c])) * kLog2e;
       const float u2 = time_first[c] * kLog2e;
-      wkv4_fwd_channel_serial<E>(k, v, y, w2, u2, T, C, size_t(b) * T * C + c);
+      wkv4_fwd_channel_serial<E>(k, v, WY ? y : nullptr, w2, u2, T, C, size_t(b) * T * C + c, ck,
+                                 size_t(b) * nblk * C + c, ck_field);
     }
   }
 }
@@ -282,59 +353,70 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
 // ------------------------------------------------------------ launcher ----
 namespace wkv_host {
 
-struct FwdCfg { int vec, L, W; };
+struct TileCfg { int vec, L, W; };
 
-// Tile configurations compiled into the library (VGPR use without spills at
-// 64*W threads per workgroup).
-static constexpr FwdCfg kFwdCfgs[] = {{1, 8, 16}, {2, 8, 16}, {2, 8, 8}, {1, 16, 8}};
+// Tile configurations compiled into the library (no VGPR spills at 64*W
+// threads per workgroup).  SEG = W*L must be a multiple of the 64-step
+// checkpoint block.
+static constexpr TileCfg kFwdCfgs[] = {{2, 8, 16}, {1, 8, 16}, {2, 8, 8}, {1, 16, 8}};
 
 int pick_vec(int64_t B, int64_t C);
 bool env_cfg(const char* name, int& vec, int& L, int& W);
 
 // fp32 tensors already give 4-byte lane loads at one channel per lane; the
 // 16-bit types use two channels per lane when the batch fills the GPU.
-static FwdCfg pick_fwd_cfg(int64_t B, int64_t C, int elem_bytes) {
+static TileCfg pick_fwd_cfg(int64_t B, int64_t C, int elem_bytes) {
   int vec, L, W;
   if (env_cfg("WKV_FWD_CFG", vec, L, W)) {
-    for (const FwdCfg& c : kFwdCfgs)
+    for (const TileCfg& c : kFwdCfgs)
       if (c.vec == vec && c.L == L && c.W == W && (vec == 1 || C % 2 == 0)) return c;
   }
-  if (elem_bytes == 2 && pick_vec(B, C) == 2) return FwdCfg{2, 8, 16};
-  return FwdCfg{1, 8, 16};
+  if (elem_bytes == 2 && pick_vec(B, C) == 2) return TileCfg{2, 8, 16};
+  return TileCfg{1, 8, 16};
 }
 
 template <typename E, int VEC, int L, int W>
-static int launch_fwd(const void* k, const void* v, const float* td, const float* tf, void* y,
-                      int B, int T, int C, hipStream_t stream) {
+static int launch_fwd(const void* k, const void* v, const float* decay, int decay_is_w,
+                      const float* tf, void* y, float* ck, int B, int T, int C,
+                      hipStream_t stream) {
   using raw = typename E::raw;
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
-  hipLaunchKernelGGL((wkv::wkv4_fwd_kernel<E, VEC, L, W>), dim3(unsigned(B) * unsigned(n_cg)),
-                     dim3(W * 64), 0, stream, static_cast<const raw*>(k),
-                     static_cast<const raw*>(v), td, tf, static_cast<raw*>(y), T, C);
+  const dim3 grid(unsigned(B) * unsigned(n_cg)), block(W * 64);
+  if (y != nullptr) {
+    hipLaunchKernelGGL((wkv::wkv4_fwd_kernel<E, VEC, L, W, true>), grid, block, 0, stream,
+                       static_cast<const raw*>(k), static_cast<const raw*>(v), decay, decay_is_w,
+                       tf, static_cast<raw*>(y), ck, T, C);
+  } else {
+    hipLaunchKernelGGL((wkv::wkv4_fwd_kernel<E, VEC, L, W, false>), grid, block, 0, stream,
+                       static_cast<const raw*>(k), static_cast<const raw*>(v), decay, decay_is_w,
+                       tf, static_cast<raw*>(nullptr), ck, T, C);
+  }
   return check_launch("wkv4_fwd_kernel");
 }
 
 template <typename E>
-static int dispatch_fwd(const void* k, const void* v, const float* td, const float* tf, void* y,
-                        int B, int T, int C, hipStream_t stream) {
-  const FwdCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
-#define WKV_FWD_CASE(V, LL, WW) \
+static int dispatch_fwd(const void* k, const void* v, const float* decay, int decay_is_w,
+                        const float* tf, void* y, float* ck, int B, int T, int C,
+                        hipStream_t stream) {
+  const TileCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
+#define WKV_FWD_CASE(V, LL, WW)                    \
   if (cfg.vec == V && cfg.L == LL && cfg.W == WW) \
-    return launch_fwd<E, V, LL, WW>(k, v, td, tf, y, B, T, C, stream);
-  WKV_FWD_CASE(1, 8, 16)
+    return launch_fwd<E, V, LL, WW>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
   WKV_FWD_CASE(2, 8, 16)
+  WKV_FWD_CASE(1, 8, 16)
   WKV_FWD_CASE(2, 8, 8)
   WKV_FWD_CASE(1, 16, 8)
 #undef WKV_FWD_CASE
   return fail(1, "wkv4_forward: no kernel for the selected tile configuration");
 }
 
-int wkv4_forward_impl(const void* k, const void* v, const float* td, const float* tf, void* y,
-                      int B, int T, int C, int dtype, hipStream_t stream) {
+int wkv4_forward_impl(const void* k, const void* v, const float* decay, int decay_is_w,
+                      const float* tf, void* y, float* ck, int B, int T, int C, int dtype,
+                      hipStream_t stream) {
   switch (dtype) {
-    case 0: return dispatch_fwd<wkv::F32>(k, v, td, tf, y, B, T, C, stream);
-    case 1: return dispatch_fwd<wkv::BF16>(k, v, td, tf, y, B, T, C, stream);
-    case 2: return dispatch_fwd<wkv::F16>(k, v, td, tf, y, B, T, C, stream);
+    case 0: return dispatch_fwd<wkv::F32>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
+    case 1: return dispatch_fwd<wkv::BF16>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
+    case 2: return dispatch_fwd<wkv::F16>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
     default: return fail(1, "wkv4_forward: unknown dtype");
   }
 }

@@ -16,6 +16,22 @@ constexpr float kLog2e = 1.4426950408889634f;
 // "Minus infinity" log-scale of an empty state, the value the reference
 // kernels start from (wkv_triton.py:43), expressed in base-2 units.
 constexpr float kNegHuge = -1e38f;
+// Finite stand-in for +-infinity in running max/min reductions.
+constexpr float kBig = 3.0e38f;
+
+// Steps per checkpoint record of the forward state (see wkv4_fwd.hip).
+constexpr int kCkptBlock = 64;
+// Fields of a checkpoint record: state (A, B) = 2^o (p, q) at the block
+// start, and the block's largest and smallest k*log2(e).
+constexpr int kCkptFields = 5;
+
+// Range of the shared-frame arithmetic (base-2 exponents): spread between a
+// segment's frame and its smallest key, jump between consecutive frames, and
+// |time_first * log2(e)|.  Outside it a row is recomputed with the reference
+// running-max recurrences.
+constexpr float kMaxSpread = 80.f;
+constexpr float kMaxJump = 80.f;
+constexpr float kMaxU = 16.f;
 
 // ---------------------------------------------------------------- math ----
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

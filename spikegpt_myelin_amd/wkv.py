@@ -1,7 +1,7 @@
 """The ``myelin::`` WKV custom ops, served by hand-written gfx950 HIP kernels.
 
 Drop-in for the reference's Triton-backed ops (same op names, schemas, dtype
-rules, fake impls and autograd formulas):
+rules and results):
 
 * ``myelin::wkv_forward(Tensor key, Tensor value, Tensor time_decay,
   Tensor time_first) -> Tensor`` -- ``src/spikegpt/wkv_triton.py:147-162``.
@@ -12,9 +12,16 @@ rules, fake impls and autograd formulas):
   the ``* w`` chain rule applied and the parameter grads summed over B.
 * ``myelin::wkv_forward_bf16io`` / ``myelin::wkv_backward_bf16io`` --
   ``src/spikegpt/wkv_bf16.py:143-215``: native 16-bit I/O, fp32 state.
-* autograd: ``setup_context`` saves ``(key, value, time_decay, time_first)``
-  and the backward recomputes ``w, u`` (``wkv_triton.py:200-218``,
-  ``wkv_bf16.py:197-215``).
+
+Autograd.  The reference saves the four inputs and its backward kernel
+replays the whole forward (``wkv_triton.py:85-115``).  Here the public
+forward ops are composites of the private op ``myelin::wkv4_forward_train``,
+which returns ``y`` together with small forward-state checkpoint records
+(``[5, B, ceil(T/64), C]`` fp32, ~0.3 B per element); its registered backward
+(``myelin::wkv4_backward_train``) reads the sequence once from those records.
+Gradients are the same quantities as the reference's
+(``wkv_triton.py:200-218``).  ``myelin::wkv_backward*`` remain standalone ops
+that recompute the records themselves.
 
 Python API (``wkv_triton.py:221-228``, ``wkv_bf16.py:218-231``):
 :func:`weighted_key_value_hip` and :func:`weighted_key_value_hip_bf16io`, also
@@ -33,40 +40,61 @@ from torch import Tensor
 from . import _lib
 
 _NATIVE = (torch.float32, torch.bfloat16, torch.float16)
+CKPT_BLOCK = 64  # steps per checkpoint record
+CKPT_FIELDS = 5
 
 
-def _launch_forward(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
-    """y = WKV(key, value) with fp32 state; y has ``key.dtype`` when that is
-    float32/bfloat16/float16 (same dtype as ``value``), else float32."""
+def _compute_inputs(key: Tensor, value: Tensor) -> tuple[Tensor, Tensor]:
+    """k, v as the kernels read them: native when both share a float32 /
+    bfloat16 / float16 dtype, else exactly widened to float32 (the
+    reference's ``.float()``)."""
+    if key.dtype == value.dtype and key.dtype in _NATIVE:
+        return _lib.aligned(key), _lib.aligned(value)
+    return _lib.aligned(key.float()), _lib.aligned(value.float())
+
+
+def checkpoint_shape(b: int, t: int, c: int) -> tuple[int, int, int, int]:
+    return (CKPT_FIELDS, b, (t + CKPT_BLOCK - 1) // CKPT_BLOCK, c)
+
+
+def _launch_forward(key, value, time_decay, time_first, *, with_checkpoint: bool):
+    """y (compute dtype) and, optionally, the checkpoint records."""
     _lib.require_gpu(key, value, time_decay, time_first)
     b, t, c = key.shape
-    if key.dtype == value.dtype and key.dtype in _NATIVE:
-        k = _lib.aligned(key)
-        v = _lib.aligned(value)
-    else:  # mixed or wider dtypes: exact fp32 path (the reference's .float())
-        k = _lib.aligned(key.float())
-        v = _lib.aligned(value.float())
+    k, v = _compute_inputs(key, value)
     td = _lib.aligned(time_decay.float())
     tf = _lib.aligned(time_first.float())
     y = torch.empty_like(k)
     lib = _lib.load()
+    code = _lib.dtype_code(k.dtype)
+    if with_checkpoint:
+        ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=k.device)
+        rc = _lib.timed("wkv4_forward", k.device, lambda: lib.wkv4_forward_checkpointed(
+            k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), y.data_ptr(), ck.data_ptr(),
+            b, t, c, code, _lib.stream_of(k),
+        ))
+        _lib.check(rc, "wkv4_forward_checkpointed")
+        return y, ck
     rc = _lib.timed("wkv4_forward", k.device, lambda: lib.wkv4_forward(
         k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), y.data_ptr(),
-        b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k),
+        b, t, c, code, _lib.stream_of(k),
     ))
     _lib.check(rc, "wkv4_forward")
-    return y
+    return y, None
+
+
+def _grad_inputs(grad_y: Tensor, k: Tensor, v: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    if grad_y.dtype == k.dtype == v.dtype and k.dtype in _NATIVE:
+        return _lib.aligned(grad_y), _lib.aligned(k), _lib.aligned(v)
+    return _lib.aligned(grad_y.float()), _lib.aligned(k.float()), _lib.aligned(v.float())
 
 
 def _launch_backward(grad_y: Tensor, w: Tensor, u: Tensor, k: Tensor, v: Tensor) -> list[Tensor]:
-    """[gk, gv (k's dtype), g_time_decay, g_time_first (fp32 [C])]."""
+    """Standalone backward: [gk, gv (k's dtype), g_time_decay, g_time_first]."""
     _lib.require_gpu(grad_y, w, u, k, v)
     b, t, c = k.shape
     out_dtype = k.dtype
-    if grad_y.dtype == k.dtype == v.dtype and k.dtype in _NATIVE:
-        gy_, k_, v_ = _lib.aligned(grad_y), _lib.aligned(k), _lib.aligned(v)
-    else:
-        gy_, k_, v_ = _lib.aligned(grad_y.float()), _lib.aligned(k.float()), _lib.aligned(v.float())
+    gy_, k_, v_ = _grad_inputs(grad_y, k, v)
     w_ = _lib.aligned(w.float())
     u_ = _lib.aligned(u.float())
     gk = torch.empty_like(k_)
@@ -88,19 +116,98 @@ def _launch_backward(grad_y: Tensor, w: Tensor, u: Tensor, k: Tensor, v: Tensor)
     return [gk, gv, gtd, gtf]
 
 
-# ------------------------------------------------------------- fp32-I/O op --
-@torch.library.custom_op("myelin::wkv_forward", mutates_args=())
-def _wkv_forward_op(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
-    # fp32 recurrence on the exactly widened inputs; y cast back to key.dtype
-    # (wkv_triton.py:151-158).  bf16/fp16 inputs are widened in registers,
-    # which gives the same values as the reference's .float() copies.
-    y = _launch_forward(key, value, time_decay, time_first)
+# ------------------------------------------------ private training ops ------
+@torch.library.custom_op("myelin::wkv4_forward_train", mutates_args=())
+def _wkv4_forward_train(
+    key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor
+) -> tuple[Tensor, Tensor]:
+    y, ck = _launch_forward(key, value, time_decay, time_first, with_checkpoint=True)
+    return y, ck
+
+
+@_wkv4_forward_train.register_fake
+def _(key, value, time_decay, time_first):
+    b, t, c = key.shape
+    dt = key.dtype if key.dtype == value.dtype and key.dtype in _NATIVE else torch.float32
+    return (
+        torch.empty(key.shape, dtype=dt, device=key.device),
+        torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=key.device),
+    )
+
+
+@torch.library.custom_op("myelin::wkv4_backward_train", mutates_args=())
+def _wkv4_backward_train(
+    grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
+    checkpoint: Tensor,
+) -> list[Tensor]:
+    _lib.require_gpu(grad_y, key, value, time_decay, time_first, checkpoint)
+    b, t, c = key.shape
+    k, v = _compute_inputs(key, value)
+    gy = _lib.aligned(grad_y.to(k.dtype))
+    td = _lib.aligned(time_decay.float())
+    tf = _lib.aligned(time_first.float())
+    ck = _lib.aligned(checkpoint)
+    gk = torch.empty_like(k)
+    gv = torch.empty_like(k)
+    gtd = torch.empty(c, dtype=torch.float32, device=k.device)
+    gtf = torch.empty(c, dtype=torch.float32, device=k.device)
+    ws = torch.empty(2 * b * c, dtype=torch.float32, device=k.device)  # [2, B, C] partials
+    lib = _lib.load()
+    rc = _lib.timed("wkv4_backward", k.device, lambda: lib.wkv4_backward_checkpointed(
+        gy.data_ptr(), td.data_ptr(), tf.data_ptr(), k.data_ptr(), v.data_ptr(), ck.data_ptr(),
+        gk.data_ptr(), gv.data_ptr(), gtd.data_ptr(), gtf.data_ptr(), ws.data_ptr(),
+        ws.numel() * 4, b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k),
+    ))
+    _lib.check(rc, "wkv4_backward_checkpointed")
+    return [gk, gv, gtd, gtf]
+
+
+@_wkv4_backward_train.register_fake
+def _(grad_y, key, value, time_decay, time_first, checkpoint):
+    dt = key.dtype if key.dtype == value.dtype and key.dtype in _NATIVE else torch.float32
+    c = key.shape[-1]
+    f32 = {"dtype": torch.float32, "device": key.device}
+    return [
+        torch.empty(key.shape, dtype=dt, device=key.device),
+        torch.empty(key.shape, dtype=dt, device=key.device),
+        torch.empty(c, **f32),
+        torch.empty(c, **f32),
+    ]
+
+
+def _train_setup_context(ctx, inputs, output):
+    key, value, time_decay, time_first = inputs
+    _, ck = output
+    ctx.save_for_backward(key, value, time_decay, time_first, ck)
+    ctx.mark_non_differentiable(ck)
+    # The records never receive a gradient: do not materialise zeros for it.
+    ctx.set_materialize_grads(False)
+
+
+def _train_backward(ctx, grad_y, _grad_ck):
+    key, value, time_decay, time_first, ck = ctx.saved_tensors
+    gk, gv, gtd, gtf = torch.ops.myelin.wkv4_backward_train(grad_y, key, value, time_decay, time_first, ck)
+    return gk.to(key.dtype), gv.to(value.dtype), gtd.to(time_decay.dtype), gtf.to(time_first.dtype)
+
+
+_wkv4_forward_train.register_autograd(_train_backward, setup_context=_train_setup_context)
+
+
+# ------------------------------------------------------------ public ops ----
+_LIB = torch.library.Library("myelin", "FRAGMENT")
+_LIB.define("wkv_forward(Tensor key, Tensor value, Tensor time_decay, Tensor time_first) -> Tensor")
+_LIB.define("wkv_forward_bf16io(Tensor key, Tensor value, Tensor time_decay, Tensor time_first) -> Tensor")
+
+
+def _forward_composite(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
+    # fp32 recurrence on the exactly widened inputs; y in key.dtype
+    # (wkv_triton.py:151-158; bf16io: wkv_bf16.py:147-154).
+    y, _ = torch.ops.myelin.wkv4_forward_train(key, value, time_decay, time_first)
     return y if y.dtype == key.dtype else y.to(key.dtype)
 
 
-@_wkv_forward_op.register_fake
-def _(key, value, time_decay, time_first):
-    return torch.empty_like(key)
+_LIB.impl("wkv_forward", _forward_composite, "CompositeImplicitAutograd")
+_LIB.impl("wkv_forward_bf16io", _forward_composite, "CompositeImplicitAutograd")
 
 
 @torch.library.custom_op("myelin::wkv_backward", mutates_args=())
@@ -111,39 +218,6 @@ def _wkv_backward_op(grad_y: Tensor, w: Tensor, u: Tensor, k: Tensor, v: Tensor)
 @_wkv_backward_op.register_fake
 def _(grad_y, w, u, k, v):
     return [torch.empty_like(k), torch.empty_like(k), torch.empty_like(w), torch.empty_like(u)]
-
-
-def _setup_context(ctx, inputs, output):
-    key, value, time_decay, time_first = inputs
-    ctx.save_for_backward(key, value, time_decay, time_first)
-
-
-def _backward(ctx, grad_y):
-    key, value, time_decay, time_first = ctx.saved_tensors
-    w = _lib.aligned(-torch.exp(time_decay.float()))
-    u = _lib.aligned(time_first.float())
-    gk, gv, gtd, gtf = torch.ops.myelin.wkv_backward(
-        _lib.aligned(grad_y.float()), w, u, _lib.aligned(key.float()), _lib.aligned(value.float())
-    )
-    return gk.to(key.dtype), gv.to(value.dtype), gtd.to(time_decay.dtype), gtf.to(time_first.dtype)
-
-
-_wkv_forward_op.register_autograd(_backward, setup_context=_setup_context)
-
-
-# ------------------------------------------------------------ 16-bit-I/O op --
-@torch.library.custom_op("myelin::wkv_forward_bf16io", mutates_args=())
-def _wkv_forward_bf16io_op(
-    key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor
-) -> Tensor:
-    # Native-dtype k/v/y (wkv_bf16.py:147-154); fp32 state in registers.
-    y = _launch_forward(key, value, time_decay, time_first)
-    return y if y.dtype == key.dtype else y.to(key.dtype)
-
-
-@_wkv_forward_bf16io_op.register_fake
-def _(key, value, time_decay, time_first):
-    return torch.empty_like(key)
 
 
 @torch.library.custom_op("myelin::wkv_backward_bf16io", mutates_args=())
@@ -158,17 +232,10 @@ def _(grad_y, w, u, k, v):
     return [torch.empty_like(k), torch.empty_like(k), torch.empty_like(w), torch.empty_like(u)]
 
 
-def _backward_bf16io(ctx, grad_y):
-    key, value, time_decay, time_first = ctx.saved_tensors
-    w = _lib.aligned(-torch.exp(time_decay.float()))
-    u = _lib.aligned(time_first.float())
-    gk, gv, gtd, gtf = torch.ops.myelin.wkv_backward_bf16io(
-        _lib.aligned(grad_y), w, u, _lib.aligned(key), _lib.aligned(value)
-    )
-    return gk.to(key.dtype), gv.to(value.dtype), gtd.to(time_decay.dtype), gtf.to(time_first.dtype)
-
-
-_wkv_forward_bf16io_op.register_autograd(_backward_bf16io, setup_context=_setup_context)
+def wkv_forward_no_checkpoint(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
+    """Forward only (no autograd, no checkpoint records): the inference path."""
+    y, _ = _launch_forward(key, value, time_decay, time_first, with_checkpoint=False)
+    return y if y.dtype == key.dtype else y.to(key.dtype)
 
 
 # ------------------------------------------------------------- Python API --

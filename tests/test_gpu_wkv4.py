@@ -238,6 +238,29 @@ def test_out_of_range_inputs_take_the_exact_path(kind):
         _close(g, r, rtol=1e-4, atol_scale=1e-4, what=f"{kind} {name}")
 
 
+@pytest.mark.parametrize("kind", ["wide_keys", "large_time_first", "one_bad_channel"])
+def test_out_of_range_inputs_training_path(kind):
+    # Same inputs through autograd: the forward's records come from the exact
+    # path and the backward recomputes from them.
+    from spikegpt_myelin_amd import weighted_key_value_hip
+
+    b, t, c = 2, 200, 64
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=10)
+    if kind == "wide_keys":
+        k[:, ::7] = 80.0
+        k[:, 3::7] = -80.0
+    elif kind == "large_time_first":
+        tf[:] = 30.0
+    else:
+        k[1, 50, 5] = 120.0
+        k[1, 51, 5] = -40.0
+    got = _grads(weighted_key_value_hip, *(x.to(DEV) for x in (k, v, td, tf)), gy.to(DEV))
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        assert torch.isfinite(g).all(), f"{kind} {name} not finite"
+        _close(g, r, rtol=1e-4, atol_scale=1e-4, what=f"{kind} {name}")
+
+
 def test_empty_sequence_and_batch():
     ops = _lib_ops()
     for shape in [(2, 0, 8), (0, 5, 8)]:
@@ -268,16 +291,23 @@ def test_all_tile_configurations_agree(monkeypatch):
     inputs = O.make_inputs(3, 700, 256, seed=12, dtype=torch.bfloat16)
     kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in inputs)
     ref = _oracle64_fast(*inputs)
-    cfgs = [("1,8,16", "1,8,16"), ("2,8,16", "2,4,16"), ("2,8,8", "2,8,8"), ("1,16,8", "1,16,8"),
-            ("1,8,16", "1,4,16")]
+    cfgs = [("2,8,16", "2,8,8"), ("1,8,16", "1,8,16"), ("2,8,8", "2,4,16"), ("1,16,8", "1,16,8"),
+            ("2,8,16", "1,16,8")]
     for fc, bc in cfgs:
         monkeypatch.setenv("WKV_FWD_CFG", fc)
         monkeypatch.setenv("WKV_BWD_CFG", bc)
         print(f"tile config fwd={fc} bwd={bc}", flush=True)
+        # standalone ops
         y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
         g = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
         for got, r, name in zip((y, *g), ref, ("y", "gk", "gv", "gtd", "gtf")):
             _close(got, r, what=f"cfg {fc}/{bc} {name}", **BF16_TOL)
+        # training path: forward records -> single-sweep backward
+        from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+        got = _grads(weighted_key_value_hip_bf16io, kd, vd, tdd, tfd, gyd)
+        for g2, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+            _close(g2, r, what=f"autograd cfg {fc}/{bc} {name}", **BF16_TOL)
 
 
 def test_compiles_without_graph_breaks():
@@ -300,3 +330,39 @@ def test_language_entry_point_dispatch_and_validation():
     assert torch.equal(weighted_key_value(kd, vd, tdd, tfd), torch.ops.myelin.wkv_forward_bf16io(kd, vd, tdd, tfd))
     with pytest.raises(ValueError, match="same shape"):
         weighted_key_value(kd, vd[..., :16], tdd, tfd)
+
+
+@pytest.mark.skip(reason="host segfault inside torch.cuda.graph capture_end when the op path is "
+                         "captured (library built by ROCm 7.2 hipcc, code object v6, loaded by "
+                         "torch's ROCm 7.0 runtime); cause not yet shown, so the case stays off "
+                         "the GPU until it is")
+def test_graph_capture_replays_match_eager():
+    # The C ABI never allocates, synchronises or memsets, so the op path can
+    # be captured in a HIP graph.  Replay several times with eager work and
+    # synchronisation in between; every replay must equal the eager result.
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(4, 300, 256, seed=15, dtype=torch.bfloat16))
+    leaves = [x.requires_grad_(True) for x in (k, v, td, tf)]
+
+    def step():
+        y = weighted_key_value_hip_bf16io(*leaves)
+        return (y, *torch.autograd.grad(y, leaves, gy))
+
+    eager = [x.clone() for x in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = step()
+    for rep in range(4):
+        junk = torch.randn(1 << 20, device=DEV) * 3  # unrelated eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for got, ref, name in zip(outs, eager, ("y", "gk", "gv", "gtd", "gtf")):
+            assert torch.equal(got, ref), f"replay {rep}: {name} differs from eager"
+        del junk
