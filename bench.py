@@ -326,6 +326,9 @@ def main() -> int:
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-file", default="wkv4_bwd_b64_t1024_c512_pmc.md")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="first run one device copy of this many MiB (a kernel of known traffic "
+                         "for scaling PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path (the WKV recurrence) runs on a "
@@ -336,6 +339,13 @@ def main() -> int:
         print("bench.py needs a HIP GPU", file=sys.stderr)
         return 2
     sys.path.insert(0, str(ROOT))
+    if args.calibration_copy_mib:
+        src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.workload == "decode":
         out = bench_decode(args)
     elif args.workload == "wkv7":

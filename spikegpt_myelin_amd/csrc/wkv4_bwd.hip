@@ -166,41 +166,43 @@ struct Bwd {
     float mx[BPS][VEC], mn[BPS][VEC];
   };
 
-  // row_base is wave-uniform (SGPRs), lane_off the lane's 32-bit offset;
-  // steps past the end re-read step T-1 (masked in the arithmetic).
+  // row_base and ck_row are wave-uniform (SGPRs), lane_boff and ck_boff the
+  // lane's byte offsets; steps past the end re-read step T-1 (masked in the
+  // arithmetic).
   __device__ static __forceinline__ void load(const raw* __restrict__ k, const raw* __restrict__ v,
                                               const raw* __restrict__ g,
-                                              const float* __restrict__ ck, size_t ck_lane,
-                                              size_t ck_field, int seg, int nblk, size_t row_base,
-                                              unsigned lane_off, int t0, int T, int C,
+                                              const float* __restrict__ ck, size_t ck_row,
+                                              unsigned ck_boff, size_t ck_field, int seg, int nblk,
+                                              size_t row_base, unsigned lane_boff, int t0, int T,
+                                              int C,
                                               PackT (&kb)[L], PackT (&vb)[L], PackT (&gb)[L],
                                               Recs& rc) {
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const size_t step = row_base + size_t(min(t0 + i, T - 1)) * C;
-      kb[i].load((k + step) + lane_off);
-      vb[i].load((v + step) + lane_off);
-      gb[i].load((g + step) + lane_off);
+      kb[i].load(byte_offset(k + step, lane_boff));
+      vb[i].load(byte_offset(v + step, lane_boff));
+      gb[i].load(byte_offset(g + step, lane_boff));
     }
-    const float* rec = ck + ck_lane + size_t(seg) * BPS * C;
+    const float* rec = ck + ck_row + size_t(seg) * BPS * C;
     Pack<F32, VEC> a;
-    a.load(rec + 0 * ck_field);
+    a.load(byte_offset(rec + 0 * ck_field, ck_boff));
 #pragma unroll
     for (int c = 0; c < VEC; ++c) rc.o[c] = a.x[c];
-    a.load(rec + 1 * ck_field);
+    a.load(byte_offset(rec + 1 * ck_field, ck_boff));
 #pragma unroll
     for (int c = 0; c < VEC; ++c) rc.p[c] = a.x[c];
-    a.load(rec + 2 * ck_field);
+    a.load(byte_offset(rec + 2 * ck_field, ck_boff));
 #pragma unroll
     for (int c = 0; c < VEC; ++c) rc.q[c] = a.x[c];
 #pragma unroll
     for (int j = 0; j < BPS; ++j) {
       // Blocks past the end repeat the last one (its range is a valid bound).
-      const float* rj = ck + ck_lane + size_t(min(seg * BPS + j, nblk - 1)) * C;
-      a.load(rj + 3 * ck_field);
+      const float* rj = ck + ck_row + size_t(min(seg * BPS + j, nblk - 1)) * C;
+      a.load(byte_offset(rj + 3 * ck_field, ck_boff));
 #pragma unroll
       for (int c = 0; c < VEC; ++c) rc.mx[j][c] = a.x[c];
-      a.load(rj + 4 * ck_field);
+      a.load(byte_offset(rj + 4 * ck_field, ck_boff));
 #pragma unroll
       for (int c = 0; c < VEC; ++c) rc.mn[j][c] = a.x[c];
     }
@@ -212,7 +214,7 @@ struct Bwd {
   template <bool FULL>
   __device__ static __forceinline__ bool segment(
       Smem& sm, int seg, int nseg, int T, int C, int wave, int lane, bool active, size_t row_base,
-      unsigned lane_off, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
+      unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
       const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC],
       bool u_ok, raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC],
       float (&gu)[VEC]) {
@@ -266,8 +268,8 @@ struct Bwd {
         Q[c] = fmaf(Q[c], DL[c], sm.q[c][w][lane]);
       }
     }
-    // Forward recompute: keep z~ = gy/den~ and y (zero past the end).
-    float zz[L][VEC], yy[L][VEC];
+    // Forward recompute: keep z~ = gy/den~ and z~ y (zero past the end).
+    float zz[L][VEC], zy[L][VEC];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const bool valid = FULL || (t0 + i) < T;
@@ -280,7 +282,7 @@ struct Bwd {
         const float z = gb[i].get(c) * r;
         const float y = fmaf(e1, vv, P[c]) * r;
         zz[i][c] = FULL || valid ? z : 0.f;
-        yy[i][c] = FULL || valid ? y : 0.f;
+        zy[i][c] = FULL || valid ? z * y : 0.f;
         P[c] = fmaf(e, vv, P[c] * D[c]);
         Q[c] = fmaf(Q[c], D[c], e);
       }
@@ -293,11 +295,10 @@ struct Bwd {
     for (int i = L - 1; i >= 0; --i) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        const float z = zz[i][c];
         Gp[c] = (Gp[c] + G[c]) * D[c];
         Hp[c] = (Hp[c] + H[c]) * D[c];
-        G[c] = fmaf(G[c], D[c], z);
-        H[c] = fmaf(H[c], D[c], z * yy[i][c]);
+        G[c] = fmaf(G[c], D[c], zz[i][c]);
+        H[c] = fmaf(H[c], D[c], zy[i][c]);
       }
     }
 #pragma unroll
@@ -336,31 +337,40 @@ struct Bwd {
         H[c] = fmaf(DL[c], H[c], sm.H[c][w][lane]);
       }
     }
-    // Reverse pass with outputs.
+    // Reverse pass with outputs (stored together after the pass).
+    OutPack<E, VEC> gko_p[L], gvo_p[L];
 #pragma unroll
     for (int i = L - 1; i >= 0; --i) {
-      const int t = t0 + i;
       float gko[VEC], gvo[VEC];
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
         const float vv = vb[i].get(c);
         const float e = ek[i][c];
         const float z = zz[i][c];
-        const float ze = z * (e * U[c]);
-        const float gkd = ze * (vv - yy[i][c]);
-        gvo[c] = fmaf(e, G[c], ze);
+        const float e1 = e * U[c];
+        // z e1 (v - y) = e1 (z v - z y)
+        const float gkd = e1 * fmaf(z, vv, -zy[i][c]);
+        gvo[c] = fmaf(e, G[c], z * e1);
         gko[c] = fmaf(e, fmaf(vv, G[c], -H[c]), gkd);
         gu[c] += gkd;
         gw[c] = fmaf(e, fmaf(vv, Gp[c], -Hp[c]), gw[c]);
         Gp[c] = (Gp[c] + G[c]) * D[c];
         Hp[c] = (Hp[c] + H[c]) * D[c];
         G[c] = fmaf(G[c], D[c], z);
-        H[c] = fmaf(H[c], D[c], z * yy[i][c]);
+        H[c] = fmaf(H[c], D[c], zy[i][c]);
       }
-      if (active && (FULL || t < T)) {
-        const size_t step = row_base + size_t(t) * C;
-        store_vec<E, VEC>((gk + step) + lane_off, gko);
-        store_vec<E, VEC>((gv + step) + lane_off, gvo);
+      gko_p[i].set(gko);
+      gvo_p[i].set(gvo);
+    }
+    if (active) {
+#pragma unroll
+      for (int i = L - 1; i >= 0; --i) {
+        const int t = t0 + i;
+        if (FULL || t < T) {
+          const size_t step = row_base + size_t(t) * C;
+          gko_p[i].store(byte_offset(gk + step, lane_boff));
+          gvo_p[i].store(byte_offset(gv + step, lane_boff));
+        }
       }
     }
     if (wave == 0) {
@@ -399,12 +409,13 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
   const bool active = c0 < C;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
   // Lanes past the last channel read channel 0 of the row (never stored).
-  const unsigned lane_off = active ? unsigned(lane * VEC) : 0u;
+  const unsigned lane_boff = active ? unsigned(lane * VEC * sizeof(typename E::raw)) : 0u;
   const int nseg = (T + F::SEG - 1) / F::SEG;
   const int nfull = T / F::SEG;
   const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
   const size_t ck_field = size_t(gridDim.x / n_cg) * nblk * C;
-  const size_t ck_lane = size_t(b) * nblk * C + (active ? c0 : 0);
+  const size_t ck_row = size_t(b) * nblk * C + size_t(cg) * F::CPW;
+  const unsigned ck_boff = active ? unsigned(lane * VEC * sizeof(float)) : 0u;
 
   float D[VEC], DL[VEC], U[VEC];
   bool u_ok = true;
@@ -428,29 +439,31 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
     PackT kA[L], vA[L], gA[L], kB[L], vB[L], gB[L];
     typename F::Recs rA, rB;
     const int last = nseg - 1;
-    F::load(k, v, gy, ck, ck_lane, ck_field, last, nblk, row_base, lane_off,
+    F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, last, nblk, row_base, lane_boff,
             last * F::SEG + wave * L, T, C, kA, vA, gA, rA);
+    // The next segment is prefetched on every path (segment 0 prefetches
+    // itself again, a cache hit), so that the wait before a segment's
+    // arithmetic only covers the loads it consumes.
     for (int seg = last; seg >= 0; seg -= 2) {
-      if (seg - 1 >= 0)
-        F::load(k, v, gy, ck, ck_lane, ck_field, seg - 1, nblk, row_base, lane_off,
-                (seg - 1) * F::SEG + wave * L, T, C, kB, vB, gB, rB);
+      const int s1 = max(seg - 1, 0), s2 = max(seg - 2, 0);
+      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s1, nblk, row_base, lane_boff,
+              s1 * F::SEG + wave * L, T, C, kB, vB, gB, rB);
       bad = seg < nfull
                 ? F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base,
-                                            lane_off, kA, vA, gA, rA, D, DL, U, u_ok, gk, gv, gw,
+                                            lane_boff, kA, vA, gA, rA, D, DL, U, u_ok, gk, gv, gw,
                                             gu)
                 : F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base,
-                                             lane_off, kA, vA, gA, rA, D, DL, U, u_ok, gk, gv, gw,
+                                             lane_boff, kA, vA, gA, rA, D, DL, U, u_ok, gk, gv, gw,
                                              gu);
       if (bad || seg - 1 < 0) break;
-      if (seg - 2 >= 0)
-        F::load(k, v, gy, ck, ck_lane, ck_field, seg - 2, nblk, row_base, lane_off,
-                (seg - 2) * F::SEG + wave * L, T, C, kA, vA, gA, rA);
+      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s2, nblk, row_base, lane_boff,
+              s2 * F::SEG + wave * L, T, C, kA, vA, gA, rA);
       bad = seg - 1 < nfull
                 ? F::template segment<true>(sm, seg - 1, nseg, T, C, wave, lane, active,
-                                            row_base, lane_off, kB, vB, gB, rB, D, DL, U, u_ok,
+                                            row_base, lane_boff, kB, vB, gB, rB, D, DL, U, u_ok,
                                             gk, gv, gw, gu)
                 : F::template segment<false>(sm, seg - 1, nseg, T, C, wave, lane, active,
-                                             row_base, lane_off, kB, vB, gB, rB, D, DL, U, u_ok,
+                                             row_base, lane_boff, kB, vB, gB, rB, D, DL, U, u_ok,
                                              gk, gv, gw, gu);
       if (bad) break;
     }
@@ -497,20 +510,23 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
 // grad_time_decay[c] = sum_b gw[b,c] * w[c] (chain rule through
 // w = -exp(time_decay), applied per batch element as the reference does,
 // wkv_triton.py:117,194); grad_time_first[c] = sum_b gu[b,c].  A block
-// covers 64 channels with 4 threads per channel that each sum every fourth
-// batch row; the four partials are added in fixed order (deterministic).
-__global__ __launch_bounds__(256) void wkv4_param_grad_kernel(
+// covers 64 channels with 16 threads per channel, each summing every 16th
+// batch row; the 16 partials are added in a fixed tree order
+// (deterministic).
+__global__ __launch_bounds__(1024) void wkv4_param_grad_kernel(
     const float* __restrict__ gw_part, const float* __restrict__ gu_part,
     const float* __restrict__ decay, int decay_is_w, float* __restrict__ gtd,
     float* __restrict__ gtf, int B, int C) {
-  __shared__ float sw[4][64], su[4][64];
+  constexpr int G = 16;
+  __shared__ float sw[G][64], su[G][64];
   const int lane = threadIdx.x & 63;
   const int grp = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   float aw = 0.f, au = 0.f;
   if (c < C) {
     const float wc = decay_is_w ? decay[c] : -expf(decay[c]);
-    for (int b = grp; b < B; b += 4) {
+#pragma unroll 4
+    for (int b = grp; b < B; b += G) {
       aw += gw_part[size_t(b) * C + c] * wc;
       au += gu_part[size_t(b) * C + c];
     }
@@ -518,9 +534,16 @@ __global__ __launch_bounds__(256) void wkv4_param_grad_kernel(
   sw[grp][lane] = aw;
   su[grp][lane] = au;
   __syncthreads();
+  for (int h = G / 2; h > 0; h >>= 1) {
+    if (grp < h) {
+      sw[grp][lane] += sw[grp + h][lane];
+      su[grp][lane] += su[grp + h][lane];
+    }
+    __syncthreads();
+  }
   if (grp == 0 && c < C) {
-    gtd[c] = (sw[0][lane] + sw[1][lane]) + (sw[2][lane] + sw[3][lane]);
-    gtf[c] = (su[0][lane] + su[1][lane]) + (su[2][lane] + su[3][lane]);
+    gtd[c] = sw[0][lane];
+    gtf[c] = su[0][lane];
   }
 }
 
@@ -537,10 +560,12 @@ namespace wkv_host {
 
 struct TileCfg { int vec, L, W; };
 
-// Tile configurations compiled into the library (no VGPR spills at 64*W
-// threads per workgroup).  SEG = W*L must be a multiple of the 64-step
-// checkpoint block.
-static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}};
+// Tile configurations compiled into the library (selectable with
+// WKV_BWD_CFG="vec,L,W" for measurement).  SEG = W*L must be a multiple of
+// the 64-step checkpoint block.  Defaults: (2,8,8) for 16-bit tensors with
+// enough rows of 128 channels to fill the chip, else (1,16,8); the W=16
+// configurations are capped at 128 VGPRs and spill.
+static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}, {1, 8, 8}};
 
 int pick_vec(int64_t B, int64_t C);
 bool env_cfg(const char* name, int& vec, int& L, int& W);
@@ -554,7 +579,7 @@ static TileCfg pick_bwd_cfg(int64_t B, int64_t C, int elem_bytes) {
       if (c.vec == vec && c.L == L && c.W == W && (vec == 1 || C % 2 == 0)) return c;
   }
   if (elem_bytes == 2 && pick_vec(B, C) == 2) return TileCfg{2, 8, 8};
-  return TileCfg{1, 8, 16};
+  return TileCfg{1, 16, 8};
 }
 
 size_t wkv4_checkpoint_floats(int64_t B, int64_t T, int64_t C) {
@@ -579,7 +604,7 @@ static int launch_bwd(const void* gy, const float* decay, int decay_is_w, const 
                      static_cast<raw*>(gk), static_cast<raw*>(gv), gw_part, gu_part, T, C);
   int rc = check_launch("wkv4_bwd_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(wkv::wkv4_param_grad_kernel, dim3((C + 63) / 64), dim3(256), 0, stream,
+  hipLaunchKernelGGL(wkv::wkv4_param_grad_kernel, dim3((C + 63) / 64), dim3(1024), 0, stream,
                      gw_part, gu_part, decay, decay_is_w, gtd, gtf, B, C);
   return check_launch("wkv4_param_grad_kernel");
 }
@@ -598,6 +623,7 @@ static int dispatch_bwd(const void* gy, const float* decay, int decay_is_w, cons
   WKV_BWD_CASE(1, 8, 16)
   WKV_BWD_CASE(2, 4, 16)
   WKV_BWD_CASE(1, 16, 8)
+  WKV_BWD_CASE(1, 8, 8)
 #undef WKV_BWD_CASE
   return fail(1, "wkv4_backward: no kernel for the selected tile configuration");
 }

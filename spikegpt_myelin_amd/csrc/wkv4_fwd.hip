@@ -67,17 +67,17 @@ struct Fwd {
     float carry[2][3][VEC][64];  // (R, p, q) of the segment carry, by segment parity
   };
 
-  // row_base is wave-uniform (SGPRs); lane_off is the lane's 32-bit element
-  // offset.  Steps past the end re-read step T-1 (masked in the arithmetic).
+  // row_base is wave-uniform (SGPRs); lane_boff is the lane's byte offset.
+  // Steps past the end re-read step T-1 (masked in the arithmetic).
   __device__ static __forceinline__ void load_chunk(const raw* __restrict__ k,
                                                     const raw* __restrict__ v, size_t row_base,
-                                                    unsigned lane_off, int t0, int T, int C,
+                                                    unsigned lane_boff, int t0, int T, int C,
                                                     PackT (&kb)[L], PackT (&vb)[L]) {
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const size_t step = row_base + size_t(min(t0 + i, T - 1)) * C;
-      kb[i].load((k + step) + lane_off);
-      vb[i].load((v + step) + lane_off);
+      kb[i].load(byte_offset(k + step, lane_boff));
+      vb[i].load(byte_offset(v + step, lane_boff));
     }
   }
 
@@ -86,8 +86,8 @@ struct Fwd {
   template <bool FULL>
   __device__ static __forceinline__ bool segment(
       Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
-      unsigned lane_off, raw* __restrict__ y, float* __restrict__ ck, size_t ck_lane,
-      size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L], const float (&D)[VEC],
+      unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
+      unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L], const float (&D)[VEC],
       const float (&DL)[VEC], const float (&U)[VEC], bool u_ok) {
     const int t0 = seg * SEG + wave * L;
     // Phase 0: chunk range of k.
@@ -186,12 +186,12 @@ struct Fwd {
         bmax[c] = br * kLog2e;
         bmin[c] = bl * kLog2e;
       }
-      float* rec = ck + ck_lane + size_t(t0 / kCkptBlock) * C;
-      store_vec<F32, VEC>(rec + 0 * ck_field, R);
-      store_vec<F32, VEC>(rec + 1 * ck_field, pin);
-      store_vec<F32, VEC>(rec + 2 * ck_field, qin);
-      store_vec<F32, VEC>(rec + 3 * ck_field, bmax);
-      store_vec<F32, VEC>(rec + 4 * ck_field, bmin);
+      float* rec = ck + ck_row + size_t(t0 / kCkptBlock) * C;
+      store_vec<F32, VEC>(byte_offset(rec + 0 * ck_field, ck_boff), R);
+      store_vec<F32, VEC>(byte_offset(rec + 1 * ck_field, ck_boff), pin);
+      store_vec<F32, VEC>(byte_offset(rec + 2 * ck_field, ck_boff), qin);
+      store_vec<F32, VEC>(byte_offset(rec + 3 * ck_field, ck_boff), bmax);
+      store_vec<F32, VEC>(byte_offset(rec + 4 * ck_field, ck_boff), bmin);
     }
     if (wave == W - 1) {
 #pragma unroll
@@ -204,9 +204,9 @@ struct Fwd {
 
     // Phase 2: outputs.
     if constexpr (WY) {
+      OutPack<E, VEC> yp[L];
 #pragma unroll
       for (int i = 0; i < L; ++i) {
-        const int t = t0 + i;
         float yv[VEC];
 #pragma unroll
         for (int c = 0; c < VEC; ++c) {
@@ -219,7 +219,14 @@ struct Fwd {
           pin[c] = fmaf(e, vv, pin[c] * D[c]);
           qin[c] = fmaf(qin[c], D[c], e);
         }
-        if (active && (FULL || t < T)) store_vec<E, VEC>((y + (row_base + size_t(t) * C)) + lane_off, yv);
+        yp[i].set(yv);
+      }
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+          const int t = t0 + i;
+          if (FULL || t < T) yp[i].store(byte_offset(y + (row_base + size_t(t) * C), lane_boff));
+        }
       }
     }
     return false;
@@ -290,10 +297,11 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const bool active = c0 < C;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
   // Lanes past the last channel read channel 0 of the row (never stored).
-  const unsigned lane_off = active ? unsigned(lane * VEC) : 0u;
+  const unsigned lane_boff = active ? unsigned(lane * VEC * sizeof(typename E::raw)) : 0u;
   const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
   const size_t ck_field = size_t(gridDim.x / n_cg) * nblk * C;  // B * nblk * C
-  const size_t ck_lane = size_t(b) * nblk * C + (active ? c0 : 0);
+  const size_t ck_row = size_t(b) * nblk * C + size_t(cg) * F::CPW;
+  const unsigned ck_boff = active ? unsigned(lane * VEC * sizeof(float)) : 0u;
 
   float D[VEC], DL[VEC], U[VEC];
   bool u_ok = true;
@@ -313,24 +321,29 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const int nfull = T / F::SEG;
   PackT kA[L], vA[L], kB[L], vB[L];
   bool bad = false;
-  F::load_chunk(k, v, row_base, lane_off, wave * L, T, C, kA, vA);
+  // The next segment is prefetched on every path (the last segment prefetches
+  // itself again, a cache hit): with the same loads issued on every path, the
+  // compiler's wait before a segment's arithmetic only covers the loads it
+  // consumes, not the prefetch issued just before it.
+  const int lastseg = nseg - 1;
+  F::load_chunk(k, v, row_base, lane_boff, wave * L, T, C, kA, vA);
   for (int seg = 0; seg < nseg; seg += 2) {
-    if (seg + 1 < nseg)
-      F::load_chunk(k, v, row_base, lane_off, (seg + 1) * F::SEG + wave * L, T, C, kB, vB);
+    F::load_chunk(k, v, row_base, lane_boff, min(seg + 1, lastseg) * F::SEG + wave * L, T, C, kB,
+                  vB);
     bad = seg < nfull
-              ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, lane_off, y,
-                                          ck, ck_lane, ck_field, kA, vA, D, DL, U, u_ok)
-              : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, lane_off,
-                                           y, ck, ck_lane, ck_field, kA, vA, D, DL, U, u_ok);
+              ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, lane_boff, y,
+                                          ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U, u_ok)
+              : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, lane_boff,
+                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U, u_ok);
     if (bad || seg + 1 >= nseg) break;
-    if (seg + 2 < nseg)
-      F::load_chunk(k, v, row_base, lane_off, (seg + 2) * F::SEG + wave * L, T, C, kA, vA);
+    F::load_chunk(k, v, row_base, lane_boff, min(seg + 2, lastseg) * F::SEG + wave * L, T, C, kA,
+                  vA);
     bad = seg + 1 < nfull
               ? F::template segment<true>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                          lane_off, y, ck, ck_lane, ck_field, kB, vB, D, DL, U,
+                                          lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL, U,
                                           u_ok)
               : F::template segment<false>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                           lane_off, y, ck, ck_lane, ck_field, kB, vB, D, DL, U,
+                                           lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL, U,
                                            u_ok);
     if (bad) break;
   }
@@ -358,7 +371,7 @@ struct TileCfg { int vec, L, W; };
 // Tile configurations compiled into the library (no VGPR spills at 64*W
 // threads per workgroup).  SEG = W*L must be a multiple of the 64-step
 // checkpoint block.
-static constexpr TileCfg kFwdCfgs[] = {{2, 8, 16}, {1, 8, 16}, {2, 8, 8}, {1, 16, 8}};
+static constexpr TileCfg kFwdCfgs[] = {{2, 8, 16}, {1, 8, 16}, {2, 8, 8}, {1, 16, 8}, {1, 8, 8}};
 
 int pick_vec(int64_t B, int64_t C);
 bool env_cfg(const char* name, int& vec, int& L, int& W);
@@ -406,6 +419,7 @@ static int dispatch_fwd(const void* k, const void* v, const float* decay, int de
   WKV_FWD_CASE(1, 8, 16)
   WKV_FWD_CASE(2, 8, 8)
   WKV_FWD_CASE(1, 16, 8)
+  WKV_FWD_CASE(1, 8, 8)
 #undef WKV_FWD_CASE
   return fail(1, "wkv4_forward: no kernel for the selected tile configuration");
 }

@@ -33,6 +33,22 @@ constexpr float kMaxSpread = 80.f;
 constexpr float kMaxJump = 80.f;
 constexpr float kMaxU = 16.f;
 
+// p advanced by b bytes.  Spelled as a 32-bit byte offset added to a
+// wave-uniform pointer so that loads and stores can use the scalar-base +
+// 32-bit vector-offset address form (no per-lane 64-bit address arithmetic).
+template <typename T>
+__device__ __forceinline__ T* byte_offset(T* p, unsigned b) {
+  // Opaque to the optimiser: keeps it from folding the lane offset into a
+  // loop-invariant 64-bit per-lane pointer (which needs a 64-bit vector add
+  // per access instead of the free scalar-base + offset form).
+  asm volatile("" : "+v"(b));
+  if constexpr (__is_const(T)) {
+    return reinterpret_cast<T*>(reinterpret_cast<const char*>(p) + b);
+  } else {
+    return reinterpret_cast<T*>(reinterpret_cast<char*>(p) + b);
+  }
+}
+
 // ---------------------------------------------------------------- math ----
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
@@ -139,6 +155,57 @@ template <int VEC> struct Pack<F16, VEC> {
   __device__ __forceinline__ float get(int c) const {
     const uint32_t w = u[c >> 1];
     return f16_bits_to_float((c & 1) ? (w >> 16) : (w & 0xffffu));
+  }
+};
+
+// VEC floats already converted to the element type, held as 32-bit words
+// until one vector store writes them.  Kernels convert each output as it is
+// produced and issue a segment's stores together, under a single lane
+// predicate.
+template <typename E, int VEC> struct OutPack {
+  static constexpr bool k32 = sizeof(typename E::raw) == 4;
+  static constexpr int N = k32 ? VEC : (VEC + 1) / 2;
+  uint32_t u[N];
+  __device__ __forceinline__ void set(const float (&x)[VEC]) {
+    if constexpr (k32) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) u[c] = __float_as_uint(x[c]);
+    } else {
+      uint16_t h[VEC];
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        if constexpr (__is_same(E, BF16)) {
+          h[c] = float_to_bf16_bits(x[c]);
+        } else {
+          h[c] = float_to_f16_bits(x[c]);
+        }
+      }
+      if constexpr (VEC == 1) {
+        u[0] = h[0];
+      } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) u[i] = uint32_t(h[2 * i]) | (uint32_t(h[2 * i + 1]) << 16);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(typename E::raw* p) const {
+    if constexpr (k32) {
+      if constexpr (VEC == 1) {
+        *reinterpret_cast<uint32_t*>(p) = u[0];
+      } else if constexpr (VEC == 2) {
+        *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
+      } else {
+        *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+      }
+    } else {
+      if constexpr (VEC == 1) {
+        *p = static_cast<uint16_t>(u[0]);
+      } else if constexpr (VEC == 2) {
+        *reinterpret_cast<uint32_t*>(p) = u[0];
+      } else {
+        *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
+      }
+    }
   }
 };
 

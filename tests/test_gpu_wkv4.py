@@ -292,7 +292,7 @@ def test_all_tile_configurations_agree(monkeypatch):
     kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in inputs)
     ref = _oracle64_fast(*inputs)
     cfgs = [("2,8,16", "2,8,8"), ("1,8,16", "1,8,16"), ("2,8,8", "2,4,16"), ("1,16,8", "1,16,8"),
-            ("2,8,16", "1,16,8")]
+            ("2,8,16", "1,16,8"), ("1,8,8", "1,8,8")]
     for fc, bc in cfgs:
         monkeypatch.setenv("WKV_FWD_CFG", fc)
         monkeypatch.setenv("WKV_BWD_CFG", bc)
