@@ -49,10 +49,11 @@ FP32_VALU_PEAK_TFLOPS = 157.3
 METRIC = "WKV fwd+bwd tokens/sec & HBM GB/s (% of peak), B=64 T=1024 C=512 bf16"
 
 WORKLOADS = {
-    "wkv4": dict(B=64, T=1024, C=512, dtype=torch.bfloat16, layers=1),
-    "long": dict(B=24, T=3072, C=512, dtype=torch.bfloat16, layers=1),
-    "216m": dict(B=16, T=1024, C=768, dtype=torch.bfloat16, layers=18),
-    "c0": dict(B=2, T=128, C=512, dtype=torch.float32, layers=1),
+    "wkv4": dict(B=64, T=1024, C=512, dtype=torch.bfloat16, layers=1, slug="wkv4_b64_t1024_c512"),
+    "long": dict(B=24, T=3072, C=512, dtype=torch.bfloat16, layers=1, slug="wkv4_b24_t3072_c512"),
+    "216m": dict(B=16, T=1024, C=768, dtype=torch.bfloat16, layers=18,
+                 slug="wkv4_b16_t1024_c768_x18"),
+    "c0": dict(B=2, T=128, C=512, dtype=torch.float32, layers=1, slug="wkv4_fwd_f32_b2_t128_c512"),
 }
 
 
@@ -106,7 +107,8 @@ def cpu_baseline(B: int, T: int, C: int, sample_batch: int, fwd_only: bool = Fal
 
 
 def read_traffic(path: Path, kernel: str) -> int | None:
-    """HBM bytes per dispatch of ``kernel`` from a committed PMC summary.
+    """HBM bytes per dispatch of ``kernel`` from a committed PMC summary of the
+    same workload.
 
     The summary lists ``traffic_bytes <kernel> <N>`` lines (FETCH_SIZE +
     WRITE_SIZE scaled by a copy-kernel calibration)."""
@@ -150,10 +152,14 @@ def bench_wkv4(args, cfg) -> dict:
                                                   gtf.data_ptr(), ws.data_ptr(), ws.numel() * 4,
                                                   B, T, C, code, sp), "backward")
 
-    def step(events=None):
+    dom_name = "fwd" if fwd_only else "bwd"
+
+    def step(events=None, timed=(dom_name,)):
+        # HIP events (on the launch stream) bracket the launches named in
+        # `timed`; the others run back to back.
         for _ in range(layers):
             for name, fn in (("fwd", fwd),) if fwd_only else (("fwd", fwd), ("bwd", bwd)):
-                if events is None:
+                if events is None or name not in timed:
                     fn()
                     continue
                 s_ev = torch.cuda.Event(enable_timing=True)
@@ -166,6 +172,7 @@ def bench_wkv4(args, cfg) -> dict:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # Timed region: K steps; events around the dominant launch only.
     events: list = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -176,8 +183,16 @@ def bench_wkv4(args, cfg) -> dict:
     per = {}
     for name, s_ev, e_ev in events:
         per.setdefault(name, []).append(s_ev.elapsed_time(e_ev) * 1e-3)
-    fwd_s = statistics.mean(per["fwd"])
-    bwd_s = statistics.mean(per["bwd"]) if "bwd" in per else float("nan")
+    # Attribution pass (not in `value`): events around every launch.
+    events = []
+    for _ in range(args.steps):
+        step(events, timed=("fwd", "bwd"))
+    torch.cuda.synchronize()
+    attr = {}
+    for name, s_ev, e_ev in events:
+        attr.setdefault(name, []).append(s_ev.elapsed_time(e_ev) * 1e-3)
+    fwd_s = statistics.mean(attr["fwd"])
+    bwd_s = statistics.mean(attr["bwd"]) if "bwd" in attr else float("nan")
 
     # The same work through the drop-in op path (torch.library dispatch,
     # allocation and autograd on every call), for reference.
@@ -229,19 +244,25 @@ def bench_wkv4(args, cfg) -> dict:
         "op_tokens_per_s": B * T / op_step_s,
         "fwd_launch_us": fwd_s * 1e6,
     }
+    dom_t = statistics.mean(per[dom_name])
     if fwd_only:
-        dom, dom_bytes, dom_t = "wkv4_fwd_kernel", 3 * esize * B * T * C, fwd_s
+        dom, dom_bytes, launch_kernels = "wkv4_fwd_kernel", 3 * esize * B * T * C, ["wkv4_fwd_kernel"]
     else:
         out["bwd_launch_us"] = bwd_s * 1e6
-        dom, dom_bytes, dom_t = "wkv4_bwd_kernel", 5 * esize * B * T * C, bwd_s
+        dom, dom_bytes = "wkv4_bwd_kernel", 5 * esize * B * T * C
+        launch_kernels = ["wkv4_bwd_kernel", "wkv4_param_grad_kernel"]
     achieved = dom_bytes / dom_t / 1e9
-    traffic = read_traffic(ROOT / "profiles" / args.traffic_file, dom) if args.traffic_file else None
+    traffic_file = ROOT / "profiles" / f"{cfg['slug']}_pmc.md"
+    parts = [read_traffic(traffic_file, kname) for kname in launch_kernels]
+    traffic = sum(parts) if all(p is not None for p in parts) else None
     out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
                        "algorithmic_bytes_per_launch": dom_bytes,
                        "avg_launch_us": dom_t * 1e6,
-                       "launch": ("wkv4_backward_checkpointed: the reverse-sweep kernel plus the "
-                                  "batch-sum kernel" if not fwd_only else "wkv4_forward_checkpointed")}
+                       "launch": ("wkv4_backward_checkpointed: " if not fwd_only
+                                  else "wkv4_forward_checkpointed: ") + " + ".join(launch_kernels),
+                       "traffic_source": (str(traffic_file.relative_to(ROOT))
+                                          if traffic is not None else None)}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, T, C, args.cpu_sample_batch, fwd_only=fwd_only)
     return out
@@ -325,15 +346,14 @@ def main() -> int:
     ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--traffic-file", default="wkv4_bwd_b64_t1024_c512_pmc.md")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="first run one device copy of this many MiB (a kernel of known traffic "
                          "for scaling PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build's hot path (the WKV recurrence) runs on a "
-              "single MI355X; multi-GPU runs are not part of it (see DESIGN.md for how it would "
-              "shard).", file=sys.stderr)
+        print("bench.py measures one GPU: the WKV recurrence is benchmarked on a single MI355X "
+              "(per-GPU throughput at the per-GPU batch); multi-GPU runs are not part of it.",
+              file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)

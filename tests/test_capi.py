@@ -60,6 +60,14 @@ def test_host_side_argument_errors(lib):
     assert lib.wkv4_forward(None, None, None, None, None, 0, 5, 8, 0, None) == 0
 
 
+def test_checkpoint_size_matches_python_layout(lib):
+    from spikegpt_myelin_amd.wkv import checkpoint_shape
+    for b, t, c in [(64, 1024, 512), (3, 7, 96), (1, 1, 1), (24, 3072, 512), (2, 65, 4100)]:
+        f, bb, nblk, cc = checkpoint_shape(b, t, c)
+        assert (f, bb, nblk, cc) == (5, b, (t + 63) // 64, c)
+        assert lib.wkv4_checkpoint_bytes(b, t, c) == 4 * f * bb * nblk * cc
+
+
 def test_backward_workspace_size_and_check(lib):
     n = lib.wkv4_backward_workspace_bytes(64, 1024, 512, 1)
     # per-segment checkpoints (3 floats per channel per segment) + [B, C] partials
