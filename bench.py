@@ -118,6 +118,27 @@ def read_traffic(path: Path, kernel: str) -> int | None:
     return int(m.group(1)) if m else None
 
 
+class EventPool:
+    """Timing events created and recorded once before the timed region (a
+    HIP event is created at its first record, which costs host time that
+    would otherwise land inside the timed loop)."""
+
+    def __init__(self, n: int, stream) -> None:
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        for ev in self.events:
+            ev.record(stream)
+        torch.cuda.synchronize()
+        self.next = 0
+
+    def take(self):
+        ev = self.events[self.next]
+        self.next += 1
+        return ev
+
+    def reset(self) -> None:
+        self.next = 0
+
+
 def bench_wkv4(args, cfg) -> dict:
     import spikegpt_myelin_amd  # noqa: F401  -- registers the ops
     from spikegpt_myelin_amd import _lib
@@ -153,6 +174,7 @@ def bench_wkv4(args, cfg) -> dict:
                                                   B, T, C, code, sp), "backward")
 
     dom_name = "fwd" if fwd_only else "bwd"
+    pool = EventPool(4 * args.steps * layers, stream)
 
     def step(events=None, timed=(dom_name,)):
         # HIP events (on the launch stream) bracket the launches named in
@@ -162,8 +184,8 @@ def bench_wkv4(args, cfg) -> dict:
                 if events is None or name not in timed:
                     fn()
                     continue
-                s_ev = torch.cuda.Event(enable_timing=True)
-                e_ev = torch.cuda.Event(enable_timing=True)
+                s_ev = pool.take()
+                e_ev = pool.take()
                 s_ev.record(stream)
                 fn()
                 e_ev.record(stream)
@@ -184,6 +206,7 @@ def bench_wkv4(args, cfg) -> dict:
     for name, s_ev, e_ev in events:
         per.setdefault(name, []).append(s_ev.elapsed_time(e_ev) * 1e-3)
     # Attribution pass (not in `value`): events around every launch.
+    pool.reset()
     events = []
     for _ in range(args.steps):
         step(events, timed=("fwd", "bwd"))
@@ -270,7 +293,7 @@ def bench_wkv4(args, cfg) -> dict:
 
 def bench_decode(args) -> dict:
     import spikegpt_myelin_amd  # noqa: F401
-    from spikegpt_myelin_amd import initial_wkv_state
+    from spikegpt_myelin_amd import _lib, initial_wkv_state
     from oracle import wkv4 as O
 
     B, C, layers = 256, 768, 18
@@ -280,11 +303,21 @@ def bench_decode(args) -> dict:
         k, v, td, tf, _ = O.make_inputs(B, 1, C, seed=100 + layer, with_grad=False)
         ks.append(k[:, 0].to(dev)); vs.append(v[:, 0].to(dev)); tds.append(td.to(dev)); tfs.append(tf.to(dev))
     states = [initial_wkv_state(B, C, dev) for _ in range(layers)]
+    ys = [torch.empty_like(k) for k in ks]
+    lib = _lib.load()
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    code = _lib.dtype_code(torch.float32)
 
     def step():
+        # One token through the 18 layers' state updates (C-ABI launches,
+        # state updated in place, outputs preallocated).
         for layer in range(layers):
-            y, *st = torch.ops.myelin.wkv_decode_step(ks[layer], vs[layer], tds[layer], tfs[layer], *states[layer])
-            states[layer] = st
+            num, den, ls = states[layer]
+            _lib.check(lib.wkv4_decode_step(
+                ks[layer].data_ptr(), vs[layer].data_ptr(), tds[layer].data_ptr(),
+                tfs[layer].data_ptr(), num.data_ptr(), den.data_ptr(), ls.data_ptr(),
+                ys[layer].data_ptr(), num.data_ptr(), den.data_ptr(), ls.data_ptr(), B, C, code, sp),
+                "decode")
 
     for _ in range(args.warmup):
         step()
