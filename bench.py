@@ -24,8 +24,8 @@ Reported beside the throughput:
 
 Other workloads (``--workload``): ``long`` (B=24, T=3072, C=512), ``216m``
 (B=16, T=1024, C=768, 18 layers), ``decode`` (B=256, C=768, 18 layers, fp32
-state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward), ``c0`` (fp32
-forward B=2, T=128, C=512).
+state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward + backward), ``c0``
+(fp32 forward B=2, T=128, C=512).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -341,33 +341,82 @@ def bench_decode(args) -> dict:
 
 
 def bench_wkv7(args) -> dict:
+    """RWKV-7 DPLR forward (with state checkpoints) + backward through the C
+    ABI on preallocated buffers, B=16 T=1024 H=12 N=64, bf16 I/O, fp32 state."""
     import spikegpt_myelin_amd  # noqa: F401
     from spikegpt_myelin_amd import _lib
+    from spikegpt_myelin_amd.wkv7 import checkpoint_shape
     from oracle import wkv7 as O7
 
     B, T, H, N = 16, 1024, 12, 64
     dev = torch.device("cuda", 0)
     xs = [x.to(dev) for x in O7.make_inputs(B, T, H, N, seed=4, dtype=torch.bfloat16)]
+    gy = torch.randn(B, T, H, N, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
+    y = torch.empty_like(xs[0])
+    s_out = torch.empty(B, H, N, N, dtype=torch.float32, device=dev)
+    ck = torch.empty(checkpoint_shape(B, T, H), dtype=torch.float32, device=dev)
+    grads = [torch.empty_like(xs[0]) for _ in range(6)]
+    lib = _lib.load()
+    code = _lib.dtype_code(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    ptrs = [x.data_ptr() for x in xs]
+
+    def fwd():
+        _lib.check(lib.wkv7_forward_checkpointed(*ptrs, None, y.data_ptr(), s_out.data_ptr(),
+                                                 ck.data_ptr(), B, T, H, N, code, sp), "wkv7 forward")
+
+    def bwd():
+        _lib.check(lib.wkv7_backward_checkpointed(*ptrs, ck.data_ptr(), gy.data_ptr(), None,
+                                                  *[g.data_ptr() for g in grads], None,
+                                                  B, T, H, N, code, sp), "wkv7 backward")
+
+    pool = EventPool(4 * args.steps, stream)
     for _ in range(args.warmup):
-        torch.ops.myelin.wkv7_forward(*xs, None)
+        fwd()
+        bwd()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        torch.ops.myelin.wkv7_forward(*xs, None)
+        fwd()
+        bwd()
     torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
-    flops = 9 * N * N * B * T * H
-    alg = 14 * N * B * T * H
+    elapsed = time.perf_counter() - t0
+    step_s = elapsed / args.steps
+    per = {"fwd": [], "bwd": []}
+    evs = []
+    for _ in range(args.steps):
+        for name, fn in (("fwd", fwd), ("bwd", bwd)):
+            s_ev, e_ev = pool.take(), pool.take()
+            s_ev.record(stream)
+            fn()
+            e_ev.record(stream)
+            evs.append((name, s_ev, e_ev))
+    torch.cuda.synchronize()
+    for name, s_ev, e_ev in evs:
+        per[name].append(s_ev.elapsed_time(e_ev) * 1e-3)
+    fwd_t, bwd_t = statistics.mean(per["fwd"]), statistics.mean(per["bwd"])
+    units = B * T * H
+    fwd_flops = 9 * N * N * units   # sa, update, y per state element
+    bwd_flops = 19 * N * N * units  # reverse recurrence (recomputation not counted)
+    fwd_bytes = 14 * N * units      # r, w, k, v, a, b read, y written (bf16)
+    bwd_bytes = 26 * N * units      # 6 inputs + dy read, 6 grads written (bf16)
+    achieved = bwd_flops / bwd_t / 1e12
     return {
-        "metric": "RWKV-7 DPLR forward tokens/sec, B=16 T=1024 H=12 N=64 bf16 I/O fp32 state",
+        "metric": "RWKV-7 DPLR fwd+bwd tokens/sec, B=16 T=1024 H=12 N=64 bf16 I/O fp32 state",
         "value": B * T / step_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "wkv7_forward", "B": B, "T": T, "H": H, "N": N, "io_dtype": "bfloat16"},
-        "roofline": {"bound": "valu", "achieved": flops / step_s / 1e12, "peak": FP32_VALU_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": flops / step_s / 1e12 / FP32_VALU_PEAK_TFLOPS,
-                     "traffic": None, "kernel": "wkv7_fwd_kernel"},
-        "hbm_gbps_algorithmic": alg / step_s / 1e9,
+        "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "wkv7_fwd_bwd", "B": B, "T": T, "H": H, "N": N,
+                   "io_dtype": "bfloat16", "state_dtype": "float32",
+                   "timing": "C-ABI launches on preallocated buffers"},
+        "fwd_launch_us": fwd_t * 1e6, "bwd_launch_us": bwd_t * 1e6,
+        "fwd_tflops": fwd_flops / fwd_t / 1e12,
+        "hbm_gbps_algorithmic": (fwd_bytes + bwd_bytes) / step_s / 1e9,
+        "roofline": {"bound": "valu", "achieved": achieved, "peak": FP32_VALU_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_VALU_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "wkv7_bwd_kernel", "algorithmic_flops_per_launch": bwd_flops,
+                     "avg_launch_us": bwd_t * 1e6},
     }
 
 

@@ -117,12 +117,50 @@ int wkv4_decode_step(const void* k, const void* v, const float* time_decay, cons
  *   S_t = S_{t-1} (diag(w_t) + a_t b_t^T) + v_t k_t^T,   y_t = S_t r_t
  * r, w, k, v, a, b, y: [B,T,H,64] in `dtype`; S is [N_v=64, N_k=64] fp32.
  * s0 (optional, may be NULL = zeros) and s_out (optional, may be NULL):
- * [B,H,64,64] fp32.  The reference's RWKV-7 code was deleted
- * (benchmarks/results/optimizer_wkv_experiments_5090.md:3); this op has no
+ * [B,H,64,64] fp32.  All pointers 16-byte aligned.  The reference's RWKV-7
+ * code was deleted (benchmarks/results/optimizer_wkv_experiments_5090.md:3,
+ * where its arithmetic came from the external `fla` package); this op has no
  * surviving counterpart there. */
 int wkv7_forward(const void* r, const void* w, const void* k, const void* v, const void* a,
                  const void* b, const float* s0, void* y, float* s_out, int64_t B, int64_t T,
                  int64_t H, int64_t N, int dtype, void* stream);
+
+/* Bytes of the RWKV-7 state checkpoints: the 64x64 fp32 state at the start of
+ * every 16-step block, [B*H][ceil(T/16)][64][64]. */
+size_t wkv7_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int64_t N);
+
+/* wkv7_forward that also writes the state checkpoints (y and s_out may be
+ * NULL).  Used by the training path so that the backward does not replay the
+ * sequence from its start; no counterpart in the reference. */
+int wkv7_forward_checkpointed(const void* r, const void* w, const void* k, const void* v,
+                              const void* a, const void* b, const float* s0, void* y,
+                              float* s_out, float* checkpoint, int64_t B, int64_t T, int64_t H,
+                              int64_t N, int dtype, void* stream);
+
+/* Bytes of device workspace wkv7_backward needs (the checkpoints it computes
+ * itself). */
+size_t wkv7_backward_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t N);
+
+/* RWKV-7 DPLR backward.  Inputs as wkv7_forward plus grad_y [B,T,H,64] in
+ * `dtype` and grad_s_out [B,H,64,64] fp32 (gradient of the final state; may be
+ * NULL = zeros).  Outputs grad_r, grad_w, grad_k, grad_v, grad_a, grad_b
+ * [B,T,H,64] in `dtype` and grad_s0 [B,H,64,64] fp32 (may be NULL).
+ * `workspace` must hold wkv7_backward_workspace_bytes() bytes.  No
+ * counterpart in the reference (see wkv7_forward). */
+int wkv7_backward(const void* r, const void* w, const void* k, const void* v, const void* a,
+                  const void* b, const float* s0, const void* grad_y, const float* grad_s_out,
+                  void* grad_r, void* grad_w, void* grad_k, void* grad_v, void* grad_a,
+                  void* grad_b, float* grad_s0, void* workspace, size_t workspace_bytes,
+                  int64_t B, int64_t T, int64_t H, int64_t N, int dtype, void* stream);
+
+/* wkv7_backward from the checkpoints of wkv7_forward_checkpointed on the same
+ * inputs and initial state (no workspace). */
+int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, const void* v,
+                               const void* a, const void* b, const float* checkpoint,
+                               const void* grad_y, const float* grad_s_out, void* grad_r,
+                               void* grad_w, void* grad_k, void* grad_v, void* grad_a,
+                               void* grad_b, float* grad_s0, int64_t B, int64_t T, int64_t H,
+                               int64_t N, int dtype, void* stream);
 
 /* Text of the last error raised on the calling thread ("" if none). */
 const char* wkv_last_error_string(void);

@@ -81,3 +81,61 @@ def make_inputs(batch: int, steps: int, heads: int, n: int = 64, *, seed: int, d
     a = -kappa
     b = kappa * iclr
     return tuple(t.to(dtype) for t in (r, w, k, v, a, b))
+
+
+def wkv7_autograd_grads(r, w, k, v, a, b, state, gy, gs=None):
+    """Gradients of ``sum(y * gy) + sum(S_T * gs)`` by torch autograd through
+    :func:`wkv7_loop` (in the inputs' dtype, normally float64).  Returns
+    ``(y, S_T, dr, dw, dk, dv, da, db, d_state)``."""
+    leaves = [x.detach().clone().requires_grad_(True) for x in (r, w, k, v, a, b)]
+    s0 = None if state is None else state.detach().clone().requires_grad_(True)
+    y, s = wkv7_loop(*leaves, state=s0)
+    loss = (y * gy).sum()
+    if gs is not None:
+        loss = loss + (s * gs).sum()
+    wrt = leaves + ([s0] if s0 is not None else [])
+    grads = torch.autograd.grad(loss, wrt, allow_unused=True)
+    grads = [torch.zeros_like(x) if g is None else g for g, x in zip(grads, wrt)]
+    ds0 = grads[6] if s0 is not None else None
+    return (y.detach(), s.detach(), *grads[:6], ds0)
+
+
+def wkv7_backward_loop(r, w, k, v, a, b, state, gy, gs=None):
+    """The explicit reverse recurrence (a second formulation of the gradients,
+    the one the HIP backward evaluates), with G = dL/dS_t::
+
+        G += dy_t r_t^T;       dr_t = S_t^T dy_t
+        c  = G b_t;            dv_t = G k_t;   dk_t = G^T v_t;  db_t = G^T (S_{t-1} a_t)
+        dw_t = colsum(G o S_{t-1});            da_t = S_{t-1}^T c
+        G  = G diag(w_t) + c a_t^T             (after t = 0: dL/dS_0)
+
+    Forward states are stored for every step (small inputs only).  Returns
+    ``(dr, dw, dk, dv, da, db, d_state)``.
+    """
+    bsz, steps, heads, n = r.shape
+    dt = r.dtype
+    s = torch.zeros((bsz, heads, n, n), dtype=dt) if state is None else state.to(dt).clone()
+    states = [s]
+    sas = []
+    for t in range(steps):
+        rt, wt, kt, vt, at, bt = (x[:, t] for x in (r, w, k, v, a, b))
+        sa = (s * at[:, :, None, :]).sum(-1)
+        sas.append(sa)
+        s = s * wt[:, :, None, :] + sa[..., :, None] * bt[:, :, None, :] + vt[..., :, None] * kt[:, :, None, :]
+        states.append(s)
+    g = torch.zeros((bsz, heads, n, n), dtype=dt) if gs is None else gs.to(dt).clone()
+    outs = [torch.zeros_like(r) for _ in range(6)]
+    dr, dw, dk, dv, da, db = outs
+    for t in range(steps - 1, -1, -1):
+        rt, wt, kt, vt, at, bt, dyt = (x[:, t] for x in (r, w, k, v, a, b, gy))
+        s_t, s_prev = states[t + 1], states[t]
+        g = g + dyt[..., :, None] * rt[:, :, None, :]
+        dr[:, t] = (s_t * dyt[..., :, None]).sum(-2)
+        c = (g * bt[:, :, None, :]).sum(-1)
+        dv[:, t] = (g * kt[:, :, None, :]).sum(-1)
+        dk[:, t] = (g * vt[..., :, None]).sum(-2)
+        db[:, t] = (g * sas[t][..., :, None]).sum(-2)
+        dw[:, t] = (g * s_prev).sum(-2)
+        da[:, t] = (s_prev * c[..., :, None]).sum(-2)
+        g = g * wt[:, :, None, :] + c[..., :, None] * at[:, :, None, :]
+    return (*outs, g)

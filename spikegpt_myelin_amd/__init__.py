@@ -8,7 +8,8 @@ spikegpt_myelin_amd.build``):
   ``myelin::wkv_forward_bf16io`` / ``myelin::wkv_backward_bf16io`` (16-bit
   I/O) -- the reference's op names and schemas;
 * ``myelin::wkv_decode_step`` -- one-token WKV state update for generation;
-* ``myelin::wkv7_forward`` -- RWKV-7 DPLR recurrence.
+* ``myelin::wkv7_forward`` / ``myelin::wkv7_backward`` -- RWKV-7 DPLR
+  recurrence (the forward is differentiable).
 """
 
 from .decode import initial_wkv_state, wkv_decode_step
@@ -19,7 +20,7 @@ from .wkv import (
     weighted_key_value_triton,
     weighted_key_value_triton_bf16io,
 )
-from .wkv7 import wkv7_forward
+from .wkv7 import wkv7_backward, wkv7_forward
 
 __all__ = [
     "initial_wkv_state",
@@ -29,6 +30,7 @@ __all__ = [
     "weighted_key_value_hip_bf16io",
     "weighted_key_value_triton",
     "weighted_key_value_triton_bf16io",
+    "wkv7_backward",
     "wkv7_forward",
     "wkv_decode_step",
 ]

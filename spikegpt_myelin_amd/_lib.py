@@ -48,6 +48,20 @@ SIGNATURES = {
     ),
     "wkv4_decode_step": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
     "wkv7_forward": (_INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P]),
+    "wkv7_checkpoint_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "wkv7_forward_checkpointed": (
+        _INT,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _INT, _P],
+    ),
+    "wkv7_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "wkv7_backward": (
+        _INT,
+        [_P] * 16 + [_P, _SZ, _I64, _I64, _I64, _I64, _INT, _P],
+    ),
+    "wkv7_backward_checkpointed": (
+        _INT,
+        [_P] * 16 + [_I64, _I64, _I64, _I64, _INT, _P],
+    ),
     "wkv_last_error_string": (ctypes.c_char_p, []),
     "wkv_version": (ctypes.c_char_p, []),
 }

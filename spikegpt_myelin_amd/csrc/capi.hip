@@ -68,7 +68,12 @@ int wkv4_decode_impl(const void*, const void*, const float*, const float*, const
                      const float*, const float*, void*, float*, float*, float*, int, int, int,
                      hipStream_t);
 int wkv7_forward_impl(const void*, const void*, const void*, const void*, const void*,
-                      const void*, const float*, void*, float*, int, int, int, int, hipStream_t);
+                      const void*, const float*, void*, float*, float*, int, int, int, int,
+                      hipStream_t);
+int wkv7_backward_ck_impl(const void*, const void*, const void*, const void*, const void*,
+                          const void*, const void*, const float*, const float*, void*, void*,
+                          void*, void*, void*, void*, float*, int, int, int, int, hipStream_t);
+size_t wkv7_checkpoint_floats(int64_t, int64_t, int64_t);
 
 static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }
 
@@ -220,8 +225,113 @@ int wkv7_forward(const void* r, const void* w, const void* k, const void* v, con
   if (T > 0 && (!r || !w || !k || !v || !a || !b || !y))
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: null pointer");
   if (T == 0 && !s_out) return WKV_OK;
-  return wkv7_forward_impl(r, w, k, v, a, b, s0, y, s_out, int(B), int(T), int(H), dtype,
+  if (!aligned16({r, w, k, v, a, b, s0, y, s_out}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: tensors must be 16-byte aligned");
+  return wkv7_forward_impl(r, w, k, v, a, b, s0, y, s_out, nullptr, int(B), int(T), int(H), dtype,
                            static_cast<hipStream_t>(stream));
+}
+
+size_t wkv7_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int64_t N) {
+  if (N != 64 || !dims_ok(B, T, H * N)) return 0;
+  return wkv7_checkpoint_floats(B, T, H) * sizeof(float);
+}
+
+int wkv7_forward_checkpointed(const void* r, const void* w, const void* k, const void* v,
+                              const void* a, const void* b, const float* s0, void* y,
+                              float* s_out, float* checkpoint, int64_t B, int64_t T, int64_t H,
+                              int64_t N, int dtype, void* stream) {
+  set_error("");
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward_checkpointed: unknown dtype");
+  if (N != 64)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward_checkpointed: head size must be 64");
+  if (!dims_ok(B, T, H * N))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward_checkpointed: bad sizes");
+  if (B == 0 || H == 0) return WKV_OK;
+  if (T > 0 && (!r || !w || !k || !v || !a || !b || !checkpoint))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward_checkpointed: null pointer");
+  if (T == 0 && !s_out) return WKV_OK;
+  if (!aligned16({r, w, k, v, a, b, s0, y, s_out, checkpoint}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv7_forward_checkpointed: tensors must be 16-byte aligned");
+  return wkv7_forward_impl(r, w, k, v, a, b, s0, y, s_out, T > 0 ? checkpoint : nullptr, int(B),
+                           int(T), int(H), dtype, static_cast<hipStream_t>(stream));
+}
+
+static int wkv7_backward_checks(const char* what, const void* r, const void* w, const void* k,
+                                const void* v, const void* a, const void* b, const void* grad_y,
+                                const float* grad_s_out, void* grad_r, void* grad_w, void* grad_k,
+                                void* grad_v, void* grad_a, void* grad_b, float* grad_s0,
+                                int64_t B, int64_t T, int64_t H, int64_t N, int dtype) {
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, std::string(what) + ": unknown dtype");
+  if (N != 64)
+    return fail(WKV_ERR_INVALID_ARGUMENT, std::string(what) + ": head size must be 64");
+  if (!dims_ok(B, T, H * N)) return fail(WKV_ERR_INVALID_ARGUMENT, std::string(what) + ": bad sizes");
+  if (T > 0 && (!r || !w || !k || !v || !a || !b || !grad_y || !grad_r || !grad_w || !grad_k ||
+                !grad_v || !grad_a || !grad_b))
+    return fail(WKV_ERR_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+  if (!aligned16({r, w, k, v, a, b, grad_y, grad_s_out, grad_r, grad_w, grad_k, grad_v, grad_a,
+                  grad_b, grad_s0}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                std::string(what) + ": tensors must be 16-byte aligned");
+  return WKV_OK;
+}
+
+size_t wkv7_backward_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t N) {
+  return wkv7_checkpoint_bytes(B, T, H, N);
+}
+
+int wkv7_backward(const void* r, const void* w, const void* k, const void* v, const void* a,
+                  const void* b, const float* s0, const void* grad_y, const float* grad_s_out,
+                  void* grad_r, void* grad_w, void* grad_k, void* grad_v, void* grad_a,
+                  void* grad_b, float* grad_s0, void* workspace, size_t workspace_bytes,
+                  int64_t B, int64_t T, int64_t H, int64_t N, int dtype, void* stream) {
+  set_error("");
+  int rc = wkv7_backward_checks("wkv7_backward", r, w, k, v, a, b, grad_y, grad_s_out, grad_r,
+                                grad_w, grad_k, grad_v, grad_a, grad_b, grad_s0, B, T, H, N,
+                                dtype);
+  if (rc) return rc;
+  if (B == 0 || H == 0) return WKV_OK;
+  if (T == 0 && !grad_s0) return WKV_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* ck = nullptr;
+  if (T > 0) {
+    const size_t need = wkv7_checkpoint_floats(B, T, H) * sizeof(float);
+    if (!workspace || workspace_bytes < need)
+      return fail(WKV_ERR_WORKSPACE_TOO_SMALL,
+                  "wkv7_backward: workspace too small (need " + std::to_string(need) + " bytes)");
+    if (!aligned16({s0, workspace}))
+      return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_backward: tensors must be 16-byte aligned");
+    ck = static_cast<float*>(workspace);
+    rc = wkv7_forward_impl(r, w, k, v, a, b, s0, nullptr, nullptr, ck, int(B), int(T), int(H),
+                           dtype, s);
+    if (rc) return rc;
+  }
+  return wkv7_backward_ck_impl(r, w, k, v, a, b, grad_y, ck, grad_s_out, grad_r, grad_w, grad_k,
+                               grad_v, grad_a, grad_b, grad_s0, int(B), int(T), int(H), dtype, s);
+}
+
+int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, const void* v,
+                               const void* a, const void* b, const float* checkpoint,
+                               const void* grad_y, const float* grad_s_out, void* grad_r,
+                               void* grad_w, void* grad_k, void* grad_v, void* grad_a,
+                               void* grad_b, float* grad_s0, int64_t B, int64_t T, int64_t H,
+                               int64_t N, int dtype, void* stream) {
+  set_error("");
+  int rc = wkv7_backward_checks("wkv7_backward_checkpointed", r, w, k, v, a, b, grad_y,
+                                grad_s_out, grad_r, grad_w, grad_k, grad_v, grad_a, grad_b,
+                                grad_s0, B, T, H, N, dtype);
+  if (rc) return rc;
+  if (B == 0 || H == 0) return WKV_OK;
+  if (T == 0 && !grad_s0) return WKV_OK;
+  if (T > 0 && !checkpoint)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_backward_checkpointed: null pointer");
+  if (!aligned16({checkpoint}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv7_backward_checkpointed: tensors must be 16-byte aligned");
+  return wkv7_backward_ck_impl(r, w, k, v, a, b, grad_y, checkpoint, grad_s_out, grad_r, grad_w,
+                               grad_k, grad_v, grad_a, grad_b, grad_s0, int(B), int(T), int(H),
+                               dtype, static_cast<hipStream_t>(stream));
 }
 
 const char* wkv_last_error_string(void) { return g_last_error.c_str(); }

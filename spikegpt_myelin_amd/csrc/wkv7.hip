@@ -1,16 +1,39 @@
-// RWKV-7 DPLR ("diagonal plus low rank") recurrence, forward, for gfx950.
+// RWKV-7 DPLR ("diagonal plus low rank") recurrence, forward and backward,
+// for gfx950.
 //
 // Per (batch, head) with head size N = 64 and state S[i][j] (i: value index,
 // j: key index), for each step t:
-//   S <- S (diag(w_t) + a_t b_t^T) + v_t k_t^T,   y_t = S r_t.
-// Row i evolves as  S_i <- S_i * w + (S_i . a) b + v_i k ,  so the 64 rows
-// are independent recurrences sharing the step's vectors.  One workgroup owns
-// one (batch, head); NT threads share a row, each holding N/NT state columns
-// in registers; the step's six input vectors are staged through LDS
-// (double-buffered, loaded one step ahead) and the two row dot products
-// (S_i . a and S_i . r) are reduced across the NT threads with cross-lane
-// shuffles.  The arithmetic is fp32 on the vector ALUs: ~5 operations per
-// state element per step, no matrix cores.
+//   sa_t = S_{t-1} a_t,
+//   S_t  = S_{t-1} diag(w_t) + sa_t b_t^T + v_t k_t^T,
+//   y_t  = S_t r_t.
+// Row i evolves as  S_i <- S_i * w + (S_i . a) b + v_i k :  the 64 rows are
+// independent recurrences that share the step's vectors.
+//
+// Backward (G = dL/dS_t, accumulated from the last step to the first):
+//   G     += dy_t r_t^T                      dr_t = S_t^T dy_t
+//   c      = G b_t                           dv_t = G k_t
+//   dk_t   = G^T v_t                         db_t = G^T sa_t
+//   dw_t   = colsum(G o S_{t-1})             da_t = S_{t-1}^T c
+//   G     <- G diag(w_t) + c a_t^T           (dL/dS_{t-1}; after step 0, dL/dS_0)
+//
+// Layout.  One 256-thread workgroup (4 waves) owns one (batch, head).  Lane
+// (rg, cg) of wave wv (rg = lane / 16 is the 16-lane DPP row, cg = lane % 16)
+// holds the 4x4 block of the state at rows 16 wv + 4 rg .. +3 and columns
+// 4 cg .. +3 in registers.  Sums over j (S a, S r, G k, G b) are in-thread
+// over 4 columns, then a DPP butterfly across the 16 lanes of a DPP row (no
+// LDS).  Sums over i (the key-indexed gradients) are in-thread over 4 rows,
+// then two gfx950 permlane swaps across the 4 DPP rows of the wave, then LDS
+// across the 4 waves once per sub-chunk.  The step vectors of KC = 16 steps
+// are staged in LDS as fp32 (double-buffered; the next block is loaded into
+// registers while the current one is computed).  Arithmetic is fp32 on the
+// vector ALUs; no matrix cores.
+//
+// Checkpoints.  The forward can write the state at the start of every
+// KC-step block ([B*H][ceil(T/KC)][64][64] fp32; block 0 holds the initial
+// state).  The backward walks the blocks last to first; for each block it
+// recomputes the forward of sub-chunks of KS steps from the block's
+// checkpoint, holding S_{t-1} and sa_t of the sub-chunk in registers, and
+// then runs the reverse recurrence over the sub-chunk.
 //
 // The reference's RWKV-7 code was deleted
 // (benchmarks/results/optimizer_wkv_experiments_5090.md:3); the output
@@ -19,107 +42,571 @@
 #include "wkv_common.h"
 
 namespace wkv {
+namespace w7 {
 
-template <typename E, int NT>
-__global__ __launch_bounds__(64 * NT) void wkv7_fwd_kernel(
-    const typename E::raw* __restrict__ r, const typename E::raw* __restrict__ w,
-    const typename E::raw* __restrict__ k, const typename E::raw* __restrict__ v,
-    const typename E::raw* __restrict__ a, const typename E::raw* __restrict__ b,
-    const float* __restrict__ s0, typename E::raw* __restrict__ y, float* __restrict__ s_out,
-    int T, int H) {
-  constexpr int N = 64;
-  constexpr int CPT = N / NT;
+constexpr int kN = 64;          // head size
+constexpr int kThreads = 256;   // threads per (batch, head)
+constexpr int kKC = 16;         // steps per staged block / checkpoint
+constexpr int kKS = 8;          // steps per backward sub-chunk (registers)
+constexpr int kNSub = kKC / kKS;
+
+__device__ __forceinline__ float as_f(unsigned u) { return __uint_as_float(u); }
+__device__ __forceinline__ unsigned as_u(float f) { return __float_as_uint(f); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the
+// same bits (each step adds a value and its mirror partner, which commute):
+// xor 1, xor 2 (quad permutes), then half-row mirror and row mirror.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+// Sums four per-lane values over the wave's four 16-lane rows.  Row r of the
+// result holds the total of value r.  v_permlane32_swap exchanges the upper
+// half of its first operand with the lower half of its second;
+// v_permlane16_swap exchanges the odd rows of the first with the even rows
+// of the second.
+__device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v3) {
+  // rows of s1: [v0_0+v0_2, v0_1+v0_3, v2_0+v2_2, v2_1+v2_3]
+  const auto p = __builtin_amdgcn_permlane32_swap(as_u(v0), as_u(v2), false, false);
+  const float s1 = as_f(p[0]) + as_f(p[1]);
+  // rows of s2: likewise for v1, v3
+  const auto q = __builtin_amdgcn_permlane32_swap(as_u(v1), as_u(v3), false, false);
+  const float s2 = as_f(q[0]) + as_f(q[1]);
+  // row 0: s1_0 + s1_1 = sum v0; row 1: s2_0 + s2_1 = sum v1;
+  // row 2: s1_2 + s1_3 = sum v2; row 3: s2_2 + s2_3 = sum v3
+  const auto r = __builtin_amdgcn_permlane16_swap(as_u(s1), as_u(s2), false, false);
+  return as_f(r[0]) + as_f(r[1]);
+}
+
+template <typename E, int NV>
+struct Vecs {
+  const typename E::raw* p[NV];
+  __device__ __forceinline__ const typename E::raw* pick(int q) const {
+    const typename E::raw* r = p[0];
+#pragma unroll
+    for (int i = 1; i < NV; ++i) r = (q == i) ? p[i] : r;
+    return r;
+  }
+};
+
+// Loads KC steps of NV step vectors of one (batch, head) in 16-byte pieces
+// into registers, then writes them to LDS as fp32 [NV][KC][64].  Steps past
+// the end re-read step T-1 (never used).
+template <typename E, int NV>
+struct Stager {
   using raw = typename E::raw;
-  __shared__ float vec[2][6][N];  // r, w, k, v, a, b
+  static constexpr int EPP = 16 / int(sizeof(raw));  // elements per piece
+  static constexpr int PPV = kN / EPP;               // pieces per step vector
+  static constexpr int NP = NV * kKC * PPV;
+  static constexpr int PPT = (NP + kThreads - 1) / kThreads;
+  uint4 buf[PPT];
 
+  __device__ __forceinline__ void load(const Vecs<E, NV>& src, int bi, int h, int t0, int T,
+                                       int H) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = int(threadIdx.x) + k * kThreads;
+      if (NP % kThreads == 0 || p < NP) {
+        const int q = p / (kKC * PPV);
+        const int rem = p - q * (kKC * PPV);
+        const int s = rem / PPV;
+        const int pc = rem - s * PPV;
+        const int t = min(t0 + s, T - 1);
+        const raw* base = src.pick(q) + ((size_t(bi) * T + t) * H + h) * kN + pc * EPP;
+        buf[k] = *reinterpret_cast<const uint4*>(base);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(float* lds) const {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = int(threadIdx.x) + k * kThreads;
+      if (NP % kThreads == 0 || p < NP) {
+        const int q = p / (kKC * PPV);
+        const int rem = p - q * (kKC * PPV);
+        const int s = rem / PPV;
+        const int pc = rem - s * PPV;
+        float* dst = lds + (q * kKC + s) * kN + pc * EPP;
+        const uint32_t w[4] = {buf[k].x, buf[k].y, buf[k].z, buf[k].w};
+        if constexpr (EPP == 4) {
+          *reinterpret_cast<float4*>(dst) =
+              make_float4(as_f(w[0]), as_f(w[1]), as_f(w[2]), as_f(w[3]));
+        } else {
+          float f[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (__is_same(E, BF16)) {
+              f[2 * e] = __uint_as_float(w[e] << 16);
+              f[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+            } else {
+              f[2 * e] = f16_bits_to_float(w[e] & 0xffffu);
+              f[2 * e + 1] = f16_bits_to_float(w[e] >> 16);
+            }
+          }
+          *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+          *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+        }
+      }
+    }
+  }
+};
+
+// Index of each step vector in the staged block.
+enum { QR = 0, QW = 1, QK = 2, QV = 3, QA = 4, QB = 5, QDY = 6 };
+
+__device__ __forceinline__ float4 lds4(const float* stage, int q, int s, int j) {
+  return *reinterpret_cast<const float4*>(stage + (q * kKC + s) * kN + j);
+}
+
+struct Lane {
+  int wv, rg, cg, i0, j0;
+  __device__ __forceinline__ Lane() {
+    wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int lane = int(threadIdx.x) & 63;
+    rg = lane >> 4;
+    cg = lane & 15;
+    i0 = 16 * wv + 4 * rg;
+    j0 = 4 * cg;
+  }
+};
+
+// One forward step on the lane's 4x4 block: returns sa (S_{t-1} a) per row
+// and advances S.  The same code runs in the forward kernel and in the
+// backward's recomputation, so both produce the same state bits.
+__device__ __forceinline__ void fwd_step(float (&S)[4][4], const float* stage, int s,
+                                         const Lane& L, float (&sa)[4]) {
+  const float4 a4 = lds4(stage, QA, s, L.j0);
+  const float4 w4 = lds4(stage, QW, s, L.j0);
+  const float4 b4 = lds4(stage, QB, s, L.j0);
+  const float4 k4 = lds4(stage, QK, s, L.j0);
+  const float4 v4 = lds4(stage, QV, s, L.i0);
+  const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+  const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+  const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+  const float k[4] = {k4.x, k4.y, k4.z, k4.w};
+  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float x = S[r][0] * a[0];
+#pragma unroll
+    for (int c = 1; c < 4; ++c) x = fmaf(S[r][c], a[c], x);
+    sa[r] = x;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sa[r] = row16_sum(sa[r]);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) S[r][c] = fmaf(S[r][c], w[c], fmaf(sa[r], b[c], v[r] * k[c]));
+}
+
+__device__ __forceinline__ size_t state_off(int bh, int i, int j) {
+  return (size_t(bh) * kN + i) * kN + j;
+}
+
+__device__ __forceinline__ void load_state(float (&S)[4][4], const float* src, const Lane& L) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float4 x = *reinterpret_cast<const float4*>(src + (L.i0 + r) * kN + L.j0);
+    S[r][0] = x.x; S[r][1] = x.y; S[r][2] = x.z; S[r][3] = x.w;
+  }
+}
+
+__device__ __forceinline__ void store_state(float* dst, const float (&S)[4][4], const Lane& L) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *reinterpret_cast<float4*>(dst + (L.i0 + r) * kN + L.j0) =
+        make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
+}
+
+// Writes rows [n][64] of fp32 LDS data to out[(bi, t0 + s, h, :)] in the
+// element type, 16 bytes per thread-iteration.
+template <typename E>
+__device__ __forceinline__ void store_steps(typename E::raw* out, const float* buf, int bi, int h,
+                                            int t0, int n, int T, int H) {
+  constexpr int EPP = 16 / int(sizeof(typename E::raw));
+  constexpr int PPV = kN / EPP;
+  for (int p = int(threadIdx.x); p < n * PPV; p += kThreads) {
+    const int s = p / PPV;
+    const int pc = p - s * PPV;
+    const float* src = buf + s * kN + pc * EPP;
+    float f[EPP];
+#pragma unroll
+    for (int e = 0; e < EPP; e += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(src + e);
+      f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
+    }
+    typename E::raw* dst = out + ((size_t(bi) * T + t0 + s) * H + h) * kN + pc * EPP;
+    if constexpr (EPP == 4) {
+      *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+    } else {
+      OutPack<E, 8> o;
+      o.set(f);
+      *reinterpret_cast<uint4*>(dst) = make_uint4(o.u[0], o.u[1], o.u[2], o.u[3]);
+    }
+  }
+}
+
+}  // namespace w7
+
+// ------------------------------------------------------------- forward ----
+// One workgroup per (batch, head).  ck (optional): state at the start of
+// every kKC-step block, [B*H][ceil(T/kKC)][64][64].  y may be null (records
+// only).
+template <typename E>
+__global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
+    w7::Vecs<E, 6> in, const float* __restrict__ s0, typename E::raw* __restrict__ y,
+    float* __restrict__ s_out, float* __restrict__ ck, int T, int H) {
+  using namespace w7;
+  __shared__ float stage[2][6 * kKC * kN];
+  __shared__ float ybuf[2][kKC * kN];
   const int bh = blockIdx.x;
   const int bi = bh / H;
   const int h = bh - bi * H;
-  const int tid = threadIdx.x;
-  const int row = tid / NT;
-  const int part = tid - row * NT;
-  const int j0 = part * CPT;
-  const raw* src[6] = {r, w, k, v, a, b};
+  const Lane L;
 
-  float S[CPT];
-  const size_t sbase = (size_t(bh) * N + row) * N + j0;
+  float S[4][4];
+  if (s0) {
+    load_state(S, s0 + state_off(bh, 0, 0), L);
+  } else {
 #pragma unroll
-  for (int j = 0; j < CPT; ++j) S[j] = s0 ? s0[sbase + j] : 0.f;
-
-  auto step_base = [&](int t) { return ((size_t(bi) * T + t) * H + h) * N; };
-  const int which = tid / N;
-  const int idx = tid - which * N;
-  const bool loader = tid < 6 * N;
-  if (loader && T > 0) vec[0][which][idx] = load_scalar<E>(src[which] + step_base(0) + idx);
-  __syncthreads();
-
-  for (int t = 0; t < T; ++t) {
-    const int cur = t & 1;
-    float nxt = 0.f;
-    if (loader && t + 1 < T) nxt = load_scalar<E>(src[which] + step_base(t + 1) + idx);
-
-    float rj[CPT], wj[CPT], kj[CPT], aj[CPT], bj[CPT];
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      rj[j] = vec[cur][0][j0 + j];
-      wj[j] = vec[cur][1][j0 + j];
-      kj[j] = vec[cur][2][j0 + j];
-      aj[j] = vec[cur][4][j0 + j];
-      bj[j] = vec[cur][5][j0 + j];
-    }
-    const float vi = vec[cur][3][row];
-
-    float sa = 0.f;
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) sa = fmaf(S[j], aj[j], sa);
-#pragma unroll
-    for (int m = 1; m < NT; m <<= 1) sa += __shfl_xor(sa, m, NT);
-
-    float yp = 0.f;
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      S[j] = fmaf(S[j], wj[j], fmaf(sa, bj[j], vi * kj[j]));
-      yp = fmaf(S[j], rj[j], yp);
-    }
-#pragma unroll
-    for (int m = 1; m < NT; m <<= 1) yp += __shfl_xor(yp, m, NT);
-    if (part == 0) store_scalar<E>(y + step_base(t) + row, yp);
-
-    if (loader && t + 1 < T) vec[cur ^ 1][which][idx] = nxt;
+      for (int c = 0; c < 4; ++c) S[r][c] = 0.f;
+  }
+  const int nblk = (T + kKC - 1) / kKC;
+  Stager<E, 6> st;
+  if (nblk > 0) {
+    st.load(in, bi, h, 0, T, H);
+    st.store(stage[0]);
     __syncthreads();
   }
-  if (s_out) {
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int t0 = blk * kKC;
+    const int n = min(kKC, T - t0);
+    if (ck) store_state(ck + (size_t(bh) * nblk + blk) * kN * kN, S, L);
+    if (blk + 1 < nblk) st.load(in, bi, h, t0 + kKC, T, H);
+    const float* sg = stage[blk & 1];
+    float* yb = ybuf[blk & 1];
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) s_out[sbase + j] = S[j];
+    for (int s = 0; s < kKC; ++s) {
+      if (s < n) {
+        float sa[4];
+        fwd_step(S, sg, s, L, sa);
+        const float4 r4 = lds4(sg, QR, s, L.j0);
+        const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+        float yr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = S[r][0] * rr[0];
+#pragma unroll
+          for (int c = 1; c < 4; ++c) x = fmaf(S[r][c], rr[c], x);
+          yr[r] = row16_sum(x);
+        }
+        if (L.cg == 0)
+          *reinterpret_cast<float4*>(yb + s * kN + L.i0) = make_float4(yr[0], yr[1], yr[2], yr[3]);
+      }
+    }
+    if (blk + 1 < nblk) st.store(stage[(blk + 1) & 1]);
+    __syncthreads();
+    if (y) store_steps<E>(y, yb, bi, h, t0, n, T, H);
   }
+  if (s_out) store_state(s_out + state_off(bh, 0, 0), S, L);
+}
+
+// ------------------------------------------------------------ backward ----
+namespace w7 {
+
+struct BwdSmem {
+  float stage[2][7 * kKC * kN];
+  // Per sub-chunk step: per-wave partial sums over the wave's 16 rows of the
+  // five key-indexed gradients (dr, dk, dw, da, db), and dv.
+  float red[kKS][4][5][kN];
+  float dvb[kKS][kN];
+};
+
+// Recompute + reverse over one sub-chunk of cnt steps starting at staged
+// step sl (FULL: cnt == kKS, no per-step guards).  Leaves the per-step
+// partial sums in sm.red / sm.dvb and advances G to before the sub-chunk.
+template <bool FULL>
+__device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const float* ckb,
+                                             int sl, int cnt, const Lane& L, float (&G)[4][4]) {
+  constexpr int KS = kKS;
+  const int col = L.j0 + L.rg;  // column this lane holds after rows4_sum
+  float S[4][4];
+  load_state(S, ckb, L);
+  float sa[4];
+#pragma unroll 1
+  for (int s = 0; s < sl; ++s) fwd_step(S, sg, s, L, sa);
+  // Recompute the sub-chunk keeping S_{t-1} and sa_t.
+  float Sp[KS][4][4], sas[KS][4];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (FULL || s < cnt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) Sp[s][r][c] = S[r][c];
+      fwd_step(S, sg, sl + s, L, sas[s]);
+    }
+  }
+  // Reverse; St holds the post-update state of step s (S_t).
+  float St[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) St[r][c] = S[r][c];
+#pragma unroll
+  for (int s = KS - 1; s >= 0; --s) {
+    if (FULL || s < cnt) {
+      const int ss = sl + s;
+      const float4 r4 = lds4(sg, QR, ss, L.j0);
+      const float4 w4 = lds4(sg, QW, ss, L.j0);
+      const float4 k4 = lds4(sg, QK, ss, L.j0);
+      const float4 a4 = lds4(sg, QA, ss, L.j0);
+      const float4 b4 = lds4(sg, QB, ss, L.j0);
+      const float4 v4 = lds4(sg, QV, ss, L.i0);
+      const float4 g4 = lds4(sg, QDY, ss, L.i0);
+      const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+      const float ww[4] = {w4.x, w4.y, w4.z, w4.w};
+      const float kk[4] = {k4.x, k4.y, k4.z, k4.w};
+      const float aa[4] = {a4.x, a4.y, a4.z, a4.w};
+      const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+      const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+      const float gy[4] = {g4.x, g4.y, g4.z, g4.w};
+      float pr[4], pk[4], pw[4], pa[4], pb[4], dvr[4], cc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float x = St[0][c] * gy[0];
+#pragma unroll
+        for (int r = 1; r < 4; ++r) x = fmaf(St[r][c], gy[r], x);
+        pr[c] = x;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) G[r][c] = fmaf(gy[r], rr[c], G[r][c]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = G[r][0] * kk[0], z = G[r][0] * bb[0];
+#pragma unroll
+        for (int c = 1; c < 4; ++c) {
+          x = fmaf(G[r][c], kk[c], x);
+          z = fmaf(G[r][c], bb[c], z);
+        }
+        dvr[r] = x;
+        cc[r] = z;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dvr[r] = row16_sum(dvr[r]);
+        cc[r] = row16_sum(cc[r]);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float xk = G[0][c] * vv[0], xw = G[0][c] * Sp[s][0][c];
+        float xa = Sp[s][0][c] * cc[0], xb = G[0][c] * sas[s][0];
+#pragma unroll
+        for (int r = 1; r < 4; ++r) {
+          xk = fmaf(G[r][c], vv[r], xk);
+          xw = fmaf(G[r][c], Sp[s][r][c], xw);
+          xa = fmaf(Sp[s][r][c], cc[r], xa);
+          xb = fmaf(G[r][c], sas[s][r], xb);
+        }
+        pk[c] = xk; pw[c] = xw; pa[c] = xa; pb[c] = xb;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) G[r][c] = fmaf(G[r][c], ww[c], cc[r] * aa[c]);
+      float* rs = &sm.red[s][L.wv][0][0];
+      rs[0 * kN + col] = rows4_sum(pr[0], pr[1], pr[2], pr[3]);
+      rs[1 * kN + col] = rows4_sum(pk[0], pk[1], pk[2], pk[3]);
+      rs[2 * kN + col] = rows4_sum(pw[0], pw[1], pw[2], pw[3]);
+      rs[3 * kN + col] = rows4_sum(pa[0], pa[1], pa[2], pa[3]);
+      rs[4 * kN + col] = rows4_sum(pb[0], pb[1], pb[2], pb[3]);
+      if (L.cg == 0)
+        *reinterpret_cast<float4*>(&sm.dvb[s][L.i0]) = make_float4(dvr[0], dvr[1], dvr[2], dvr[3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) St[r][c] = Sp[s][r][c];
+    }
+  }
+}
+
+}  // namespace w7
+
+// One workgroup per (batch, head); blocks of kKC steps last to first, each
+// in sub-chunks of kKS steps (last to first) recomputed from the block's
+// checkpoint.  ds_T (optional): gradient of the final state; ds0 (optional):
+// gradient of the initial state.
+template <typename E>
+__global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
+    w7::Vecs<E, 7> in, const float* __restrict__ ck, const float* __restrict__ ds_T,
+    typename E::raw* __restrict__ dr, typename E::raw* __restrict__ dw,
+    typename E::raw* __restrict__ dk, typename E::raw* __restrict__ dv,
+    typename E::raw* __restrict__ da, typename E::raw* __restrict__ db, float* __restrict__ ds0,
+    int T, int H) {
+  using namespace w7;
+  __shared__ BwdSmem sm;
+  const int bh = blockIdx.x;
+  const int bi = bh / H;
+  const int h = bh - bi * H;
+  const Lane L;
+
+  float G[4][4];
+  if (ds_T) {
+    load_state(G, ds_T + state_off(bh, 0, 0), L);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) G[r][c] = 0.f;
+  }
+  const int nblk = (T + kKC - 1) / kKC;
+  Stager<E, 7> st;
+  if (nblk > 0) {
+    st.load(in, bi, h, (nblk - 1) * kKC, T, H);
+    st.store(sm.stage[(nblk - 1) & 1]);
+    __syncthreads();
+  }
+  for (int blk = nblk - 1; blk >= 0; --blk) {
+    const int t0 = blk * kKC;
+    const int n = min(kKC, T - t0);
+    if (blk > 0) st.load(in, bi, h, t0 - kKC, T, H);
+    const float* sg = sm.stage[blk & 1];
+    const float* ckb = ck + (size_t(bh) * nblk + blk) * kN * kN;
+#pragma unroll 1
+    for (int m = kNSub - 1; m >= 0; --m) {
+      const int sl = m * kKS;
+      if (sl >= n) continue;
+      const int cnt = min(kKS, n - sl);
+      if (cnt == kKS) {
+        bwd_subchunk<true>(sm, sg, ckb, sl, cnt, L, G);
+      } else {
+        bwd_subchunk<false>(sm, sg, ckb, sl, cnt, L, G);
+      }
+      __syncthreads();
+      // Sum the four waves' partials and store the sub-chunk's gradients.
+      constexpr int EPP = 16 / int(sizeof(typename E::raw));
+      constexpr int PPV = kN / EPP;
+      for (int p = int(threadIdx.x); p < 6 * cnt * PPV; p += kThreads) {
+        const int q = p / (cnt * PPV);
+        const int rem = p - q * (cnt * PPV);
+        const int s = rem / PPV;
+        const int pc = rem - s * PPV;
+        float f[EPP];
+#pragma unroll
+        for (int e = 0; e < EPP; e += 4) {
+          float4 x;
+          if (q < 5) {
+            x = *reinterpret_cast<const float4*>(&sm.red[s][0][q][pc * EPP + e]);
+#pragma unroll
+            for (int wv = 1; wv < 4; ++wv) {
+              const float4 z = *reinterpret_cast<const float4*>(&sm.red[s][wv][q][pc * EPP + e]);
+              x.x += z.x; x.y += z.y; x.z += z.z; x.w += z.w;
+            }
+          } else {
+            x = *reinterpret_cast<const float4*>(&sm.dvb[s][pc * EPP + e]);
+          }
+          f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
+        }
+        typename E::raw* o = q == 0 ? dr : q == 1 ? dk : q == 2 ? dw : q == 3 ? da : q == 4 ? db : dv;
+        typename E::raw* dst = o + ((size_t(bi) * T + t0 + sl + s) * H + h) * kN + pc * EPP;
+        if constexpr (EPP == 4) {
+          *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+        } else {
+          OutPack<E, 8> o8;
+          o8.set(f);
+          *reinterpret_cast<uint4*>(dst) = make_uint4(o8.u[0], o8.u[1], o8.u[2], o8.u[3]);
+        }
+      }
+      __syncthreads();
+    }
+    if (blk > 0) {
+      st.store(sm.stage[(blk - 1) & 1]);
+      __syncthreads();
+    }
+  }
+  if (ds0) store_state(ds0 + state_off(bh, 0, 0), G, L);
 }
 
 }  // namespace wkv
 
 namespace wkv_host {
 
+size_t wkv7_checkpoint_floats(int64_t B, int64_t T, int64_t H) {
+  return size_t(B) * size_t(H) * size_t((T + wkv::w7::kKC - 1) / wkv::w7::kKC) * 64 * 64;
+}
+
 template <typename E>
-static int launch_wkv7(const void* r, const void* w, const void* k, const void* v, const void* a,
-                       const void* b, const float* s0, void* y, float* s_out, int B, int T,
-                       int H, hipStream_t stream) {
+static int launch_wkv7_fwd(const void* r, const void* w, const void* k, const void* v,
+                           const void* a, const void* b, const float* s0, void* y, float* s_out,
+                           float* ck, int B, int T, int H, hipStream_t stream) {
   using raw = typename E::raw;
-  constexpr int NT = 16;
-  hipLaunchKernelGGL((wkv::wkv7_fwd_kernel<E, NT>), dim3(unsigned(B) * H), dim3(64 * NT), 0,
-                     stream, static_cast<const raw*>(r), static_cast<const raw*>(w),
-                     static_cast<const raw*>(k), static_cast<const raw*>(v),
-                     static_cast<const raw*>(a), static_cast<const raw*>(b), s0,
-                     static_cast<raw*>(y), s_out, T, H);
+  wkv::w7::Vecs<E, 6> in{{static_cast<const raw*>(r), static_cast<const raw*>(w),
+                          static_cast<const raw*>(k), static_cast<const raw*>(v),
+                          static_cast<const raw*>(a), static_cast<const raw*>(b)}};
+  hipLaunchKernelGGL((wkv::wkv7_fwd_kernel<E>), dim3(unsigned(B) * H), dim3(wkv::w7::kThreads), 0,
+                     stream, in, s0, static_cast<raw*>(y), s_out, ck, T, H);
   return check_launch("wkv7_fwd_kernel");
 }
 
 int wkv7_forward_impl(const void* r, const void* w, const void* k, const void* v, const void* a,
-                      const void* b, const float* s0, void* y, float* s_out, int B, int T, int H,
-                      int dtype, hipStream_t stream) {
+                      const void* b, const float* s0, void* y, float* s_out, float* ck, int B,
+                      int T, int H, int dtype, hipStream_t stream) {
   switch (dtype) {
-    case 0: return launch_wkv7<wkv::F32>(r, w, k, v, a, b, s0, y, s_out, B, T, H, stream);
-    case 1: return launch_wkv7<wkv::BF16>(r, w, k, v, a, b, s0, y, s_out, B, T, H, stream);
-    case 2: return launch_wkv7<wkv::F16>(r, w, k, v, a, b, s0, y, s_out, B, T, H, stream);
+    case 0: return launch_wkv7_fwd<wkv::F32>(r, w, k, v, a, b, s0, y, s_out, ck, B, T, H, stream);
+    case 1: return launch_wkv7_fwd<wkv::BF16>(r, w, k, v, a, b, s0, y, s_out, ck, B, T, H, stream);
+    case 2: return launch_wkv7_fwd<wkv::F16>(r, w, k, v, a, b, s0, y, s_out, ck, B, T, H, stream);
     default: return fail(1, "wkv7_forward: unknown dtype");
+  }
+}
+
+template <typename E>
+static int launch_wkv7_bwd(const void* r, const void* w, const void* k, const void* v,
+                           const void* a, const void* b, const void* dy, const float* ck,
+                           const float* ds_T, void* dr, void* dw, void* dk, void* dv, void* da,
+                           void* db, float* ds0, int B, int T, int H, hipStream_t stream) {
+  using raw = typename E::raw;
+  wkv::w7::Vecs<E, 7> in{{static_cast<const raw*>(r), static_cast<const raw*>(w),
+                          static_cast<const raw*>(k), static_cast<const raw*>(v),
+                          static_cast<const raw*>(a), static_cast<const raw*>(b),
+                          static_cast<const raw*>(dy)}};
+  hipLaunchKernelGGL((wkv::wkv7_bwd_kernel<E>), dim3(unsigned(B) * H), dim3(wkv::w7::kThreads), 0,
+                     stream, in, ck, ds_T, static_cast<raw*>(dr), static_cast<raw*>(dw),
+                     static_cast<raw*>(dk), static_cast<raw*>(dv), static_cast<raw*>(da),
+                     static_cast<raw*>(db), ds0, T, H);
+  return check_launch("wkv7_bwd_kernel");
+}
+
+int wkv7_backward_ck_impl(const void* r, const void* w, const void* k, const void* v,
+                          const void* a, const void* b, const void* dy, const float* ck,
+                          const float* ds_T, void* dr, void* dw, void* dk, void* dv, void* da,
+                          void* db, float* ds0, int B, int T, int H, int dtype,
+                          hipStream_t stream) {
+  switch (dtype) {
+    case 0:
+      return launch_wkv7_bwd<wkv::F32>(r, w, k, v, a, b, dy, ck, ds_T, dr, dw, dk, dv, da, db,
+                                       ds0, B, T, H, stream);
+    case 1:
+      return launch_wkv7_bwd<wkv::BF16>(r, w, k, v, a, b, dy, ck, ds_T, dr, dw, dk, dv, da, db,
+                                        ds0, B, T, H, stream);
+    case 2:
+      return launch_wkv7_bwd<wkv::F16>(r, w, k, v, a, b, dy, ck, ds_T, dr, dw, dk, dv, da, db,
+                                       ds0, B, T, H, stream);
+    default: return fail(1, "wkv7_backward: unknown dtype");
   }
 }
 

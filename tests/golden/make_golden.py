@@ -44,7 +44,10 @@ def wkv7_cases():
     cases = {}
     r, w, k, v, a, b = wkv7.make_inputs(1, 12, 2, 64, seed=3, dtype=torch.float64)
     y, s = wkv7.wkv7_loop(r, w, k, v, a, b)
-    for key, val in dict(r=r, w=w, k=k, v=v, a=a, b=b, y=y, s=s).items():
+    gy = torch.randn(y.shape, generator=torch.Generator().manual_seed(4), dtype=torch.float64)
+    _, _, dr, dw, dk, dv, da, db, _ = wkv7.wkv7_autograd_grads(r, w, k, v, a, b, None, gy)
+    fields = dict(r=r, w=w, k=k, v=v, a=a, b=b, y=y, s=s, gy=gy, dr=dr, dw=dw, dk=dk, dv=dv, da=da, db=db)
+    for key, val in fields.items():
         cases[f"b1t12h2__{key}"] = val.numpy()
     return cases
 

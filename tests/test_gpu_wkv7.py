@@ -1,0 +1,164 @@
+"""GPU parity of the RWKV-7 DPLR forward and backward against the float64 oracle.
+
+The HIP path is called through the ``myelin::`` ops (autograd and the
+standalone backward) and through the C ABI; expected values come from torch
+autograd through the oracle's sequential loop (itself pinned by finite
+differences and an independent reverse recurrence on the CPU).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import wkv7 as O7
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+NAMES = ("dr", "dw", "dk", "dv", "da", "db")
+
+
+def _ops():
+    import spikegpt_myelin_amd  # noqa: F401
+
+    return torch.ops.myelin
+
+
+def _case(b, t, h, seed, dtype, with_state):
+    xs = O7.make_inputs(b, t, h, 64, seed=seed, dtype=dtype)
+    g = torch.Generator().manual_seed(1000 + seed)
+    s0 = 0.5 * torch.randn(b, h, 64, 64, generator=g) if with_state else None
+    gy = torch.randn(b, t, h, 64, generator=g).to(dtype)
+    gs = torch.randn(b, h, 64, 64, generator=g) if with_state else None
+    return xs, s0, gy, gs
+
+
+def _tol(dtype):
+    # fp32 I/O: the kernel's fp32 state against fp64 over the sequence;
+    # 16-bit I/O: the documented 2e-2 relative / 1e-2 absolute bar, the
+    # absolute part scaled by the tensor's magnitude.
+    return (1e-4, 1e-4) if dtype == torch.float32 else (2e-2, 1e-2)
+
+
+def _close(got, exp, dtype, name):
+    rtol, atol = _tol(dtype)
+    got = got.detach().double().cpu()
+    scale = max(float(exp.abs().max()), 1e-30)
+    ok = torch.allclose(got, exp, rtol=rtol, atol=atol * scale)
+    err = float((got - exp).abs().max()) / scale
+    assert ok, f"{name}: max abs err / max|ref| = {err:.3e}"
+
+
+def _reference(xs, s0, gy, gs):
+    d = [x.double() for x in xs]
+    return O7.wkv7_autograd_grads(*d, None if s0 is None else s0.double(), gy.double(),
+                                  None if gs is None else gs.double())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("t", [1, 7, 16, 17, 40])
+def test_autograd_matches_oracle(dtype, t):
+    ops = _ops()
+    with_state = t in (17, 40)
+    xs, s0, gy, gs = _case(2, t, 3, seed=t, dtype=dtype, with_state=with_state)
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    sd = s0.to(DEV).requires_grad_(True) if with_state else None
+    y, s = ops.wkv7_forward(*leaves, sd)
+    outs = [y, s] if with_state else [y]
+    grads_in = [gy.to(DEV), gs.to(DEV)] if with_state else [gy.to(DEV)]
+    wrt = leaves + ([sd] if with_state else [])
+    got = torch.autograd.grad(outs, wrt, grads_in)
+    ref = _reference(xs, s0, gy, gs)
+    assert y.dtype == dtype and s.dtype == torch.float32
+    _close(y, ref[0], dtype, "y")
+    _close(s, ref[1], dtype, "s")
+    for name, g, e in zip(NAMES, got[:6], ref[2:8]):
+        assert g.dtype == dtype
+        _close(g, e, dtype, name)
+    if with_state:
+        _close(got[6], ref[8], dtype, "ds0")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_standalone_backward_matches_autograd_path(dtype):
+    ops = _ops()
+    xs, s0, gy, gs = _case(2, 33, 2, seed=11, dtype=dtype, with_state=True)
+    xd = [x.to(DEV) for x in xs]
+    out = ops.wkv7_backward(*xd, s0.to(DEV), gy.to(DEV), gs.to(DEV))
+    assert len(out) == 7
+    ref = _reference(xs, s0, gy, gs)
+    for name, g, e in zip((*NAMES, "ds0"), out, ref[2:]):
+        _close(g, e, dtype, name)
+    # no initial state, no final-state gradient: six gradients
+    out = ops.wkv7_backward(*xd, None, gy.to(DEV), None)
+    assert len(out) == 6
+    ref = _reference(xs, None, gy, None)
+    for name, g, e in zip(NAMES, out, ref[2:8]):
+        _close(g, e, dtype, name)
+
+
+def test_forward_without_checkpoints_equals_training_forward():
+    from spikegpt_myelin_amd.wkv7 import wkv7_forward_no_checkpoint
+
+    ops = _ops()
+    xs, s0, _, _ = _case(2, 37, 2, seed=12, dtype=torch.bfloat16, with_state=True)
+    xd = [x.to(DEV) for x in xs]
+    y1, s1 = wkv7_forward_no_checkpoint(*xd, s0.to(DEV))
+    y2, s2, ck = ops.wkv7_forward_train(*xd, s0.to(DEV))
+    assert torch.equal(y1, y2) and torch.equal(s1, s2)
+    # checkpoint 0 is the initial state, checkpoint j the state after 16 j steps
+    assert torch.equal(ck[:, :, 0], s0.to(DEV))
+    _, s16 = wkv7_forward_no_checkpoint(*(x[:, :16] for x in xd), s0.to(DEV))
+    assert torch.equal(ck[:, :, 1], s16)
+
+
+def test_deterministic():
+    ops = _ops()
+    xs, s0, gy, gs = _case(2, 29, 2, seed=13, dtype=torch.bfloat16, with_state=True)
+    xd = [x.to(DEV) for x in xs]
+    a = ops.wkv7_backward(*xd, s0.to(DEV), gy.to(DEV), gs.to(DEV))
+    b = ops.wkv7_backward(*xd, s0.to(DEV), gy.to(DEV), gs.to(DEV))
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_empty_sequence():
+    ops = _ops()
+    xs, s0, gy, gs = _case(2, 0, 2, seed=14, dtype=torch.float32, with_state=True)
+    xd = [x.to(DEV) for x in xs]
+    y, s = ops.wkv7_forward(*xd, s0.to(DEV))
+    assert y.shape == (2, 0, 2, 64) and torch.equal(s.cpu(), s0)
+    out = ops.wkv7_backward(*xd, s0.to(DEV), gy.to(DEV), gs.to(DEV))
+    assert all(g.shape == (2, 0, 2, 64) for g in out[:6])
+    assert torch.equal(out[6].cpu(), gs)
+
+
+def test_golden_fixture_gradients():
+    ops = _ops()
+    from pathlib import Path
+
+    data = np.load(Path(__file__).parent / "golden" / "wkv7_small.npz", allow_pickle=False)
+    g = {n.split("__")[1]: torch.from_numpy(data[n]) for n in data.files}
+    xs = [g[n].float().to(DEV) for n in ("r", "w", "k", "v", "a", "b")]
+    out = ops.wkv7_backward(*xs, None, g["gy"].float().to(DEV), None)
+    for name, got in zip(NAMES, out):
+        _close(got, g[name], torch.float32, name)
+
+
+def test_benchmark_shape_full_size():
+    # B=16, T=1024, H=12 bf16 (the RWKV-7 benchmark configuration): every
+    # (batch, head) is independent, so the first two batch rows are compared
+    # with the oracle run on those rows alone.
+    ops = _ops()
+    b, t, h = 16, 1024, 12
+    xs = O7.make_inputs(b, t, h, 64, seed=4, dtype=torch.bfloat16)
+    gy = torch.randn(b, t, h, 64, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    y, _ = ops.wkv7_forward(*leaves, None)
+    got = torch.autograd.grad(y, leaves, gy.to(DEV))
+    ref = _reference([x[:2] for x in xs], None, gy[:2], None)
+    _close(y[:2], ref[0], torch.bfloat16, "y")
+    for name, g_, e in zip(NAMES, got, ref[2:8]):
+        _close(g_[:2], e, torch.bfloat16, name)

@@ -63,3 +63,66 @@ def test_golden_fixture_reproduces():
     g = {n.split("__")[1]: torch.from_numpy(data[n]) for n in data.files}
     y, s = O7.wkv7_loop(*(g[n] for n in ("r", "w", "k", "v", "a", "b")))
     assert torch.allclose(y, g["y"], atol=1e-12) and torch.allclose(s, g["s"], atol=1e-12)
+    grads = O7.wkv7_backward_loop(*(g[n] for n in ("r", "w", "k", "v", "a", "b")), None, g["gy"])
+    for name, got in zip(("dr", "dw", "dk", "dv", "da", "db"), grads):
+        assert torch.allclose(got, g[name], atol=1e-11), name
+
+
+def _grad_case(seed, t=9, n=8):
+    xs = O7.make_inputs(2, t, 2, n, seed=seed, dtype=F64)
+    g = torch.Generator().manual_seed(100 + seed)
+    s0 = torch.randn(2, 2, n, n, generator=g, dtype=F64)
+    gy = torch.randn(2, t, 2, n, generator=g, dtype=F64)
+    gs = torch.randn(2, 2, n, n, generator=g, dtype=F64)
+    return xs, s0, gy, gs
+
+
+def test_explicit_reverse_recurrence_equals_autograd():
+    for seed in (5, 6):
+        xs, s0, gy, gs = _grad_case(seed)
+        auto = O7.wkv7_autograd_grads(*xs, s0, gy, gs)[2:]
+        loop = O7.wkv7_backward_loop(*xs, s0, gy, gs)
+        for name, x, y in zip(("dr", "dw", "dk", "dv", "da", "db", "ds0"), auto, loop):
+            assert torch.allclose(x, y, atol=1e-12, rtol=1e-12), name
+    # without an initial state or final-state gradient
+    xs, _, gy, _ = _grad_case(7)
+    auto = O7.wkv7_autograd_grads(*xs, None, gy)[2:8]
+    loop = O7.wkv7_backward_loop(*xs, None, gy)[:6]
+    for x, y in zip(auto, loop):
+        assert torch.allclose(x, y, atol=1e-12, rtol=1e-12)
+
+
+def test_autograd_of_every_input_matches_finite_differences():
+    xs, s0, gy, gs = _grad_case(8, t=4, n=4)
+    auto = O7.wkv7_autograd_grads(*xs, s0, gy, gs)[2:]
+
+    def loss(inputs, state):
+        y, s = O7.wkv7_loop(*inputs, state=state)
+        return float((y * gy).sum() + (s * gs).sum())
+
+    eps = 1e-6
+    for idx in range(7):
+        base = xs[idx] if idx < 6 else s0
+        fd = torch.zeros_like(base)
+        for j in range(base.numel()):
+            vals = []
+            for sgn in (1.0, -1.0):
+                pert = base.clone()
+                pert.reshape(-1)[j] += sgn * eps
+                ins = [pert if i == idx else x for i, x in enumerate(xs)]
+                vals.append(loss(ins, pert if idx == 6 else s0))
+            fd.reshape(-1)[j] = (vals[0] - vals[1]) / (2 * eps)
+        assert torch.allclose(auto[idx], fd, atol=1e-6, rtol=1e-5), idx
+
+
+def test_planted_transpose_in_the_reverse_recurrence_is_detected():
+    # Feeding the reverse recurrence a transposed G (the [value, key] vs
+    # [key, value] mix-up a kernel could make) must fail the comparison with
+    # autograd: the check has the power to see it.
+    xs, s0, gy, gs = _grad_case(9)
+    auto_dk = O7.wkv7_autograd_grads(*xs, s0, gy, gs)[4]
+    r, w, k, v, a, b = xs
+    _, _, dk, _, _, _, _ = O7.wkv7_backward_loop(r, w, k, v, a, b, s0, gy, gs)
+    assert torch.allclose(dk, auto_dk, atol=1e-12)
+    wrong = O7.wkv7_backward_loop(r, w, k, v, a, b, s0, gy, gs.transpose(-1, -2))[2]
+    assert not torch.allclose(wrong, auto_dk, atol=1e-6)
