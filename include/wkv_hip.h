@@ -49,11 +49,11 @@ enum wkv_status {
 int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
                  void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream);
 
-/* Bytes of the forward-state checkpoint records for these sizes: 5 fp32
+/* Bytes of the forward-state checkpoint records for these sizes: 3 fp32
  * per (batch, block of 64 steps, channel) -- the state (A, B) = 2^o (p, q)
- * at the block start and the block's largest and smallest k*log2(e), laid
- * out [5][B][ceil(T/64)][C].  They replace the reference's three [B,T,C] fp32
- * replay buffers (src/spikegpt/wkv_triton.py:170-172, wkv_bf16.py:167-169). */
+ * at the block start, laid out [3][B][ceil(T/64)][C].  They replace the
+ * reference's three [B,T,C] fp32 replay buffers
+ * (src/spikegpt/wkv_triton.py:170-172, wkv_bf16.py:167-169). */
 size_t wkv4_checkpoint_bytes(int64_t B, int64_t T, int64_t C);
 
 /* wkv4_forward that also writes the checkpoint records (y may be NULL to

@@ -19,10 +19,9 @@
 //
 // One reverse sweep (segments last to first; rows, chunks and segments as in
 // the forward kernel).  Per segment each wave:
-//   * takes the segment frame R (largest k*log2e over the segment's
-//     checkpoint blocks) and the forward state at the segment start from the
-//     records, prefetched with the segment's k, v, gy;
-//   * computes 2^{k log2e - R} and its chunk's forward summary; after one
+//   * takes the forward state at the segment start from the records,
+//     prefetched with the segment's k, v, gy;
+//   * computes 2^{k log2e} and its chunk's forward summary; after one
 //     barrier, an LDS Horner gives its chunk's forward carry;
 //   * recomputes the chunk's forward keeping z~ = gy/den~ and y in registers
 //     and reduces its chunk's reverse sums from a zero state; after a second
@@ -34,10 +33,12 @@
 // waves of the row into [B, C] partials that a second small kernel sums over
 // B in fixed order (deterministic).
 //
-// Reverse sums live in the segment frame: G~ = 2^R G, so that
-// e^{k_t} G_t = 2^{k_t log2e - R} G~_t and 2^R z_t = gy_t / den~_t.
-// Range guard as in the forward kernel; a rejected row is recomputed one
-// channel per thread with the reference's running-max recurrences.
+// All sums live in the forward kernel's fixed base-2 frame (e = 2^{k log2e},
+// state (A, B) = (p, q)), which is exact while the forward kernel's range
+// guard holds.  The forward kernel marks each row it recomputed with the
+// exact serial path (record o = -1e38 at block 0 instead of 0); such rows are
+// recomputed here one channel per thread with the reference's running-max
+// recurrences.
 #include "wkv_common.h"
 
 namespace wkv {
@@ -157,13 +158,12 @@ struct Bwd {
     float H[VEC][W][64];
     float Gp[VEC][W][64];
     float Hp[VEC][W][64];
-    float rcarry[2][5][VEC][64];  // reverse segment carry (R, G, H, G', H')
+    float rcarry[2][4][VEC][64];  // reverse segment carry (G, H, G', H')
   };
 
-  // The records a segment needs: state at its start and each block's range.
+  // Forward state at a segment's start.
   struct Recs {
-    float o[VEC], p[VEC], q[VEC];
-    float mx[BPS][VEC], mn[BPS][VEC];
+    float p[VEC], q[VEC];
   };
 
   // row_base and ck_row are wave-uniform (SGPRs), lane_boff and ck_boff the
@@ -172,11 +172,10 @@ struct Bwd {
   __device__ static __forceinline__ void load(const raw* __restrict__ k, const raw* __restrict__ v,
                                               const raw* __restrict__ g,
                                               const float* __restrict__ ck, size_t ck_row,
-                                              unsigned ck_boff, size_t ck_field, int seg, int nblk,
+                                              unsigned ck_boff, size_t ck_field, int seg,
                                               size_t row_base, unsigned lane_boff, int t0, int T,
-                                              int C,
-                                              PackT (&kb)[L], PackT (&vb)[L], PackT (&gb)[L],
-                                              Recs& rc) {
+                                              int C, PackT (&kb)[L], PackT (&vb)[L],
+                                              PackT (&gb)[L], Recs& rc) {
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const size_t step = row_base + size_t(min(t0 + i, T - 1)) * C;
@@ -186,59 +185,31 @@ struct Bwd {
     }
     const float* rec = ck + ck_row + size_t(seg) * BPS * C;
     Pack<F32, VEC> a;
-    a.load(byte_offset(rec + 0 * ck_field, ck_boff));
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) rc.o[c] = a.x[c];
     a.load(byte_offset(rec + 1 * ck_field, ck_boff));
 #pragma unroll
     for (int c = 0; c < VEC; ++c) rc.p[c] = a.x[c];
     a.load(byte_offset(rec + 2 * ck_field, ck_boff));
 #pragma unroll
     for (int c = 0; c < VEC; ++c) rc.q[c] = a.x[c];
-#pragma unroll
-    for (int j = 0; j < BPS; ++j) {
-      // Blocks past the end repeat the last one (its range is a valid bound).
-      const float* rj = ck + ck_row + size_t(min(seg * BPS + j, nblk - 1)) * C;
-      a.load(byte_offset(rj + 3 * ck_field, ck_boff));
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) rc.mx[j][c] = a.x[c];
-      a.load(byte_offset(rj + 4 * ck_field, ck_boff));
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) rc.mn[j][c] = a.x[c];
-    }
   }
 
   // One segment (visited last to first).  FULL: every step is inside the
-  // sequence.  Returns true when the range guard rejects the row
-  // (workgroup-uniform: every wave decides from the same records and LDS).
+  // sequence.
   template <bool FULL>
-  __device__ static __forceinline__ bool segment(
+  __device__ static __forceinline__ void segment(
       Smem& sm, int seg, int nseg, int T, int C, int wave, int lane, bool active, size_t row_base,
       unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
       const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC],
-      bool u_ok, raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC],
-      float (&gu)[VEC]) {
+      raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC], float (&gu)[VEC]) {
     const int t0 = (seg * W + wave) * L;
-    float R[VEC], P[VEC], Q[VEC];
-    bool bad = !u_ok;
+    float P[VEC], Q[VEC];
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      float r = rc.mx[0][c], lo = rc.mn[0][c];
-#pragma unroll
-      for (int j = 1; j < BPS; ++j) {
-        r = fmaxf(r, rc.mx[j][c]);
-        lo = fminf(lo, rc.mn[j][c]);
-      }
-      R[c] = r;
-      const float d = rc.o[c] - r;
-      bad |= (r - lo > kMaxSpread) || d > kMaxJump;
-      const float f = fast_exp2(d);
-      P[c] = rc.p[c] * f;
-      Q[c] = rc.q[c] * f;
+      P[c] = rc.p[c];
+      Q[c] = rc.q[c];
     }
-    if (__any(active && bad)) return true;
 
-    // e^{k-R} and this chunk's forward summary from a zero state.
+    // e^{k} and this chunk's forward summary from a zero state.
     float ek[L][VEC];
     float ps[VEC], qs[VEC];
 #pragma unroll
@@ -248,7 +219,7 @@ struct Bwd {
       const bool valid = FULL || (t0 + i) < T;
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        float e = fast_exp2(fmaf(kb[i].get(c), kLog2e, -R[c]));
+        float e = fast_exp2(kb[i].get(c) * kLog2e);
         if (!FULL) e = valid ? e : 0.f;
         ek[i][c] = e;
         ps[c] = fmaf(ps[c], D[c], e * vb[i].get(c));
@@ -268,7 +239,7 @@ struct Bwd {
         Q[c] = fmaf(Q[c], DL[c], sm.q[c][w][lane]);
       }
     }
-    // Forward recompute: keep z~ = gy/den~ and z~ y (zero past the end).
+    // Forward recompute: keep z = gy/den and z y (zero past the end).
     float zz[L][VEC], zy[L][VEC];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
@@ -309,25 +280,17 @@ struct Bwd {
       sm.Hp[c][wave][lane] = Hp[c];
     }
     __syncthreads();
-    // Carry at this chunk's end: the later segment's carry (converted to this
-    // frame), then the later chunks of this segment, nearest last.
-    bool bad2 = false;
+    // Carry at this chunk's end: the later segment's carry, then the later
+    // chunks of this segment, nearest last.
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      if (seg + 1 < nseg) {
-        const int sl = (seg + 1) & 1;
-        const float d = R[c] - sm.rcarry[sl][0][c][lane];
-        bad2 |= d > kMaxJump;
-        const float f = fast_exp2(d);
-        G[c] = sm.rcarry[sl][1][c][lane] * f;
-        H[c] = sm.rcarry[sl][2][c][lane] * f;
-        Gp[c] = sm.rcarry[sl][3][c][lane] * f;
-        Hp[c] = sm.rcarry[sl][4][c][lane] * f;
-      } else {
-        G[c] = 0.f; H[c] = 0.f; Gp[c] = 0.f; Hp[c] = 0.f;
-      }
+      const int sl = (seg + 1) & 1;
+      const bool later = seg + 1 < nseg;
+      G[c] = later ? sm.rcarry[sl][0][c][lane] : 0.f;
+      H[c] = later ? sm.rcarry[sl][1][c][lane] : 0.f;
+      Gp[c] = later ? sm.rcarry[sl][2][c][lane] : 0.f;
+      Hp[c] = later ? sm.rcarry[sl][3][c][lane] : 0.f;
     }
-    if (__any(active && bad2)) return true;
     for (int w = W - 1; w > wave; --w) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
@@ -377,14 +340,12 @@ struct Bwd {
       const int sl = seg & 1;
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        sm.rcarry[sl][0][c][lane] = R[c];
-        sm.rcarry[sl][1][c][lane] = G[c];
-        sm.rcarry[sl][2][c][lane] = H[c];
-        sm.rcarry[sl][3][c][lane] = Gp[c];
-        sm.rcarry[sl][4][c][lane] = Hp[c];
+        sm.rcarry[sl][0][c][lane] = G[c];
+        sm.rcarry[sl][1][c][lane] = H[c];
+        sm.rcarry[sl][2][c][lane] = Gp[c];
+        sm.rcarry[sl][3][c][lane] = Hp[c];
       }
     }
-    return false;
   }
 };
 
@@ -418,54 +379,59 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
   const unsigned ck_boff = active ? unsigned(lane * VEC * sizeof(float)) : 0u;
 
   float D[VEC], DL[VEC], U[VEC];
-  bool u_ok = true;
 #pragma unroll
   for (int c = 0; c < VEC; ++c) {
     const float dv = active ? decay[c0 + c] : 0.f;
     const float uv = active ? u_in[c0 + c] : 0.f;
     const float w2 = (decay_is_w ? dv : -expf(dv)) * kLog2e;
-    const float u2 = uv * kLog2e;
     D[c] = fast_exp2(w2);
     DL[c] = fast_exp2(w2 * float(L));
-    U[c] = fast_exp2(u2);
-    u_ok &= fabsf(u2) <= kMaxU;
+    U[c] = fast_exp2(uv * kLog2e);
   }
+  // Rows the forward kernel recomputed with its exact serial path carry
+  // o != 0 in their block-0 records; this row then takes the exact path too.
+  bool serial = false;
+  {
+    Pack<F32, VEC> o;
+    o.load(byte_offset(ck + ck_row, ck_boff));
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) serial |= active && o.x[c] != 0.f;
+  }
+  const bool bad = __syncthreads_or(serial) != 0;
 
   float gw[VEC], gu[VEC];
 #pragma unroll
   for (int c = 0; c < VEC; ++c) { gw[c] = 0.f; gu[c] = 0.f; }
-  bool bad = false;
-  {
+  if (!bad) {
     PackT kA[L], vA[L], gA[L], kB[L], vB[L], gB[L];
     typename F::Recs rA, rB;
     const int last = nseg - 1;
-    F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, last, nblk, row_base, lane_boff,
+    F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, last, row_base, lane_boff,
             last * F::SEG + wave * L, T, C, kA, vA, gA, rA);
     // The next segment is prefetched on every path (segment 0 prefetches
     // itself again, a cache hit), so that the wait before a segment's
     // arithmetic only covers the loads it consumes.
     for (int seg = last; seg >= 0; seg -= 2) {
       const int s1 = max(seg - 1, 0), s2 = max(seg - 2, 0);
-      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s1, nblk, row_base, lane_boff,
+      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s1, row_base, lane_boff,
               s1 * F::SEG + wave * L, T, C, kB, vB, gB, rB);
-      bad = seg < nfull
-                ? F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base,
-                                            lane_boff, kA, vA, gA, rA, D, DL, U, u_ok, gk, gv, gw,
-                                            gu)
-                : F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base,
-                                             lane_boff, kA, vA, gA, rA, D, DL, U, u_ok, gk, gv, gw,
-                                             gu);
-      if (bad || seg - 1 < 0) break;
-      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s2, nblk, row_base, lane_boff,
+      if (seg < nfull) {
+        F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base, lane_boff,
+                                  kA, vA, gA, rA, D, DL, U, gk, gv, gw, gu);
+      } else {
+        F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base, lane_boff,
+                                   kA, vA, gA, rA, D, DL, U, gk, gv, gw, gu);
+      }
+      if (seg - 1 < 0) break;
+      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s2, row_base, lane_boff,
               s2 * F::SEG + wave * L, T, C, kA, vA, gA, rA);
-      bad = seg - 1 < nfull
-                ? F::template segment<true>(sm, seg - 1, nseg, T, C, wave, lane, active,
-                                            row_base, lane_boff, kB, vB, gB, rB, D, DL, U, u_ok,
-                                            gk, gv, gw, gu)
-                : F::template segment<false>(sm, seg - 1, nseg, T, C, wave, lane, active,
-                                             row_base, lane_boff, kB, vB, gB, rB, D, DL, U, u_ok,
-                                             gk, gv, gw, gu);
-      if (bad) break;
+      if (seg - 1 < nfull) {
+        F::template segment<true>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
+                                  lane_boff, kB, vB, gB, rB, D, DL, U, gk, gv, gw, gu);
+      } else {
+        F::template segment<false>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
+                                   lane_boff, kB, vB, gB, rB, D, DL, U, gk, gv, gw, gu);
+      }
     }
   }
 
@@ -492,7 +458,6 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
       gu_part[size_t(b) * C + c] = su;
     }
   } else {
-    __syncthreads();
     for (int ch = threadIdx.x; ch < F::CPW; ch += blockDim.x) {
       const int c = cg * F::CPW + ch;
       if (c >= C) continue;
@@ -565,7 +530,8 @@ struct TileCfg { int vec, L, W; };
 // the 64-step checkpoint block.  Defaults: (2,8,8) for 16-bit tensors with
 // enough rows of 128 channels to fill the chip, else (1,16,8); the W=16
 // configurations are capped at 128 VGPRs and spill.
-static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}, {1, 8, 8}};
+static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}, {1, 8, 8},
+                                        {1, 16, 4}, {2, 16, 4}};
 
 int pick_vec(int64_t B, int64_t C);
 bool env_cfg(const char* name, int& vec, int& L, int& W);
@@ -624,6 +590,8 @@ static int dispatch_bwd(const void* gy, const float* decay, int decay_is_w, cons
   WKV_BWD_CASE(2, 4, 16)
   WKV_BWD_CASE(1, 16, 8)
   WKV_BWD_CASE(1, 8, 8)
+  WKV_BWD_CASE(1, 16, 4)
+  WKV_BWD_CASE(2, 16, 4)
 #undef WKV_BWD_CASE
   return fail(1, "wkv4_backward: no kernel for the selected tile configuration");
 }

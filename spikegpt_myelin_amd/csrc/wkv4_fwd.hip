@@ -15,32 +15,35 @@
 //   * time is cut into chunks of L steps; wave w handles chunk s*W + w of
 //     segment s, holding the chunk's k/v in registers (loaded one segment
 //     ahead, double-buffered);
-//   * all chunks of a segment share one base-2 reference frame R (the
-//     segment max of k*log2e, exchanged through LDS), so a chunk's state is
-//     (A, B) = 2^R (p, q) and joining chunks is linear: p <- p*e^{Lw} + p_j.
-//     The per-step work is one exp2 (2^{k log2e - R}) and one reciprocal per
-//     element, with no per-step max or select;
-//   * phase 1: every wave reduces its chunk to (p_j, q_j) from a zero state;
-//     after one barrier each wave folds the segment carry and its
-//     predecessors' summaries (Horner in LDS) into its own carry-in;
-//     phase 2: every wave re-runs its chunk from registers with that carry and
-//     writes y.  k and v are read from HBM exactly once and y written once.
+//   * exponents are kept in one fixed base-2 frame: the state is
+//     (A, B) = (p, q) directly and e_i = 2^{k_i log2e} needs no running max,
+//     which is exact arithmetic while |k log2e| <= 60 and |u log2e| <= 16 (see
+//     the range guard below); joining chunks is linear: p <- p*e^{Lw} + p_j.
+//     The per-step work is one exp2 and one reciprocal per element, with no
+//     per-step max or select;
+//   * phase 1: every wave reduces its chunk to (p_j, q_j) from a zero state
+//     and publishes it in LDS; after the segment's one barrier each wave folds
+//     the segment carry and its predecessors' summaries (Horner in LDS) into
+//     its own carry-in; phase 2: every wave re-runs its chunk from registers
+//     with that carry and writes y.  k and v are read from HBM exactly once
+//     and y written once.
 //
 // Checkpoints: with a checkpoint buffer the kernel also stores, at the start
-// of every block of 64 steps, the state in running-max form and the block's
-// key range: (o, p, q, max, min) with (A, B) = 2^o (p, q) and max/min the
-// extreme k*log2e of the block ([5][B][ceil(T/64)][C] fp32).  The backward
-// kernel recomputes the forward from these records instead of re-reading the
-// whole sequence; without y (y == nullptr) the kernel writes records only.
+// of every block of 64 steps, the state in running-max form (o, p, q) with
+// (A, B) = 2^o (p, q) ([3][B][ceil(T/64)][C] fp32).  Rows computed here have
+// o = 0 everywhere; rows recomputed by the exact serial path start from
+// o = -1e38 in block 0, which tells the backward kernel to take its own exact
+// path for them.  The backward recomputes the forward from these records
+// instead of re-reading the whole sequence; without y (y == nullptr) the
+// kernel writes records only.
 //
-// Range guard: the shared frame is exact arithmetic re-association, valid
-// while every quantity stays inside fp32's normal range.  Each segment checks
-// the spread between the frame and the smallest k*log2e it holds, the jump
-// between consecutive frames, and |u*log2e|.  Every wave derives the decision
-// from the same LDS data, so it is workgroup-uniform without another
-// barrier; a rejected row is recomputed by the reference's running-max
-// recurrence, one channel per thread.  Inputs whose keys stay inside +-30 (the
-// benchmark's clamp) never take that path.
+// Range guard: every element of a row must satisfy |k log2e| <= 60, and the
+// row's |u log2e| <= 16.  A wave that finds a key out of range sets a sticky
+// LDS flag before the segment's barrier; every wave reads it after the
+// barrier, so the decision is workgroup-uniform, and a rejected row is
+// recomputed by the reference's running-max recurrence, one channel per
+// thread.  Inputs whose keys stay inside +-30 (the benchmark's clamp) never
+// take that path.
 #include "wkv_common.h"
 
 namespace wkv {
@@ -55,16 +58,14 @@ struct Fwd {
   static_assert(kCkptBlock % L == 0 && SEG % kCkptBlock == 0, "segment/block layout");
 
   // [VEC][W][64]: lane index fastest, so every LDS access of a wave is one
-  // conflict-free row of 64 dwords.
-  // mx/mn are double-buffered by segment parity so that the waves writing
-  // checkpoint records can read their block's range after the second
-  // barrier without racing the next segment's writes.
+  // conflict-free row of 64 dwords.  The chunk summaries are double-buffered
+  // by segment parity: a wave may publish segment s+1's summary while a
+  // slower wave still folds segment s's.
   struct Smem {
-    float mx[2][VEC][W][64];
-    float mn[2][VEC][W][64];
-    float p[VEC][W][64];
-    float q[VEC][W][64];
-    float carry[2][3][VEC][64];  // (R, p, q) of the segment carry, by segment parity
+    float p[2][VEC][W][64];
+    float q[2][VEC][W][64];
+    float carry[2][2][VEC][64];  // (p, q) of the segment carry, by segment parity
+    int bad;                     // sticky: some key of the row is out of range
   };
 
   // row_base is wave-uniform (SGPRs); lane_boff is the lane's byte offset.
@@ -87,118 +88,66 @@ struct Fwd {
   __device__ static __forceinline__ bool segment(
       Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
       unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
-      unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L], const float (&D)[VEC],
-      const float (&DL)[VEC], const float (&U)[VEC], bool u_ok) {
+      unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L],
+      const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC]) {
     const int t0 = seg * SEG + wave * L;
-    // Phase 0: chunk range of k.
-    float s[L][VEC];
-    float m[VEC], n[VEC];
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) { m[c] = -kBig; n[c] = kBig; }
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const bool valid = FULL || (t0 + i) < T;
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        s[i][c] = kb[i].get(c);
-        m[c] = valid ? fmaxf(m[c], s[i][c]) : m[c];
-        n[c] = valid ? fminf(n[c], s[i][c]) : n[c];
-      }
-    }
     const int par = seg & 1;
+    // Phase 1: e = 2^{k log2e} and the chunk summary from a zero state.
+    float s[L][VEC];
+    float ps[VEC], qs[VEC], mk[VEC];
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      sm.mx[par][c][wave][lane] = m[c];
-      sm.mn[par][c][wave][lane] = n[c];
-    }
-    __syncthreads();
-
-    // Segment frame, the carry from the previous segment and the guard.
-    float R[VEC], pin[VEC], qin[VEC];
-    bool bad = !u_ok;
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      float r = -kBig, lo = kBig;
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        r = fmaxf(r, sm.mx[par][c][w][lane]);
-        lo = fminf(lo, sm.mn[par][c][w][lane]);
-      }
-      const bool any = r > -kBig;
-      R[c] = any ? r * kLog2e : 0.f;
-      bad |= any && (R[c] - lo * kLog2e > kMaxSpread);
-      if (seg > 0) {
-        const float d = sm.carry[(seg - 1) & 1][0][c][lane] - R[c];
-        bad |= active && d > kMaxJump;
-        const float f = fast_exp2(d);
-        pin[c] = sm.carry[(seg - 1) & 1][1][c][lane] * f;
-        qin[c] = sm.carry[(seg - 1) & 1][2][c][lane] * f;
-      } else {
-        pin[c] = 0.f;
-        qin[c] = 0.f;
-      }
-    }
-    // Identical LDS inputs in every wave: the wave vote is the workgroup's.
-    if (__any(active && bad)) return true;
-
-    // Phase 1: chunk summary from a zero state, in frame R.
-    float ps[VEC], qs[VEC];
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) { ps[c] = 0.f; qs[c] = 0.f; }
+    for (int c = 0; c < VEC; ++c) { ps[c] = 0.f; qs[c] = 0.f; mk[c] = 0.f; }
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const bool valid = FULL || (t0 + i) < T;
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        float e = fast_exp2(fmaf(s[i][c], kLog2e, -R[c]));
+        const float kk = kb[i].get(c);
+        mk[c] = fmaxf(mk[c], fabsf(kk));
+        float e = fast_exp2(kk * kLog2e);
         if (!FULL) e = valid ? e : 0.f;
         s[i][c] = e;
         ps[c] = fmaf(ps[c], D[c], e * vb[i].get(c));
         qs[c] = fmaf(qs[c], D[c], e);
       }
     }
+    bool bad = false;
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      sm.p[c][wave][lane] = ps[c];
-      sm.q[c][wave][lane] = qs[c];
+      bad |= mk[c] * kLog2e > kMaxK;
+      sm.p[par][c][wave][lane] = ps[c];
+      sm.q[par][c][wave][lane] = qs[c];
     }
+    if (__any(active && bad) && lane == 0) sm.bad = 1;
     __syncthreads();
+    if (sm.bad) return true;
 
     // Carry-in of this chunk: segment carry, then the earlier chunks.
+    float pin[VEC], qin[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      pin[c] = seg > 0 ? sm.carry[par ^ 1][0][c][lane] : 0.f;
+      qin[c] = seg > 0 ? sm.carry[par ^ 1][1][c][lane] : 0.f;
+    }
     for (int w = 0; w < wave; ++w) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        pin[c] = fmaf(pin[c], DL[c], sm.p[c][w][lane]);
-        qin[c] = fmaf(qin[c], DL[c], sm.q[c][w][lane]);
+        pin[c] = fmaf(pin[c], DL[c], sm.p[par][c][w][lane]);
+        qin[c] = fmaf(qin[c], DL[c], sm.q[par][c][w][lane]);
       }
     }
     if (ck != nullptr && wave % CPB == 0 && active && t0 < T) {
-      // Key range of this wave's checkpoint block (chunks wave..wave+CPB-1).
-      float bmax[VEC], bmin[VEC];
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        float br = -kBig, bl = kBig;
-#pragma unroll
-        for (int j = 0; j < CPB; ++j) {
-          br = fmaxf(br, sm.mx[par][c][wave + j][lane]);
-          bl = fminf(bl, sm.mn[par][c][wave + j][lane]);
-        }
-        bmax[c] = br * kLog2e;
-        bmin[c] = bl * kLog2e;
-      }
+      const float zero[VEC] = {};
       float* rec = ck + ck_row + size_t(t0 / kCkptBlock) * C;
-      store_vec<F32, VEC>(byte_offset(rec + 0 * ck_field, ck_boff), R);
+      store_vec<F32, VEC>(byte_offset(rec + 0 * ck_field, ck_boff), zero);
       store_vec<F32, VEC>(byte_offset(rec + 1 * ck_field, ck_boff), pin);
       store_vec<F32, VEC>(byte_offset(rec + 2 * ck_field, ck_boff), qin);
-      store_vec<F32, VEC>(byte_offset(rec + 3 * ck_field, ck_boff), bmax);
-      store_vec<F32, VEC>(byte_offset(rec + 4 * ck_field, ck_boff), bmin);
     }
     if (wave == W - 1) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        sm.carry[seg & 1][0][c][lane] = R[c];
-        sm.carry[seg & 1][1][c][lane] = fmaf(pin[c], DL[c], ps[c]);
-        sm.carry[seg & 1][2][c][lane] = fmaf(qin[c], DL[c], qs[c]);
+        sm.carry[par][0][c][lane] = fmaf(pin[c], DL[c], ps[c]);
+        sm.carry[par][1][c][lane] = fmaf(qin[c], DL[c], qs[c]);
       }
     }
 
@@ -246,18 +195,10 @@ __device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
   for (int t = 0; t < T; ++t) {
     const size_t idx = base + size_t(t) * C;
     if (ck != nullptr && t % kCkptBlock == 0) {
-      float bmax = -kBig, bmin = kBig;
-      for (int j = t; j < min(T, t + kCkptBlock); ++j) {
-        const float kj = load_scalar<E>(k + base + size_t(j) * C);
-        bmax = fmaxf(bmax, kj);
-        bmin = fminf(bmin, kj);
-      }
       float* rec = ck + ck_lane + size_t(t / kCkptBlock) * C;
       rec[0 * ck_field] = o;
       rec[1 * ck_field] = p;
       rec[2 * ck_field] = q;
-      rec[3 * ck_field] = bmax * kLog2e;
-      rec[4 * ck_field] = bmin * kLog2e;
     }
     const float kk = load_scalar<E>(k + idx) * kLog2e;
     const float vv = load_scalar<E>(v + idx);
@@ -316,36 +257,38 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
     U[c] = fast_exp2(u2);
     u_ok &= fabsf(u2) <= kMaxU;
   }
+  if (threadIdx.x == 0) sm.bad = 0;
+  // |u log2e| is part of the guard: a row with any channel out of range goes
+  // straight to the exact path.
+  bool bad = __syncthreads_or(!u_ok) != 0;
 
   const int nseg = (T + F::SEG - 1) / F::SEG;
   const int nfull = T / F::SEG;
   PackT kA[L], vA[L], kB[L], vB[L];
-  bool bad = false;
   // The next segment is prefetched on every path (the last segment prefetches
   // itself again, a cache hit): with the same loads issued on every path, the
   // compiler's wait before a segment's arithmetic only covers the loads it
   // consumes, not the prefetch issued just before it.
   const int lastseg = nseg - 1;
-  F::load_chunk(k, v, row_base, lane_boff, wave * L, T, C, kA, vA);
-  for (int seg = 0; seg < nseg; seg += 2) {
+  if (!bad) F::load_chunk(k, v, row_base, lane_boff, wave * L, T, C, kA, vA);
+  for (int seg = 0; seg < nseg && !bad; seg += 2) {
     F::load_chunk(k, v, row_base, lane_boff, min(seg + 1, lastseg) * F::SEG + wave * L, T, C, kB,
                   vB);
     bad = seg < nfull
               ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, lane_boff, y,
-                                          ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U, u_ok)
+                                          ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U)
               : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, lane_boff,
-                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U, u_ok);
+                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U);
     if (bad || seg + 1 >= nseg) break;
     F::load_chunk(k, v, row_base, lane_boff, min(seg + 2, lastseg) * F::SEG + wave * L, T, C, kA,
                   vA);
     bad = seg + 1 < nfull
               ? F::template segment<true>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                          lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL, U,
-                                          u_ok)
+                                          lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
+                                          U)
               : F::template segment<false>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                           lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL, U,
-                                           u_ok);
-    if (bad) break;
+                                           lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
+                                           U);
   }
   if (bad) {
     // Workgroup-uniform: recompute the row with the running-max recurrence.
@@ -371,7 +314,8 @@ struct TileCfg { int vec, L, W; };
 // Tile configurations compiled into the library (no VGPR spills at 64*W
 // threads per workgroup).  SEG = W*L must be a multiple of the 64-step
 // checkpoint block.
-static constexpr TileCfg kFwdCfgs[] = {{2, 8, 16}, {1, 8, 16}, {2, 8, 8}, {1, 16, 8}, {1, 8, 8}};
+static constexpr TileCfg kFwdCfgs[] = {{2, 8, 16}, {1, 8, 16}, {2, 8, 8}, {1, 16, 8}, {1, 8, 8},
+                                        {1, 16, 4}, {2, 16, 4}};
 
 int pick_vec(int64_t B, int64_t C);
 bool env_cfg(const char* name, int& vec, int& L, int& W);
@@ -420,6 +364,8 @@ static int dispatch_fwd(const void* k, const void* v, const float* decay, int de
   WKV_FWD_CASE(2, 8, 8)
   WKV_FWD_CASE(1, 16, 8)
   WKV_FWD_CASE(1, 8, 8)
+  WKV_FWD_CASE(1, 16, 4)
+  WKV_FWD_CASE(2, 16, 4)
 #undef WKV_FWD_CASE
   return fail(1, "wkv4_forward: no kernel for the selected tile configuration");
 }

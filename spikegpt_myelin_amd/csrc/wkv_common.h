@@ -22,15 +22,14 @@ constexpr float kBig = 3.0e38f;
 // Steps per checkpoint record of the forward state (see wkv4_fwd.hip).
 constexpr int kCkptBlock = 64;
 // Fields of a checkpoint record: state (A, B) = 2^o (p, q) at the block
-// start, and the block's largest and smallest k*log2(e).
-constexpr int kCkptFields = 5;
+// start.
+constexpr int kCkptFields = 3;
 
-// Range of the shared-frame arithmetic (base-2 exponents): spread between a
-// segment's frame and its smallest key, jump between consecutive frames, and
-// |time_first * log2(e)|.  Outside it a row is recomputed with the reference
-// running-max recurrences.
-constexpr float kMaxSpread = 80.f;
-constexpr float kMaxJump = 80.f;
+// Range of the fixed-frame arithmetic (base-2 exponents): |k * log2(e)| of
+// every element and |time_first * log2(e)| of every channel of a row.
+// Outside it the row is recomputed with the reference running-max
+// recurrences.
+constexpr float kMaxK = 60.f;
 constexpr float kMaxU = 16.f;
 
 // p advanced by b bytes.  Spelled as a 32-bit byte offset added to a
@@ -48,6 +47,10 @@ __device__ __forceinline__ T* byte_offset(T* p, unsigned b) {
     return reinterpret_cast<T*>(reinterpret_cast<char*>(p) + b);
   }
 }
+
+// Clang vector types (the nontemporal builtins take these, not HIP's structs).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- math ----
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -188,22 +191,25 @@ template <typename E, int VEC> struct OutPack {
       }
     }
   }
+  // Non-temporal (streaming) stores: outputs are not re-read by the kernel
+  // that writes them, and keeping them out of the L2 as dirty lines measured
+  // 6-10% faster for both RWKV-4 kernels than ordinary stores.
   __device__ __forceinline__ void store(typename E::raw* p) const {
     if constexpr (k32) {
       if constexpr (VEC == 1) {
-        *reinterpret_cast<uint32_t*>(p) = u[0];
+        __builtin_nontemporal_store(u[0], reinterpret_cast<uint32_t*>(p));
       } else if constexpr (VEC == 2) {
-        *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
+        __builtin_nontemporal_store(u32x2{u[0], u[1]}, reinterpret_cast<u32x2*>(p));
       } else {
-        *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+        __builtin_nontemporal_store(u32x4{u[0], u[1], u[2], u[3]}, reinterpret_cast<u32x4*>(p));
       }
     } else {
       if constexpr (VEC == 1) {
-        *p = static_cast<uint16_t>(u[0]);
+        __builtin_nontemporal_store(static_cast<uint16_t>(u[0]), p);
       } else if constexpr (VEC == 2) {
-        *reinterpret_cast<uint32_t*>(p) = u[0];
+        __builtin_nontemporal_store(u[0], reinterpret_cast<uint32_t*>(p));
       } else {
-        *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
+        __builtin_nontemporal_store(u32x2{u[0], u[1]}, reinterpret_cast<u32x2*>(p));
       }
     }
   }

@@ -17,7 +17,7 @@ Autograd.  The reference saves the four inputs and its backward kernel
 replays the whole forward (``wkv_triton.py:85-115``).  Here the public
 forward ops are composites of the private op ``myelin::wkv4_forward_train``,
 which returns ``y`` together with small forward-state checkpoint records
-(``[5, B, ceil(T/64), C]`` fp32, ~0.3 B per element); its registered backward
+(``[3, B, ceil(T/64), C]`` fp32, ~0.19 B per element); its registered backward
 (``myelin::wkv4_backward_train``) reads the sequence once from those records.
 Gradients are the same quantities as the reference's
 (``wkv_triton.py:200-218``).  ``myelin::wkv_backward*`` remain standalone ops
@@ -41,7 +41,7 @@ from . import _lib
 
 _NATIVE = (torch.float32, torch.bfloat16, torch.float16)
 CKPT_BLOCK = 64  # steps per checkpoint record
-CKPT_FIELDS = 5
+CKPT_FIELDS = 3
 
 
 def _compute_inputs(key: Tensor, value: Tensor) -> tuple[Tensor, Tensor]:

@@ -64,7 +64,7 @@ def test_checkpoint_size_matches_python_layout(lib):
     from spikegpt_myelin_amd.wkv import checkpoint_shape
     for b, t, c in [(64, 1024, 512), (3, 7, 96), (1, 1, 1), (24, 3072, 512), (2, 65, 4100)]:
         f, bb, nblk, cc = checkpoint_shape(b, t, c)
-        assert (f, bb, nblk, cc) == (5, b, (t + 63) // 64, c)
+        assert (f, bb, nblk, cc) == (3, b, (t + 63) // 64, c)
         assert lib.wkv4_checkpoint_bytes(b, t, c) == 4 * f * bb * nblk * cc
 
 
