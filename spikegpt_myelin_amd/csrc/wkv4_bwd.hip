@@ -161,27 +161,37 @@ struct Bwd {
     float rcarry[2][4][VEC][64];  // reverse segment carry (G, H, G', H')
   };
 
+  // Per channel: e^{iw} (d0[i-1]) and i e^{iw} (d1[i-1]) for i = 1..L-1.
+  struct Weights {
+    float d0[L - 1][VEC], d1[L - 1][VEC];
+  };
+
   // Forward state at a segment's start.
   struct Recs {
     float p[VEC], q[VEC];
   };
 
-  // row_base and ck_row are wave-uniform (SGPRs), lane_boff and ck_boff the
-  // lane's byte offsets; steps past the end re-read step T-1 (masked in the
-  // arithmetic).
+  // Loads the wave's chunk (L steps from t0) of segment seg through buffer
+  // descriptors based at the chunk (row_base, ck_row wave-uniform; lane_boff,
+  // ck_boff the lane's byte offsets); steps at or past T read as zero.
   __device__ static __forceinline__ void load(const raw* __restrict__ k, const raw* __restrict__ v,
                                               const raw* __restrict__ g,
                                               const float* __restrict__ ck, size_t ck_row,
                                               unsigned ck_boff, size_t ck_field, int seg,
-                                              size_t row_base, unsigned lane_boff, int t0, int T,
-                                              int C, PackT (&kb)[L], PackT (&vb)[L],
+                                              size_t row_base, size_t row_tail, unsigned lane_boff,
+                                              int t0, int C, PackT (&kb)[L], PackT (&vb)[L],
                                               PackT (&gb)[L], Recs& rc) {
+    const uint32_t bytes = span_bytes(row_tail, t0, C, int(sizeof(raw)));
+    const size_t base = row_base + size_t(t0) * C;
+    const rsrc_t rk = make_rsrc(k + base, bytes);
+    const rsrc_t rv = make_rsrc(v + base, bytes);
+    const rsrc_t rg = make_rsrc(g + base, bytes);
+    const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-      const size_t step = row_base + size_t(min(t0 + i, T - 1)) * C;
-      kb[i].load(byte_offset(k + step, lane_boff));
-      vb[i].load(byte_offset(v + step, lane_boff));
-      gb[i].load(byte_offset(g + step, lane_boff));
+      load_buf(kb[i], rk, lane_boff, unsigned(i) * stride);
+      load_buf(vb[i], rv, lane_boff, unsigned(i) * stride);
+      load_buf(gb[i], rg, lane_boff, unsigned(i) * stride);
     }
     const float* rec = ck + ck_row + size_t(seg) * BPS * C;
     Pack<F32, VEC> a;
@@ -198,9 +208,10 @@ struct Bwd {
   template <bool FULL>
   __device__ static __forceinline__ void segment(
       Smem& sm, int seg, int nseg, int T, int C, int wave, int lane, bool active, size_t row_base,
-      unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
+      size_t row_tail, unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
       const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC],
-      raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC], float (&gu)[VEC]) {
+      const Weights& Wt, raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC],
+      float (&gu)[VEC]) {
     const int t0 = (seg * W + wave) * L;
     float P[VEC], Q[VEC];
 #pragma unroll
@@ -258,18 +269,27 @@ struct Bwd {
         Q[c] = fmaf(Q[c], D[c], e);
       }
     }
-    // Reverse summary of this chunk from a zero state at its end.
+    // Reverse summary of this chunk from a zero state at its end, as dot
+    // products with the weights e^{iw} and i e^{iw} of step i:
+    // G = sum_i e^{iw} z_i, G' = sum_i i e^{iw} z_i (likewise H, H' with z y).
     float G[VEC], H[VEC], Gp[VEC], Hp[VEC];
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) { G[c] = 0.f; H[c] = 0.f; Gp[c] = 0.f; Hp[c] = 0.f; }
+    for (int c = 0; c < VEC; ++c) {
+      G[c] = zz[0][c];
+      H[c] = zy[0][c];
+      Gp[c] = zz[1][c] * Wt.d1[0][c];
+      Hp[c] = zy[1][c] * Wt.d1[0][c];
+      G[c] = fmaf(zz[1][c], Wt.d0[0][c], G[c]);
+      H[c] = fmaf(zy[1][c], Wt.d0[0][c], H[c]);
+    }
 #pragma unroll
-    for (int i = L - 1; i >= 0; --i) {
+    for (int i = 2; i < L; ++i) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        Gp[c] = (Gp[c] + G[c]) * D[c];
-        Hp[c] = (Hp[c] + H[c]) * D[c];
-        G[c] = fmaf(G[c], D[c], zz[i][c]);
-        H[c] = fmaf(H[c], D[c], zy[i][c]);
+        G[c] = fmaf(zz[i][c], Wt.d0[i - 1][c], G[c]);
+        H[c] = fmaf(zy[i][c], Wt.d0[i - 1][c], H[c]);
+        Gp[c] = fmaf(zz[i][c], Wt.d1[i - 1][c], Gp[c]);
+        Hp[c] = fmaf(zy[i][c], Wt.d1[i - 1][c], Hp[c]);
       }
     }
 #pragma unroll
@@ -310,12 +330,14 @@ struct Bwd {
         const float vv = vb[i].get(c);
         const float e = ek[i][c];
         const float z = zz[i][c];
-        const float e1 = e * U[c];
-        // z e1 (v - y) = e1 (z v - z y)
-        const float gkd = e1 * fmaf(z, vv, -zy[i][c]);
-        gvo[c] = fmaf(e, G[c], z * e1);
-        gko[c] = fmaf(e, fmaf(vv, G[c], -H[c]), gkd);
-        gu[c] += gkd;
+        // With a = e^u z + G and b = e^u z y + H:
+        //   gv = e a,  gk = e (v a - b) = e^{u+k} z (v - y) + e^k (v G - H),
+        // and gu accumulates e (z v - z y) (times e^u once at the end).
+        const float a = fmaf(U[c], z, G[c]);
+        const float bb = fmaf(U[c], zy[i][c], H[c]);
+        gvo[c] = e * a;
+        gko[c] = e * fmaf(vv, a, -bb);
+        gu[c] = fmaf(e, fmaf(z, vv, -zy[i][c]), gu[c]);
         gw[c] = fmaf(e, fmaf(vv, Gp[c], -Hp[c]), gw[c]);
         Gp[c] = (Gp[c] + G[c]) * D[c];
         Hp[c] = (Hp[c] + H[c]) * D[c];
@@ -326,14 +348,16 @@ struct Bwd {
       gvo_p[i].set(gvo);
     }
     if (active) {
+      // Steps past T fall outside the descriptors and are dropped.
+      const uint32_t bytes = span_bytes(row_tail, t0, C, int(sizeof(raw)));
+      const size_t base = row_base + size_t(t0) * C;
+      const rsrc_t rgk = make_rsrc(gk + base, bytes);
+      const rsrc_t rgv = make_rsrc(gv + base, bytes);
+      const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
 #pragma unroll
       for (int i = L - 1; i >= 0; --i) {
-        const int t = t0 + i;
-        if (FULL || t < T) {
-          const size_t step = row_base + size_t(t) * C;
-          gko_p[i].store(byte_offset(gk + step, lane_boff));
-          gvo_p[i].store(byte_offset(gv + step, lane_boff));
-        }
+        store_buf(gko_p[i], rgk, lane_boff, unsigned(i) * stride);
+        store_buf(gvo_p[i], rgv, lane_boff, unsigned(i) * stride);
       }
     }
     if (wave == 0) {
@@ -369,6 +393,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
   const int c0 = cg * F::CPW + lane * VEC;
   const bool active = c0 < C;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * F::CPW;
   // Lanes past the last channel read channel 0 of the row (never stored).
   const unsigned lane_boff = active ? unsigned(lane * VEC * sizeof(typename E::raw)) : 0u;
   const int nseg = (T + F::SEG - 1) / F::SEG;
@@ -388,6 +413,17 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
     DL[c] = fast_exp2(w2 * float(L));
     U[c] = fast_exp2(uv * kLog2e);
   }
+  typename F::Weights Wt;
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    float pw = D[c];
+#pragma unroll
+    for (int i = 1; i < L; ++i) {
+      Wt.d0[i - 1][c] = pw;
+      Wt.d1[i - 1][c] = float(i) * pw;
+      pw *= D[c];
+    }
+  }
   // Rows the forward kernel recomputed with its exact serial path carry
   // o != 0 in their block-0 records; this row then takes the exact path too.
   bool serial = false;
@@ -406,31 +442,32 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
     PackT kA[L], vA[L], gA[L], kB[L], vB[L], gB[L];
     typename F::Recs rA, rB;
     const int last = nseg - 1;
-    F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, last, row_base, lane_boff,
-            last * F::SEG + wave * L, T, C, kA, vA, gA, rA);
+    F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, last, row_base, row_tail, lane_boff,
+            last * F::SEG + wave * L, C, kA, vA, gA, rA);
     // The next segment is prefetched on every path (segment 0 prefetches
     // itself again, a cache hit), so that the wait before a segment's
-    // arithmetic only covers the loads it consumes.
+    // arithmetic only covers the loads it consumes.  Steps past T read as
+    // zero (outside the buffer descriptors).
     for (int seg = last; seg >= 0; seg -= 2) {
       const int s1 = max(seg - 1, 0), s2 = max(seg - 2, 0);
-      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s1, row_base, lane_boff,
-              s1 * F::SEG + wave * L, T, C, kB, vB, gB, rB);
+      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s1, row_base, row_tail, lane_boff,
+              s1 * F::SEG + wave * L, C, kB, vB, gB, rB);
       if (seg < nfull) {
-        F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base, lane_boff,
-                                  kA, vA, gA, rA, D, DL, U, gk, gv, gw, gu);
+        F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
+                                  kA, vA, gA, rA, D, DL, U, Wt, gk, gv, gw, gu);
       } else {
-        F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base, lane_boff,
-                                   kA, vA, gA, rA, D, DL, U, gk, gv, gw, gu);
+        F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
+                                   kA, vA, gA, rA, D, DL, U, Wt, gk, gv, gw, gu);
       }
       if (seg - 1 < 0) break;
-      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s2, row_base, lane_boff,
-              s2 * F::SEG + wave * L, T, C, kA, vA, gA, rA);
+      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s2, row_base, row_tail, lane_boff,
+              s2 * F::SEG + wave * L, C, kA, vA, gA, rA);
       if (seg - 1 < nfull) {
         F::template segment<true>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
-                                  lane_boff, kB, vB, gB, rB, D, DL, U, gk, gv, gw, gu);
+                                  row_tail, lane_boff, kB, vB, gB, rB, D, DL, U, Wt, gk, gv, gw, gu);
       } else {
         F::template segment<false>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
-                                   lane_boff, kB, vB, gB, rB, D, DL, U, gk, gv, gw, gu);
+                                   row_tail, lane_boff, kB, vB, gB, rB, D, DL, U, Wt, gk, gv, gw, gu);
       }
     }
   }
@@ -441,7 +478,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       sm.G[c][wave][lane] = gw[c];
-      sm.H[c][wave][lane] = gu[c];
+      sm.H[c][wave][lane] = gu[c] * U[c];
     }
     __syncthreads();
     for (int ch = threadIdx.x; ch < F::CPW; ch += blockDim.x) {

@@ -68,17 +68,22 @@ struct Fwd {
     int bad;                     // sticky: some key of the row is out of range
   };
 
-  // row_base is wave-uniform (SGPRs); lane_boff is the lane's byte offset.
-  // Steps past the end re-read step T-1 (masked in the arithmetic).
+  // Loads the chunk of L steps starting at t0 through buffer descriptors
+  // based at the chunk (row_base is wave-uniform, lane_boff the lane's byte
+  // offset).  Steps at or past T read as zero.
   __device__ static __forceinline__ void load_chunk(const raw* __restrict__ k,
                                                     const raw* __restrict__ v, size_t row_base,
-                                                    unsigned lane_boff, int t0, int T, int C,
-                                                    PackT (&kb)[L], PackT (&vb)[L]) {
+                                                    size_t row_tail, unsigned lane_boff, int t0,
+                                                    int C, PackT (&kb)[L], PackT (&vb)[L]) {
+    const uint32_t bytes = span_bytes(row_tail, t0, C, int(sizeof(raw)));
+    const size_t base = row_base + size_t(t0) * C;
+    const rsrc_t rk = make_rsrc(k + base, bytes);
+    const rsrc_t rv = make_rsrc(v + base, bytes);
+    const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
 #pragma unroll
     for (int i = 0; i < L; ++i) {
-      const size_t step = row_base + size_t(min(t0 + i, T - 1)) * C;
-      kb[i].load(byte_offset(k + step, lane_boff));
-      vb[i].load(byte_offset(v + step, lane_boff));
+      load_buf(kb[i], rk, lane_boff, unsigned(i) * stride);
+      load_buf(vb[i], rv, lane_boff, unsigned(i) * stride);
     }
   }
 
@@ -87,7 +92,7 @@ struct Fwd {
   template <bool FULL>
   __device__ static __forceinline__ bool segment(
       Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
-      unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
+      size_t row_tail, unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
       unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L],
       const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC]) {
     const int t0 = seg * SEG + wave * L;
@@ -171,11 +176,12 @@ struct Fwd {
         yp[i].set(yv);
       }
       if (active) {
+        // Steps past T fall outside the descriptor and are dropped.
+        const rsrc_t ry = make_rsrc(y + row_base + size_t(t0) * C,
+                                    span_bytes(row_tail, t0, C, int(sizeof(raw))));
+        const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
 #pragma unroll
-        for (int i = 0; i < L; ++i) {
-          const int t = t0 + i;
-          if (FULL || t < T) yp[i].store(byte_offset(y + (row_base + size_t(t) * C), lane_boff));
-        }
+        for (int i = 0; i < L; ++i) store_buf(yp[i], ry, lane_boff, unsigned(i) * stride);
       }
     }
     return false;
@@ -237,6 +243,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const int c0 = cg * F::CPW + lane * VEC;
   const bool active = c0 < C;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * F::CPW;
   // Lanes past the last channel read channel 0 of the row (never stored).
   const unsigned lane_boff = active ? unsigned(lane * VEC * sizeof(typename E::raw)) : 0u;
   const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
@@ -265,29 +272,27 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const int nseg = (T + F::SEG - 1) / F::SEG;
   const int nfull = T / F::SEG;
   PackT kA[L], vA[L], kB[L], vB[L];
-  // The next segment is prefetched on every path (the last segment prefetches
-  // itself again, a cache hit): with the same loads issued on every path, the
-  // compiler's wait before a segment's arithmetic only covers the loads it
-  // consumes, not the prefetch issued just before it.
-  const int lastseg = nseg - 1;
-  if (!bad) F::load_chunk(k, v, row_base, lane_boff, wave * L, T, C, kA, vA);
+  // The next segment is prefetched on every path (past the end the
+  // descriptor is empty and the loads return zeros without touching memory):
+  // with the same loads issued on every path, the compiler's wait before a
+  // segment's arithmetic only covers the loads it consumes, not the prefetch
+  // issued just before it.
+  if (!bad) F::load_chunk(k, v, row_base, row_tail, lane_boff, wave * L, C, kA, vA);
   for (int seg = 0; seg < nseg && !bad; seg += 2) {
-    F::load_chunk(k, v, row_base, lane_boff, min(seg + 1, lastseg) * F::SEG + wave * L, T, C, kB,
-                  vB);
+    F::load_chunk(k, v, row_base, row_tail, lane_boff, (seg + 1) * F::SEG + wave * L, C, kB, vB);
     bad = seg < nfull
-              ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, lane_boff, y,
+              ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, row_tail, lane_boff, y,
                                           ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U)
-              : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, lane_boff,
+              : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
                                            y, ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U);
     if (bad || seg + 1 >= nseg) break;
-    F::load_chunk(k, v, row_base, lane_boff, min(seg + 2, lastseg) * F::SEG + wave * L, T, C, kA,
-                  vA);
+    F::load_chunk(k, v, row_base, row_tail, lane_boff, (seg + 2) * F::SEG + wave * L, C, kA, vA);
     bad = seg + 1 < nfull
               ? F::template segment<true>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                          lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
+                                          row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
                                           U)
               : F::template segment<false>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                           lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
+                                           row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
                                            U);
   }
   if (bad) {
