@@ -13,9 +13,12 @@ allocation and autograd on every call) is reported as ``op_ms_per_step``.
 
 Reported beside the throughput:
 * ``roofline`` -- the dominant launch (the backward: the reverse-sweep kernel
-  plus the small batch-sum kernel), timed with HIP events recorded on the
-  launch stream around every call in the timed region; algorithmic bytes =
-  10 B per [B,T,C] element (k, v, dy read, dk, dv written); peak 8 TB/s.  ``traffic`` comes from the committed rocprofv3 PMC
+  plus the small batch-sum kernel), timed on every 10th step of the timed
+  region (``--event-every``) with HIP events bound to its first and last
+  kernel dispatch (``wkv_time_next_call``: the kernels' own start and end
+  timestamps on the launch stream, no marker packets); algorithmic bytes = 10 B per [B,T,C]
+  element (k, v, dy read, dk, dv written); peak 8 TB/s.  ``traffic`` comes
+  from the committed rocprofv3 PMC
   summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters
   on a copy of known size) when present, else null.
 * ``cpu_baseline`` -- the reference's CPU WKV path restated in eager PyTorch
@@ -177,8 +180,9 @@ def bench_wkv4(args, cfg) -> dict:
     pool = EventPool(4 * args.steps * layers, stream)
 
     def step(events=None, timed=(dom_name,)):
-        # HIP events (on the launch stream) bracket the launches named in
-        # `timed`; the others run back to back.
+        # The launches named in `timed` carry HIP events on their first and
+        # last kernel dispatch (kernel start/end timestamps; the stream gets
+        # no marker packets, so the timed step is not perturbed).
         for _ in range(layers):
             for name, fn in (("fwd", fwd),) if fwd_only else (("fwd", fwd), ("bwd", bwd)):
                 if events is None or name not in timed:
@@ -186,9 +190,8 @@ def bench_wkv4(args, cfg) -> dict:
                     continue
                 s_ev = pool.take()
                 e_ev = pool.take()
-                s_ev.record(stream)
+                _lib.arm_events(s_ev, e_ev)
                 fn()
-                e_ev.record(stream)
                 events.append((name, s_ev, e_ev))
 
     for _ in range(args.warmup):
@@ -197,8 +200,10 @@ def bench_wkv4(args, cfg) -> dict:
     # Timed region: K steps; events around the dominant launch only.
     events: list = []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step(events)
+    for i in range(args.steps):
+        # A timed launch is fenced for its events; every `event_every`-th step
+        # carries them so that the other steps run undisturbed.
+        step(events if i % args.event_every == 0 else None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     step_s = elapsed / args.steps
@@ -388,9 +393,8 @@ def bench_wkv7(args) -> dict:
     for _ in range(args.steps):
         for name, fn in (("fwd", fwd), ("bwd", bwd)):
             s_ev, e_ev = pool.take(), pool.take()
-            s_ev.record(stream)
+            _lib.arm_events(s_ev, e_ev)
             fn()
-            e_ev.record(stream)
             evs.append((name, s_ev, e_ev))
     torch.cuda.synchronize()
     for name, s_ev, e_ev in evs:
@@ -423,8 +427,10 @@ def bench_wkv7(args) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--event-every", type=int, default=10,
+                    help="time the dominant launch with HIP events on every N-th timed step")
     ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")

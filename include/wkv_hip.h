@@ -162,6 +162,17 @@ int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, cons
                                void* grad_b, float* grad_s0, int64_t B, int64_t T, int64_t H,
                                int64_t N, int dtype, void* stream);
 
+/* Measurement hook; no counterpart in the reference.  Arms two HIP events
+ * (hipEvent_t, created with timing enabled; either may be NULL) for the next
+ * entry point called on this thread: its first kernel dispatch records
+ * start_event at the kernel's start and its last dispatch records stop_event
+ * at the kernel's end.  The events ride on the dispatch packets
+ * (hipExtLaunchKernel), so the stream gets no extra marker packets and the
+ * elapsed time is the kernels' own, as a kernel trace reports it.  One call
+ * consumes the pair; an entry point that launches nothing leaves the events
+ * unrecorded. */
+int wkv_time_next_call(void* start_event, void* stop_event);
+
 /* Text of the last error raised on the calling thread ("" if none). */
 const char* wkv_last_error_string(void);
 

@@ -62,13 +62,15 @@ SIGNATURES = {
         _INT,
         [_P] * 16 + [_I64, _I64, _I64, _I64, _INT, _P],
     ),
+    "wkv_time_next_call": (_INT, [_P, _P]),
     "wkv_last_error_string": (ctypes.c_char_p, []),
     "wkv_version": (ctypes.c_char_p, []),
 }
 
 # Optional timing hook: when set to a list, every C ABI launch made through
-# ``timed`` appends (name, start_event, end_event) recorded on the launch
-# stream immediately around the call.  None (the default) costs nothing.
+# ``timed`` appends (name, start_event, end_event), the events carried by the
+# launch's first and last kernel dispatch (``wkv_time_next_call``).  None (the
+# default) costs nothing.
 EVENT_LOG: list | None = None
 
 _lock = threading.Lock()
@@ -124,18 +126,26 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def timed(name: str, device: torch.device, call):
-    """Run ``call()`` (a C ABI launch); bracket it with HIP events on the
-    current stream when ``EVENT_LOG`` is a list."""
+    """Run ``call()`` (one C ABI entry point); when ``EVENT_LOG`` is a list,
+    time its kernels with events bound to their dispatches."""
     if EVENT_LOG is None:
         return call()
-    stream = torch.cuda.current_stream(device)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
+    arm_events(start, end)
     rc = call()
-    end.record(stream)
     EVENT_LOG.append((name, start, end))
     return rc
+
+
+def arm_events(start: torch.cuda.Event, end: torch.cuda.Event) -> None:
+    """Bind ``start``/``end`` to the first/last kernel dispatch of the next C ABI
+    call on this thread (kernel start and end timestamps, no marker packets)."""
+    for ev in (start, end):
+        if ev.cuda_event == 0:
+            # torch creates the HIP event lazily at its first record.
+            ev.record(torch.cuda.current_stream())
+    load().wkv_time_next_call(start.cuda_event, end.cuda_event)
 
 
 def stream_of(t: torch.Tensor) -> int:

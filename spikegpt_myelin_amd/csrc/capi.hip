@@ -15,6 +15,22 @@
 namespace wkv_host {
 
 static thread_local std::string g_last_error;
+// Events armed by wkv_time_next_call for the next entry point on this
+// thread, and those of the entry point running now.
+static thread_local CallEvents g_pending_events;
+static thread_local CallEvents g_active_events;
+
+CallEvents& active_events() { return g_active_events; }
+
+// Moves the armed events (if any) to the running entry point for its
+// duration.
+struct TimingScope {
+  TimingScope() {
+    g_active_events = g_pending_events;
+    g_pending_events = CallEvents{};
+  }
+  ~TimingScope() { g_active_events = CallEvents{}; }
+};
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -99,6 +115,7 @@ extern "C" {
 int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
                  void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: unknown dtype");
   if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: bad sizes");
   if (B == 0 || T == 0 || C == 0) return WKV_OK;
@@ -119,6 +136,7 @@ int wkv4_forward_checkpointed(const void* k, const void* v, const float* time_de
                               const float* time_first, void* y, float* checkpoint, int64_t B,
                               int64_t T, int64_t C, int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype))
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: unknown dtype");
   if (!dims_ok(B, T, C))
@@ -143,6 +161,7 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
                   void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
                   int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: unknown dtype");
   if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: bad sizes");
   if (C == 0) return WKV_OK;
@@ -175,6 +194,7 @@ int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
                                size_t workspace_bytes, int64_t B, int64_t T, int64_t C, int dtype,
                                void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype))
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_checkpointed: unknown dtype");
   if (!dims_ok(B, T, C))
@@ -202,6 +222,7 @@ int wkv4_decode_step(const void* k, const void* v, const float* time_decay, cons
                      float* num_out, float* den_out, float* log_scale_out, int64_t B, int64_t C,
                      int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_decode_step: unknown dtype");
   if (!dims_ok(B, 1, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_decode_step: bad sizes");
   if (B == 0 || C == 0) return WKV_OK;
@@ -218,6 +239,7 @@ int wkv7_forward(const void* r, const void* w, const void* k, const void* v, con
                  const void* b, const float* s0, void* y, float* s_out, int64_t B, int64_t T,
                  int64_t H, int64_t N, int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: unknown dtype");
   if (N != 64) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: head size must be 64");
   if (!dims_ok(B, T, H * N)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward: bad sizes");
@@ -241,6 +263,7 @@ int wkv7_forward_checkpointed(const void* r, const void* w, const void* k, const
                               float* s_out, float* checkpoint, int64_t B, int64_t T, int64_t H,
                               int64_t N, int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   if (!dtype_ok(dtype))
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_forward_checkpointed: unknown dtype");
   if (N != 64)
@@ -287,6 +310,7 @@ int wkv7_backward(const void* r, const void* w, const void* k, const void* v, co
                   void* grad_b, float* grad_s0, void* workspace, size_t workspace_bytes,
                   int64_t B, int64_t T, int64_t H, int64_t N, int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   int rc = wkv7_backward_checks("wkv7_backward", r, w, k, v, a, b, grad_y, grad_s_out, grad_r,
                                 grad_w, grad_k, grad_v, grad_a, grad_b, grad_s0, B, T, H, N,
                                 dtype);
@@ -303,8 +327,12 @@ int wkv7_backward(const void* r, const void* w, const void* k, const void* v, co
     if (!aligned16({s0, workspace}))
       return fail(WKV_ERR_INVALID_ARGUMENT, "wkv7_backward: tensors must be 16-byte aligned");
     ck = static_cast<float*>(workspace);
+    // The forward stage does not end the call: it carries no stop event.
+    hipEvent_t stop = active_events().stop;
+    active_events().stop = nullptr;
     rc = wkv7_forward_impl(r, w, k, v, a, b, s0, nullptr, nullptr, ck, int(B), int(T), int(H),
                            dtype, s);
+    active_events().stop = stop;
     if (rc) return rc;
   }
   return wkv7_backward_ck_impl(r, w, k, v, a, b, grad_y, ck, grad_s_out, grad_r, grad_w, grad_k,
@@ -318,6 +346,7 @@ int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, cons
                                void* grad_b, float* grad_s0, int64_t B, int64_t T, int64_t H,
                                int64_t N, int dtype, void* stream) {
   set_error("");
+  TimingScope timing;
   int rc = wkv7_backward_checks("wkv7_backward_checkpointed", r, w, k, v, a, b, grad_y,
                                 grad_s_out, grad_r, grad_w, grad_k, grad_v, grad_a, grad_b,
                                 grad_s0, B, T, H, N, dtype);
@@ -332,6 +361,12 @@ int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, cons
   return wkv7_backward_ck_impl(r, w, k, v, a, b, grad_y, checkpoint, grad_s_out, grad_r, grad_w,
                                grad_k, grad_v, grad_a, grad_b, grad_s0, int(B), int(T), int(H),
                                dtype, static_cast<hipStream_t>(stream));
+}
+
+int wkv_time_next_call(void* start_event, void* stop_event) {
+  g_pending_events.start = static_cast<hipEvent_t>(start_event);
+  g_pending_events.stop = static_cast<hipEvent_t>(stop_event);
+  return WKV_OK;
 }
 
 const char* wkv_last_error_string(void) { return g_last_error.c_str(); }

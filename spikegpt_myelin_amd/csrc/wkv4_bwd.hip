@@ -601,13 +601,13 @@ static int launch_bwd(const void* gy, const float* decay, int decay_is_w, const 
   float* gw_part = partials;
   float* gu_part = partials + size_t(B) * C;
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
-  hipLaunchKernelGGL((wkv::wkv4_bwd_kernel<E, VEC, L, W>), dim3(unsigned(B) * n_cg),
-                     dim3(W * 64), 0, stream, static_cast<const raw*>(gy), decay, decay_is_w, u,
+  launch(wkv::wkv4_bwd_kernel<E, VEC, L, W>, dim3(unsigned(B) * n_cg),
+                     dim3(W * 64), stream, false, static_cast<const raw*>(gy), decay, decay_is_w, u,
                      static_cast<const raw*>(k), static_cast<const raw*>(v), ck,
                      static_cast<raw*>(gk), static_cast<raw*>(gv), gw_part, gu_part, T, C);
   int rc = check_launch("wkv4_bwd_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(wkv::wkv4_param_grad_kernel, dim3((C + 63) / 64), dim3(1024), 0, stream,
+  launch(wkv::wkv4_param_grad_kernel, dim3((C + 63) / 64), dim3(1024), stream, true,
                      gw_part, gu_part, decay, decay_is_w, gtd, gtf, B, C);
   return check_launch("wkv4_param_grad_kernel");
 }
@@ -660,7 +660,12 @@ int wkv4_backward_impl(const void* gy, const float* w, const float* u, const voi
                        int B, int T, int C, int dtype, hipStream_t stream) {
   float* ck = ws;
   float* partials = ws + wkv4_checkpoint_floats(B, T, C);
+  // The forward stage does not end the call: it carries no stop event.
+  CallEvents& ev = active_events();
+  hipEvent_t stop = ev.stop;
+  ev.stop = nullptr;
   int rc = wkv4_forward_impl(k, v, w, 1, u, nullptr, ck, B, T, C, dtype, stream);
+  ev.stop = stop;
   if (rc) return rc;
   return wkv4_backward_ck_impl(gy, w, 1, u, k, v, ck, gk, gv, gtd, gtf, partials, B, T, C, dtype,
                                stream);
@@ -673,7 +678,7 @@ size_t wkv4_bwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C, int dtype)
 
 int wkv4_zero_param_grads(float* gtd, float* gtf, int C, hipStream_t stream) {
   if (C <= 0) return 0;
-  hipLaunchKernelGGL(wkv::wkv4_zero2_kernel, dim3((C + 255) / 256), dim3(256), 0, stream, gtd,
+  launch(wkv::wkv4_zero2_kernel, dim3((C + 255) / 256), dim3(256), stream, true, gtd,
                      gtf, C);
   return check_launch("wkv4_zero2_kernel");
 }

@@ -68,13 +68,13 @@ static int launch_decode(const void* k, const void* v, const float* td, const fl
   const int64_t n = int64_t(B) * C;
   if (C % 4 == 0) {
     const int64_t threads = n / 4;
-    hipLaunchKernelGGL((wkv::wkv4_decode_kernel<E, 4>), dim3(unsigned((threads + 255) / 256)),
-                       dim3(256), 0, stream, static_cast<const raw*>(k),
+    launch(wkv::wkv4_decode_kernel<E, 4>, dim3(unsigned((threads + 255) / 256)),
+                       dim3(256), stream, true, static_cast<const raw*>(k),
                        static_cast<const raw*>(v), td, tf, num, den, ls, static_cast<raw*>(y),
                        num_out, den_out, ls_out, B, C);
   } else {
-    hipLaunchKernelGGL((wkv::wkv4_decode_kernel<E, 1>), dim3(unsigned((n + 255) / 256)),
-                       dim3(256), 0, stream, static_cast<const raw*>(k),
+    launch(wkv::wkv4_decode_kernel<E, 1>, dim3(unsigned((n + 255) / 256)),
+                       dim3(256), stream, true, static_cast<const raw*>(k),
                        static_cast<const raw*>(v), td, tf, num, den, ls, static_cast<raw*>(y),
                        num_out, den_out, ls_out, B, C);
   }

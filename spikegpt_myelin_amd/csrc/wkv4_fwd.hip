@@ -345,11 +345,11 @@ static int launch_fwd(const void* k, const void* v, const float* decay, int deca
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
   const dim3 grid(unsigned(B) * unsigned(n_cg)), block(W * 64);
   if (y != nullptr) {
-    hipLaunchKernelGGL((wkv::wkv4_fwd_kernel<E, VEC, L, W, true>), grid, block, 0, stream,
+    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, true>, grid, block, stream, true,
                        static_cast<const raw*>(k), static_cast<const raw*>(v), decay, decay_is_w,
                        tf, static_cast<raw*>(y), ck, T, C);
   } else {
-    hipLaunchKernelGGL((wkv::wkv4_fwd_kernel<E, VEC, L, W, false>), grid, block, 0, stream,
+    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, false>, grid, block, stream, true,
                        static_cast<const raw*>(k), static_cast<const raw*>(v), decay, decay_is_w,
                        tf, static_cast<raw*>(nullptr), ck, T, C);
   }

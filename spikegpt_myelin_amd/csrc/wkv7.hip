@@ -558,8 +558,8 @@ static int launch_wkv7_fwd(const void* r, const void* w, const void* k, const vo
   wkv::w7::Vecs<E, 6> in{{static_cast<const raw*>(r), static_cast<const raw*>(w),
                           static_cast<const raw*>(k), static_cast<const raw*>(v),
                           static_cast<const raw*>(a), static_cast<const raw*>(b)}};
-  hipLaunchKernelGGL((wkv::wkv7_fwd_kernel<E>), dim3(unsigned(B) * H), dim3(wkv::w7::kThreads), 0,
-                     stream, in, s0, static_cast<raw*>(y), s_out, ck, T, H);
+  launch(wkv::wkv7_fwd_kernel<E>, dim3(unsigned(B) * H), dim3(wkv::w7::kThreads),
+                     stream, true, in, s0, static_cast<raw*>(y), s_out, ck, T, H);
   return check_launch("wkv7_fwd_kernel");
 }
 
@@ -584,8 +584,8 @@ static int launch_wkv7_bwd(const void* r, const void* w, const void* k, const vo
                           static_cast<const raw*>(k), static_cast<const raw*>(v),
                           static_cast<const raw*>(a), static_cast<const raw*>(b),
                           static_cast<const raw*>(dy)}};
-  hipLaunchKernelGGL((wkv::wkv7_bwd_kernel<E>), dim3(unsigned(B) * H), dim3(wkv::w7::kThreads), 0,
-                     stream, in, ck, ds_T, static_cast<raw*>(dr), static_cast<raw*>(dw),
+  launch(wkv::wkv7_bwd_kernel<E>, dim3(unsigned(B) * H), dim3(wkv::w7::kThreads),
+                     stream, true, in, ck, ds_T, static_cast<raw*>(dr), static_cast<raw*>(dw),
                      static_cast<raw*>(dk), static_cast<raw*>(dv), static_cast<raw*>(da),
                      static_cast<raw*>(db), ds0, T, H);
   return check_launch("wkv7_bwd_kernel");

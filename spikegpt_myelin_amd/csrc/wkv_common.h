@@ -3,6 +3,7 @@
 // channel of the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -276,6 +277,34 @@ namespace wkv_host {
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
+
+// Timing events of the entry point running on this thread (armed by
+// wkv_time_next_call): the first kernel dispatch of the call carries `start`
+// and the dispatch that ends the call carries `stop`.  Both stay null outside
+// a timed call.
+struct CallEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+CallEvents& active_events();
+
+// Kernel launch on `stream`; `ends_call` marks the last dispatch of an entry
+// point.  During a timed call the events are bound to the dispatch packets
+// themselves (hipExtLaunchKernel): the timestamps are the kernels' own start
+// and end, and no marker packet is added to the stream.
+template <typename... KArgs, typename... Args>
+void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream, bool ends_call,
+            Args... args) {
+  CallEvents& ev = active_events();
+  hipEvent_t stop = ends_call ? ev.stop : nullptr;
+  if (ev.start != nullptr || stop != nullptr) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, ev.start, stop, 0,
+                          static_cast<KArgs>(args)...);
+    ev.start = nullptr;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, static_cast<KArgs>(args)...);
+  }
+}
 }  // namespace wkv_host
 
 namespace wkv {
