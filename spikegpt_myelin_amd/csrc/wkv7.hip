@@ -55,7 +55,7 @@ __device__ __forceinline__ unsigned as_u(float f) { return __float_as_uint(f); }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 // Sum over the 16 lanes of a DPP row; every lane of the row receives the
