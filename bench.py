@@ -28,7 +28,9 @@ Reported beside the throughput:
 Other workloads (``--workload``): ``long`` (B=24, T=3072, C=512), ``216m``
 (B=16, T=1024, C=768, 18 layers), ``decode`` (B=256, C=768, 18 layers, fp32
 state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward + backward), ``c0``
-(fp32 forward B=2, T=128, C=512).
+(fp32 forward B=2, T=128, C=512), ``e2e41m`` (the whole 41M SpikeGPT
+training step, 12 layers x 512, vocab 256, B=64, T=1024; the default run
+also reports it as ``e2e_train_step``).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -424,6 +426,50 @@ def bench_wkv7(args) -> dict:
     }
 
 
+def bench_e2e(steps: int, warmup: int) -> dict:
+    """The 41M SpikeGPT training step: 12 layers, 512 embedding, byte vocab
+    (256), B=64, T=1024, random init, synthetic tokens, bf16 autocast, fused
+    AdamW with gradient clipping -- the recipe of the reference's trainer
+    (examples/train_tiny_spikegpt.py:646-655, 797, 866-880).  WKV and LIF run
+    in the HIP kernels; GEMMs, norms and the loss are PyTorch-ROCm."""
+    from spikegpt_myelin_amd.model import SpikeGPTConfig, SpikeLanguageModel
+
+    B, T, layers, embd, vocab = 64, 1024, 12, 512, 256
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    cfg = SpikeGPTConfig(vocab_size=vocab, context_length=T, n_layer=layers, n_embd=embd,
+                         dropout=0.0)
+    model = SpikeLanguageModel(cfg).to(dev)
+    n_params = sum(p.numel() for p in model.parameters())
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.01, fused=True)
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, vocab, (B, T + 1), generator=g).to(dev)
+    x, y = ids[:, :-1].contiguous(), ids[:, 1:].contiguous()
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss, _ = model(x, y)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"tokens_per_s": B * T / dt, "ms_per_step": dt * 1e3, "steps": steps,
+            "warmup": warmup, "loss_last": float(loss), "params": n_params,
+            "config": {"model": "spikegpt-41m", "n_layer": layers, "n_embd": embd,
+                       "vocab": vocab, "B": B, "T": T, "dtype": "bf16 autocast",
+                       "optimizer": "AdamW fused, clip 1.0", "data": "synthetic tokens"}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,9 +477,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--event-every", type=int, default=10,
                     help="time the dominant launch with HIP events on every N-th timed step")
-    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7"])
+    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7", "e2e41m"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--e2e-steps", type=int, default=20,
+                    help="timed steps of the 41M SpikeGPT training step reported with the "
+                         "default workload (0 skips it)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="first run one device copy of this many MiB (a kernel of known traffic "
                          "for scaling PMC byte counters)")
@@ -458,8 +507,12 @@ def main() -> int:
         out = bench_decode(args)
     elif args.workload == "wkv7":
         out = bench_wkv7(args)
+    elif args.workload == "e2e41m":
+        out = bench_e2e(args.steps, args.warmup)
     else:
         out = bench_wkv4(args, WORKLOADS[args.workload])
+        if args.workload == "wkv4" and args.e2e_steps > 0:
+            out["e2e_train_step"] = bench_e2e(args.e2e_steps, 5)
     print(json.dumps(out), flush=True)
     return 0
 

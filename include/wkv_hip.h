@@ -162,6 +162,36 @@ int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, cons
                                void* grad_b, float* grad_s0, int64_t B, int64_t T, int64_t H,
                                int64_t N, int dtype, void* stream);
 
+/* Bytes of the sequence-LIF membrane checkpoints for these sizes: fp32
+ * [B][ceil(T/32)][C], the membrane at the start of every 32-step block. */
+size_t lif_checkpoint_bytes(int64_t B, int64_t T, int64_t C);
+
+/* Sequence LIF activation forward (SpikeGPT's spiking residual gate).
+ *
+ * Replaces the fused LIF launch inside SpikingSequenceLIF.forward
+ * (src/spikegpt/language.py:848-907, which calls the external myelin
+ * package's Triton kernels surrogate_lif_bf16io / the fp32 LIF function) and
+ * its eager fallback loop (language.py:908-918, step :813-840).  x and spikes:
+ * [B,T,C] in `dtype` (channels fastest, no [T,B,C] transpose); fp32 membrane
+ * starting at 0: h = m*decay + x, spike = [slope*(h - threshold) >= 0],
+ * m = h*(1 - spike) + reset*spike.  Spikes are exact 0/1.  membrane_checkpoint
+ * (may be NULL) receives lif_checkpoint_bytes() bytes for lif_backward.
+ * decay = 1 - 1/tau; slope > 0. */
+int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, int64_t B, int64_t T,
+                int64_t C, float decay, float threshold, float reset, float slope, int dtype,
+                void* stream);
+
+/* Sequence LIF backward: grad_x [B,T,C] in `dtype` from x, grad_spikes and the
+ * forward's membrane checkpoints, with the arctan surrogate derivative
+ * ds/dh = slope * 0.5 / (1 + (pi/2 * slope*(h - threshold))^2) and the reset
+ * path differentiated (autograd through language.py:833-839).  The
+ * surrogate's exact form lives in the external myelin package, absent from
+ * the reference tree; this is SpikingJelly's ATan surrogate with alpha =
+ * slope. */
+int lif_backward(const void* x, const void* grad_spikes, const float* membrane_checkpoint,
+                 void* grad_x, int64_t B, int64_t T, int64_t C, float decay, float threshold,
+                 float reset, float slope, int dtype, void* stream);
+
 /* Measurement hook; no counterpart in the reference.  Arms two HIP events
  * (hipEvent_t, created with timing enabled; either may be NULL) for the next
  * entry point called on this thread: its first kernel dispatch records

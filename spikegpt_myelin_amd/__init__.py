@@ -9,11 +9,16 @@ spikegpt_myelin_amd.build``):
   I/O) -- the reference's op names and schemas;
 * ``myelin::wkv_decode_step`` -- one-token WKV state update for generation;
 * ``myelin::wkv7_forward`` / ``myelin::wkv7_backward`` -- RWKV-7 DPLR
-  recurrence (the forward is differentiable).
+  recurrence (the forward is differentiable);
+* ``myelin::lif_sequence_forward`` / ``myelin::lif_sequence_backward`` -- the
+  sequence LIF spiking activation (differentiable).
+
+:mod:`spikegpt_myelin_amd.model` holds the SpikeGPT model built on them.
 """
 
 from .decode import initial_wkv_state, wkv_decode_step
 from .language import validate_wkv_inputs, weighted_key_value
+from .lif import lif_sequence
 from .wkv import (
     weighted_key_value_hip,
     weighted_key_value_hip_bf16io,
@@ -24,6 +29,7 @@ from .wkv7 import wkv7_backward, wkv7_forward
 
 __all__ = [
     "initial_wkv_state",
+    "lif_sequence",
     "validate_wkv_inputs",
     "weighted_key_value",
     "weighted_key_value_hip",

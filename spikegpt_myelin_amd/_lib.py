@@ -32,6 +32,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
+_F = ctypes.c_float
 SIGNATURES = {
     "wkv4_forward": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _INT]),
@@ -61,6 +62,15 @@ SIGNATURES = {
     "wkv7_backward_checkpointed": (
         _INT,
         [_P] * 16 + [_I64, _I64, _I64, _I64, _INT, _P],
+    ),
+    "lif_checkpoint_bytes": (_SZ, [_I64, _I64, _I64]),
+    "lif_forward": (
+        _INT,
+        [_P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
+    ),
+    "lif_backward": (
+        _INT,
+        [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
     ),
     "wkv_time_next_call": (_INT, [_P, _P]),
     "wkv_last_error_string": (ctypes.c_char_p, []),

@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <cmath>
 #include <initializer_list>
 #include <string>
 
@@ -90,6 +91,11 @@ int wkv7_backward_ck_impl(const void*, const void*, const void*, const void*, co
                           const void*, const void*, const float*, const float*, void*, void*,
                           void*, void*, void*, void*, float*, int, int, int, int, hipStream_t);
 size_t wkv7_checkpoint_floats(int64_t, int64_t, int64_t);
+size_t lif_checkpoint_floats(int64_t, int64_t, int64_t);
+int lif_forward_impl(const void*, void*, float*, int, int, int, float, float, float, float, int,
+                     hipStream_t);
+int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
+                      float, float, int, hipStream_t);
 
 static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }
 
@@ -361,6 +367,54 @@ int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, cons
   return wkv7_backward_ck_impl(r, w, k, v, a, b, grad_y, checkpoint, grad_s_out, grad_r, grad_w,
                                grad_k, grad_v, grad_a, grad_b, grad_s0, int(B), int(T), int(H),
                                dtype, static_cast<hipStream_t>(stream));
+}
+
+size_t lif_checkpoint_bytes(int64_t B, int64_t T, int64_t C) {
+  if (!dims_ok(B, T, C)) return 0;
+  return lif_checkpoint_floats(B, T, C) * sizeof(float);
+}
+
+static bool lif_params_ok(float decay, float threshold, float reset, float slope) {
+  return std::isfinite(decay) && std::isfinite(threshold) && std::isfinite(reset) &&
+         std::isfinite(slope) && slope > 0.f;
+}
+
+int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, int64_t B, int64_t T,
+                int64_t C, float decay, float threshold, float reset, float slope, int dtype,
+                void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: bad sizes");
+  if (!lif_params_ok(decay, threshold, reset, slope))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "lif_forward: parameters must be finite and surrogate_slope positive");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!x || !spikes) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: null pointer");
+  if (!aligned16({x, spikes, membrane_checkpoint}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: tensors must be 16-byte aligned");
+  return lif_forward_impl(x, spikes, membrane_checkpoint, int(B), int(T), int(C), decay, threshold,
+                          reset, slope, dtype, static_cast<hipStream_t>(stream));
+}
+
+int lif_backward(const void* x, const void* grad_spikes, const float* membrane_checkpoint,
+                 void* grad_x, int64_t B, int64_t T, int64_t C, float decay, float threshold,
+                 float reset, float slope, int dtype, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: bad sizes");
+  if (!lif_params_ok(decay, threshold, reset, slope))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "lif_backward: parameters must be finite and surrogate_slope positive");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!x || !grad_spikes || !membrane_checkpoint || !grad_x)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: null pointer");
+  if (!aligned16({x, grad_spikes, membrane_checkpoint, grad_x}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: tensors must be 16-byte aligned");
+  return lif_backward_impl(x, grad_spikes, membrane_checkpoint, grad_x, int(B), int(T), int(C),
+                           decay, threshold, reset, slope, dtype,
+                           static_cast<hipStream_t>(stream));
 }
 
 int wkv_time_next_call(void* start_event, void* stop_event) {

@@ -1,0 +1,130 @@
+"""Sequence LIF activation as custom ops served by the gfx950 HIP kernels.
+
+The reference's ``SpikingSequenceLIF.forward`` (``src/spikegpt/language.py:848-918``)
+runs the leaky integrate-and-fire recurrence over ``[B, T, C]`` through the
+external ``myelin`` package's Triton kernels (``surrogate_lif_bf16io`` for
+16-bit inputs, a store-all fp32 function otherwise) after moving time to the
+front (``[T, B, C]`` copies), or through an eager per-step loop
+(``language.py:813-840``).  Here one HIP kernel walks ``[B, T, C]`` in place:
+
+``myelin::lif_sequence_forward(Tensor x, float decay, float threshold,
+float reset, float slope) -> (Tensor spikes, Tensor checkpoint)`` -- spikes in
+``x.dtype`` (exact 0/1), fp32 membrane, plus the membrane at every 32-step
+block start for the backward;
+
+``myelin::lif_sequence_backward(Tensor grad_spikes, Tensor x, Tensor
+checkpoint, float decay, float threshold, float reset, float slope) -> Tensor``
+-- ``dL/dx`` with the arctan surrogate derivative
+``slope * 0.5 / (1 + (pi/2 * slope * (h - threshold))^2)`` and the reset path
+differentiated, as autograd does through the reference's eager step.
+
+The surrogate's exact definition lives in ``myelin`` (not part of the
+reference tree and not installed); the form used here is SpikingJelly's ATan
+surrogate with ``alpha = surrogate_slope``.  Spikes and membranes do not
+depend on it; input gradients do.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+CKPT_BLOCK = 32  # steps per membrane checkpoint
+_NATIVE = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def checkpoint_shape(b: int, t: int, c: int) -> tuple[int, int, int]:
+    return (b, (t + CKPT_BLOCK - 1) // CKPT_BLOCK, c)
+
+
+def _native(x: Tensor) -> Tensor:
+    return _lib.aligned(x if x.dtype in _NATIVE else x.float())
+
+
+@torch.library.custom_op("myelin::lif_sequence_forward", mutates_args=())
+def _lif_forward(
+    x: Tensor, decay: float, threshold: float, reset: float, slope: float
+) -> tuple[Tensor, Tensor]:
+    _lib.require_gpu(x)
+    if x.ndim != 3:
+        raise ValueError(f"inputs must have shape [B, T, C]; got {x.shape}")
+    b, t, c = x.shape
+    xs = _native(x)
+    spikes = torch.empty_like(xs)
+    ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    rc = _lib.timed("lif_forward", x.device, lambda: lib.lif_forward(
+        xs.data_ptr(), spikes.data_ptr(), ck.data_ptr(), b, t, c, decay, threshold, reset, slope,
+        _lib.dtype_code(xs.dtype), _lib.stream_of(xs),
+    ))
+    _lib.check(rc, "lif_forward")
+    return spikes, ck
+
+
+@_lif_forward.register_fake
+def _(x, decay, threshold, reset, slope):
+    b, t, c = x.shape
+    dt = x.dtype if x.dtype in _NATIVE else torch.float32
+    return (
+        torch.empty(x.shape, dtype=dt, device=x.device),
+        torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=x.device),
+    )
+
+
+@torch.library.custom_op("myelin::lif_sequence_backward", mutates_args=())
+def _lif_backward(
+    grad_spikes: Tensor, x: Tensor, checkpoint: Tensor, decay: float, threshold: float,
+    reset: float, slope: float,
+) -> Tensor:
+    _lib.require_gpu(grad_spikes, x, checkpoint)
+    b, t, c = x.shape
+    xs = _native(x)
+    gs = _lib.aligned(grad_spikes.to(xs.dtype))
+    ck = _lib.aligned(checkpoint)
+    gx = torch.empty_like(xs)
+    lib = _lib.load()
+    rc = _lib.timed("lif_backward", x.device, lambda: lib.lif_backward(
+        xs.data_ptr(), gs.data_ptr(), ck.data_ptr(), gx.data_ptr(), b, t, c, decay, threshold,
+        reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs),
+    ))
+    _lib.check(rc, "lif_backward")
+    return gx
+
+
+@_lif_backward.register_fake
+def _(grad_spikes, x, checkpoint, decay, threshold, reset, slope):
+    dt = x.dtype if x.dtype in _NATIVE else torch.float32
+    return torch.empty(x.shape, dtype=dt, device=x.device)
+
+
+def _setup_context(ctx, inputs, output):
+    x, decay, threshold, reset, slope = inputs
+    _, ck = output
+    ctx.save_for_backward(x, ck)
+    ctx.params = (decay, threshold, reset, slope)
+    ctx.mark_non_differentiable(ck)
+    ctx.set_materialize_grads(False)
+
+
+def _backward(ctx, grad_spikes, _grad_ck):
+    x, ck = ctx.saved_tensors
+    if grad_spikes is None:
+        return None, None, None, None, None
+    gx = torch.ops.myelin.lif_sequence_backward(grad_spikes, x, ck, *ctx.params)
+    return gx.to(x.dtype), None, None, None, None
+
+
+_lif_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+def lif_sequence(
+    x: Tensor, *, tau: float = 2.0, threshold: float = 1.0, reset: float = 0.0,
+    surrogate_slope: float = 2.0,
+) -> Tensor:
+    """Spikes of the LIF recurrence over ``[B, T, C]`` (``x.dtype``), differentiable."""
+    spikes, _ = torch.ops.myelin.lif_sequence_forward(
+        x, 1.0 - 1.0 / tau, float(threshold), float(reset), float(surrogate_slope)
+    )
+    return spikes if spikes.dtype == x.dtype else spikes.to(x.dtype)

@@ -1,0 +1,257 @@
+"""SpikeGPT language model around the HIP WKV and LIF kernels.
+
+Host-side mirror of the reference model (``src/spikegpt/language.py``) for the
+training and evaluation path: same class names, constructor arguments,
+parameter names and initialisation, so that a state dict moves between the
+two.  Every sequential recurrence runs in the gfx950 kernels -- the WKV time
+mix through ``myelin::wkv_forward{,_bf16io}`` (``SpikeTimeMix.forward``,
+``language.py:1015-1036``) and the spiking activations through
+``myelin::lif_sequence_forward`` (``SpikingSequenceLIF.forward``,
+``language.py:848-918``); linear layers, layer norms and the loss are
+PyTorch-ROCm (hipBLASLt GEMMs).
+
+Supported configuration: ``model_type="rwkv"``, ``attention="rwkv"``,
+``spike_input=False`` (the reference defaults, ``language.py:234-256``).
+Other variants raise ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from .language import weighted_key_value
+from .lif import lif_sequence
+
+
+@dataclass
+class SpikeGPTConfig:
+    """``SpikeGPTConfig`` of ``language.py:234-281`` (same fields and defaults)."""
+
+    vocab_size: int
+    context_length: int
+    n_layer: int = 4
+    n_embd: int = 128
+    dropout: float = 0.03
+    model_type: str = "rwkv"
+    attention: str = "rwkv"
+    n_head: int = 8
+    rope_base: float = 10000.0
+    lif_tau: float = 2.0
+    lif_threshold: float = 1.0
+    lif_reset: float = 0.0
+    surrogate_slope: float = 2.0
+    spike_embedding: bool = True
+    spiking: bool = True
+    spike_input: bool = False
+    gradient_checkpointing: bool = False
+
+    def validate(self) -> None:
+        if self.vocab_size <= 0:
+            raise ValueError("vocab_size must be positive")
+        if self.context_length <= 0:
+            raise ValueError("context_length must be positive")
+        if self.n_layer <= 0:
+            raise ValueError("n_layer must be positive")
+        if self.n_embd <= 0:
+            raise ValueError("n_embd must be positive")
+        if self.dropout < 0.0 or self.dropout >= 1.0:
+            raise ValueError("dropout must be in [0, 1)")
+        if self.lif_tau <= 0.0:
+            raise ValueError("lif_tau must be positive")
+        if self.model_type != "rwkv" or self.attention != "rwkv" or self.spike_input:
+            raise NotImplementedError(
+                "this build serves model_type='rwkv', attention='rwkv', spike_input=False"
+            )
+
+
+class _HeavisideAtan(torch.autograd.Function):
+    """Hard spike with the arctan surrogate gradient (the embedding spike of
+    ``language.py:1386-1394``): forward ``[x >= 0]``, backward
+    ``0.5 / (1 + (pi/2 x)^2)``."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor) -> Tensor:  # noqa: D102
+        ctx.save_for_backward(x)
+        return (x >= 0).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor) -> Tensor:  # noqa: D102
+        (x,) = ctx.saved_tensors
+        q = (torch.pi / 2) * x.float()
+        return (grad.float() * (0.5 / (1.0 + q * q))).to(grad.dtype)
+
+
+def _time_shift(inputs: Tensor) -> Tensor:
+    """``language.py:344-345``: the previous token's features (zeros at t=0)."""
+    return F.pad(inputs[:, :-1], (0, 0, 1, 0))
+
+
+def _mix_with_previous(inputs: Tensor, mix: Tensor) -> Tensor:
+    """``language.py:348-353``."""
+    return inputs * mix + _time_shift(inputs) * (1.0 - mix)
+
+
+class SpikingSequenceLIF(nn.Module):
+    """``language.py:766-918``: LIF over ``[B, T, C]`` in one HIP kernel."""
+
+    def __init__(self, *, tau: float = 2.0, threshold: float = 1.0, reset: float = 0.0,
+                 surrogate_slope: float = 2.0) -> None:
+        super().__init__()
+        if tau <= 0.0:
+            raise ValueError("tau must be positive")
+        self.tau = tau
+        self.threshold = threshold
+        self.reset = reset
+        self.surrogate_slope = surrogate_slope
+
+    @property
+    def decay(self) -> float:
+        return 1.0 - (1.0 / self.tau)
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        if inputs.ndim != 3:
+            raise ValueError(f"inputs must have shape [B, T, C]; got {inputs.shape}")
+        return lif_sequence(inputs, tau=self.tau, threshold=self.threshold, reset=self.reset,
+                            surrogate_slope=self.surrogate_slope)
+
+
+class SpikeTimeMix(nn.Module):
+    """``language.py:921-1036``: token-shift mixes, k/v/r projections, WKV,
+    ``sigmoid(r) * wkv`` and the output projection."""
+
+    def __init__(self, n_embd: int, n_layer: int, layer_id: int) -> None:
+        super().__init__()
+        if n_embd <= 0:
+            raise ValueError("n_embd must be positive")
+        attn = n_embd
+        ratio_0_to_1 = layer_id / max(1, n_layer - 1)
+        ratio_1_to_almost0 = 1.0 - (layer_id / n_layer)
+        position = torch.arange(n_embd, dtype=torch.float32) / n_embd
+        # Initialisation of language.py:938-950.
+        decay_speed = -5.0 + 8.0 * torch.pow(
+            torch.arange(attn, dtype=torch.float32) / max(1, attn - 1), 0.7 + 1.3 * ratio_0_to_1
+        )
+        zigzag = torch.tensor([(i + 1) % 3 - 1 for i in range(attn)], dtype=torch.float32)
+        self.time_decay = nn.Parameter(decay_speed)
+        self.time_first = nn.Parameter(torch.ones(attn) * -1.2039728 + zigzag * 0.5)
+        self.time_mix_k = nn.Parameter(torch.pow(position, ratio_1_to_almost0).view(1, 1, -1))
+        self.time_mix_v = nn.Parameter(
+            (torch.pow(position, ratio_1_to_almost0) + 0.3 * ratio_0_to_1).view(1, 1, -1)
+        )
+        self.time_mix_r = nn.Parameter(torch.pow(position, 0.5 * ratio_1_to_almost0).view(1, 1, -1))
+        self.key = nn.Linear(n_embd, attn, bias=False)
+        self.value = nn.Linear(n_embd, attn, bias=False)
+        self.receptance = nn.Linear(n_embd, attn, bias=False)
+        self.output = nn.Linear(attn, n_embd, bias=False)
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        key = self.key(_mix_with_previous(inputs, self.time_mix_k))
+        value = self.value(_mix_with_previous(inputs, self.time_mix_v))
+        receptance = torch.sigmoid(self.receptance(_mix_with_previous(inputs, self.time_mix_r)))
+        wkv = weighted_key_value(key, value, self.time_decay, self.time_first)
+        return self.output(receptance * wkv)
+
+
+class SpikeChannelMix(nn.Module):
+    """``language.py:1145-1196``: squared-ReLU feed-forward with a receptance gate."""
+
+    def __init__(self, n_embd: int, n_layer: int, layer_id: int) -> None:
+        super().__init__()
+        ratio_1_to_almost0 = 1.0 - (layer_id / n_layer)
+        position = torch.arange(n_embd, dtype=torch.float32) / n_embd
+        self.time_mix_k = nn.Parameter(torch.pow(position, ratio_1_to_almost0).view(1, 1, -1))
+        self.time_mix_r = nn.Parameter(torch.pow(position, ratio_1_to_almost0).view(1, 1, -1))
+        self.key = nn.Linear(n_embd, 4 * n_embd, bias=False)
+        self.receptance = nn.Linear(n_embd, n_embd, bias=False)
+        self.value = nn.Linear(4 * n_embd, n_embd, bias=False)
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        key = torch.relu(self.key(_mix_with_previous(inputs, self.time_mix_k))).square()
+        receptance = torch.sigmoid(self.receptance(_mix_with_previous(inputs, self.time_mix_r)))
+        return receptance * self.value(key)
+
+
+class SpikeGPTBlock(nn.Module):
+    """``language.py:1223-1360``: ``x + LIF(att(ln1 x))``, then ``+ LIF(ffn(ln2 x))``."""
+
+    def __init__(self, config: SpikeGPTConfig, layer_id: int) -> None:
+        super().__init__()
+        self.config = config
+        self.layer_id = layer_id
+        self.ln0 = nn.LayerNorm(config.n_embd) if layer_id == 0 else None
+        self.ln1 = nn.LayerNorm(config.n_embd)
+        self.ln2 = nn.LayerNorm(config.n_embd)
+        self.att = SpikeTimeMix(config.n_embd, config.n_layer, layer_id)
+        self.ffn = SpikeChannelMix(config.n_embd, config.n_layer, layer_id)
+
+        def make_lif() -> nn.Module:
+            if not config.spiking:
+                return nn.Identity()
+            return SpikingSequenceLIF(tau=config.lif_tau, threshold=config.lif_threshold,
+                                      reset=config.lif_reset,
+                                      surrogate_slope=config.surrogate_slope)
+
+        self.lif1 = make_lif()
+        self.lif2 = make_lif()
+        self.dropout = nn.Dropout(config.dropout)
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        residual = self.ln0(inputs) if self.ln0 is not None else inputs
+        residual = residual + self.lif1(self.att(self.ln1(residual)))
+        residual = residual + self.lif2(self.ffn(self.ln2(residual)))
+        return self.dropout(residual)
+
+
+class SpikeLanguageModel(nn.Module):
+    """``language.py:1363-1480``: spiking embedding, blocks, ``ln_out``, head."""
+
+    def __init__(self, config: SpikeGPTConfig) -> None:
+        super().__init__()
+        config.validate()
+        self.config = config
+        self.embedding = nn.Embedding(config.vocab_size, config.n_embd)
+        self.blocks = nn.ModuleList(SpikeGPTBlock(config, i) for i in range(config.n_layer))
+        self.ln_out = nn.LayerNorm(config.n_embd)
+        self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
+        self.apply(self._init_weights)
+
+    @staticmethod
+    def _init_weights(module: nn.Module) -> None:
+        # language.py:1378-1384
+        if isinstance(module, nn.Embedding):
+            nn.init.normal_(module.weight, mean=0.0, std=1.0e-3)
+        elif isinstance(module, nn.Linear):
+            nn.init.normal_(module.weight, mean=0.0, std=0.01)
+            if module.bias is not None:
+                nn.init.zeros_(module.bias)
+
+    def embed_tokens(self, input_ids: Tensor) -> Tensor:
+        embeddings = self.embedding(input_ids)
+        if not self.config.spike_embedding:
+            return embeddings
+        return _HeavisideAtan.apply(self.config.surrogate_slope * embeddings)
+
+    def forward(self, input_ids: Tensor, targets: Tensor | None = None):
+        if input_ids.ndim != 2:
+            raise ValueError(f"input_ids must have shape [B, T]; got {input_ids.shape}")
+        if input_ids.shape[1] > self.config.context_length:
+            raise ValueError(
+                "input sequence length exceeds context_length; "
+                f"got {input_ids.shape[1]} and {self.config.context_length}"
+            )
+        hidden = self.embed_tokens(input_ids)
+        for block in self.blocks:
+            hidden = block(hidden)
+        if targets is None:
+            return self.head(self.ln_out(hidden))
+        return self.loss_tail(hidden, targets)
+
+    def loss_tail(self, hidden: Tensor, targets: Tensor) -> tuple[Tensor, Tensor]:
+        """``language.py:1469-1480``: ``ln_out -> head -> cross_entropy``."""
+        logits = self.head(self.ln_out(hidden))
+        loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1))
+        return loss, logits

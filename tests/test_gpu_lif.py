@@ -1,0 +1,127 @@
+"""GPU parity of the sequence-LIF kernels against the CPU oracle.
+
+Bars (written per test):
+* spikes: bit-exact against the reference loop evaluated in float32 on the
+  same (widened) inputs -- the kernel does the loop's float32 operations in
+  the same order, so membranes and spikes agree exactly;
+* dL/dx, fp32 I/O: ``rtol=1e-5`` with ``atol=1e-5 * max|ref|`` against the
+  float64 reverse recurrence over the float32 forward's spike pattern;
+* dL/dx, bf16/fp16 I/O: ``rtol=2e-2, atol=1e-2 * max|ref|``.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import lif as L
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float32: (1e-5, 1e-5), torch.bfloat16: (2e-2, 1e-2), torch.float16: (2e-2, 1e-2)}
+
+
+def _ops():
+    import spikegpt_myelin_amd  # noqa: F401
+
+    return torch.ops.myelin
+
+
+def _inputs(b, t, c, dtype, seed=0, scale=1.5):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(b, t, c, generator=g) * scale).to(dtype)
+    gs = torch.randn(b, t, c, generator=g).to(dtype)
+    return x, gs
+
+
+def _check_grad(got, ref, dtype, what):
+    rtol, atol_scale = TOL[dtype]
+    got = got.double().cpu()
+    ref = ref.double()
+    atol = atol_scale * max(float(ref.abs().max()) if ref.numel() else 0.0, 1.0)
+    err = float((got - ref).abs().max()) if ref.numel() else 0.0
+    assert torch.allclose(got, ref, rtol=rtol, atol=atol), f"{what}: max abs err {err:.3e}"
+
+
+def _run(x, gs, tau=2.0, threshold=1.0, reset=0.0, slope=2.0):
+    ops = _ops()
+    decay = 1.0 - 1.0 / tau
+    xd = x.to(DEV)
+    spikes, ck = ops.lif_sequence_forward(xd, decay, threshold, reset, slope)
+    gx = ops.lif_sequence_backward(gs.to(DEV), xd, ck, decay, threshold, reset, slope)
+    torch.cuda.synchronize()
+    return spikes.cpu(), gx.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(3, 1, 96), (3, 7, 96), (2, 64, 128), (2, 100, 70),
+                                   (1, 33, 129), (4, 257, 256)])
+def test_forward_and_backward_match_oracle(dtype, shape):
+    b, t, c = shape
+    x, gs = _inputs(b, t, c, dtype, seed=b * 1000 + t + c)
+    spikes, gx = _run(x, gs)
+    ref_s = L.lif_loop(x.float()).to(dtype)
+    assert spikes.dtype == dtype
+    assert torch.equal(spikes, ref_s), f"spikes differ at {shape} {dtype}"
+    ref_g = L.lif_reverse(x.float(), gs.float(), forward_dtype=torch.float32)
+    _check_grad(gx, ref_g, dtype, f"grad_x {shape} {dtype}")
+
+
+@pytest.mark.parametrize("params", [dict(tau=3.0, threshold=0.7, reset=-0.25, slope=1.5),
+                                    dict(tau=1.25, threshold=1.2, reset=0.1, slope=4.0)])
+def test_neuron_parameters(params):
+    x, gs = _inputs(2, 130, 192, torch.float32, seed=7)
+    spikes, gx = _run(x, gs, **params)
+    assert torch.equal(spikes, L.lif_loop(x, params["tau"], params["threshold"], params["reset"],
+                                          params["slope"]))
+    ref_g = L.lif_reverse(x, gs, params["tau"], params["threshold"], params["reset"],
+                          params["slope"], forward_dtype=torch.float32)
+    _check_grad(gx, ref_g, torch.float32, f"grad_x {params}")
+
+
+def test_autograd_through_the_op_and_module():
+    from spikegpt_myelin_amd import lif_sequence
+    from spikegpt_myelin_amd.model import SpikingSequenceLIF
+
+    x, gs = _inputs(2, 90, 160, torch.bfloat16, seed=11)
+    xd = x.to(DEV).requires_grad_(True)
+    s = SpikingSequenceLIF(tau=2.0)(xd)
+    (gx,) = torch.autograd.grad(s, xd, gs.to(DEV))
+    assert torch.equal(s.detach().cpu(), L.lif_loop(x.float()).to(torch.bfloat16))
+    _check_grad(gx, L.lif_reverse(x.float(), gs.float(), forward_dtype=torch.float32),
+                torch.bfloat16, "module grad")
+    # The functional form gives the same bits.
+    s2 = lif_sequence(xd.detach())
+    assert torch.equal(s2, s.detach())
+
+
+def test_empty_inputs():
+    ops = _ops()
+    for shape in [(0, 5, 8), (2, 0, 8), (2, 5, 0)]:
+        x = torch.zeros(shape, device=DEV)
+        s, ck = ops.lif_sequence_forward(x, 0.5, 1.0, 0.0, 2.0)
+        assert s.shape == x.shape
+        gx = ops.lif_sequence_backward(torch.zeros_like(x), x, ck, 0.5, 1.0, 0.0, 2.0)
+        assert gx.shape == x.shape
+
+
+def test_bad_parameters_raise():
+    ops = _ops()
+    x = torch.zeros(1, 4, 8, device=DEV)
+    with pytest.raises(RuntimeError, match="surrogate_slope positive"):
+        ops.lif_sequence_forward(x, 0.5, 1.0, 0.0, 0.0)
+    with pytest.raises(ValueError, match=r"\[B, T, C\]"):
+        ops.lif_sequence_forward(torch.zeros(4, 8, device=DEV), 0.5, 1.0, 0.0, 2.0)
+
+
+def test_benchmark_shape_full_size():
+    # B=64, T=1024, C=512 bf16 (the 41M model's activation shape; two
+    # channels per lane): exact spikes and gradients against the oracle.
+    x, gs = _inputs(64, 1024, 512, torch.bfloat16, seed=3, scale=1.0)
+    spikes, gx = _run(x, gs)
+    assert torch.equal(spikes, L.lif_loop(x.float()).to(torch.bfloat16))
+    rate = float(spikes.float().mean())
+    assert 0.01 < rate < 0.9
+    _check_grad(gx, L.lif_reverse(x.float(), gs.float(), forward_dtype=torch.float32),
+                torch.bfloat16, "grad_x full size")
