@@ -28,7 +28,8 @@ Reported beside the throughput:
 Other workloads (``--workload``): ``long`` (B=24, T=3072, C=512), ``216m``
 (B=16, T=1024, C=768, 18 layers), ``decode`` (B=256, C=768, 18 layers, fp32
 state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward + backward), ``c0``
-(fp32 forward B=2, T=128, C=512), ``e2e41m`` (the whole 41M SpikeGPT
+(fp32 forward B=2, T=128, C=512), ``lif`` (sequence LIF forward + backward, B=64, T=1024, C=512 bf16),
+``e2e41m`` (the whole 41M SpikeGPT
 training step, 12 layers x 512, vocab 256, B=64, T=1024; the default run
 also reports it as ``e2e_train_step``).
 
@@ -426,6 +427,95 @@ def bench_wkv7(args) -> dict:
     }
 
 
+def bench_lif(args) -> dict:
+    """Sequence LIF forward (with membrane checkpoints) + backward through the
+    C ABI on preallocated buffers: B=64, T=1024, C=512 bf16 (the 41M model's
+    activation shape), tau 2, threshold 1, reset 0, slope 2."""
+    import spikegpt_myelin_amd  # noqa: F401
+    from spikegpt_myelin_amd import _lib
+    from spikegpt_myelin_amd.lif import checkpoint_shape
+    from oracle import lif as L
+
+    B, T, C = 64, 1024, 512
+    decay, thr, reset, slope = 0.5, 1.0, 0.0, 2.0
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(B, T, C, generator=g).to(torch.bfloat16).to(dev)
+    gs = torch.randn(B, T, C, generator=g).to(torch.bfloat16).to(dev)
+    spk = torch.empty_like(x)
+    gx = torch.empty_like(x)
+    ck = torch.empty(checkpoint_shape(B, T, C), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    code = _lib.dtype_code(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    xp, spkp, ckp, gsp, gxp = (t.data_ptr() for t in (x, spk, ck, gs, gx))
+
+    def fwd():
+        _lib.check(lib.lif_forward(xp, spkp, ckp, B, T, C, decay, thr, reset, slope, code, sp),
+                   "lif forward")
+
+    def bwd():
+        _lib.check(lib.lif_backward(xp, gsp, ckp, gxp, B, T, C, decay, thr, reset, slope, code, sp),
+                   "lif backward")
+
+    pool = EventPool(4 * args.steps, stream)
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    evs = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        fwd()
+        if i % args.event_every == 0:
+            s_ev, e_ev = pool.take(), pool.take()
+            _lib.arm_events(s_ev, e_ev)
+            bwd()
+            evs.append((s_ev, e_ev))
+        else:
+            bwd()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    bwd_t = statistics.mean(s.elapsed_time(e) * 1e-3 for s, e in evs)
+    step_s = elapsed / args.steps
+    n = B * T * C
+    bwd_bytes = 6 * n  # x, grad_spikes read; grad_x written (bf16)
+    achieved = bwd_bytes / bwd_t / 1e9
+    out = {
+        "metric": "sequence LIF fwd+bwd tokens/sec, B=64 T=1024 C=512 bf16",
+        "value": B * T / step_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "lif_fwd_bwd", "B": B, "T": T, "C": C, "io_dtype": "bfloat16",
+                   "state_dtype": "float32", "tau": 2.0, "threshold": thr, "reset": reset,
+                   "slope": slope},
+        "hbm_gbps_algorithmic": 10 * n / step_s / 1e9,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "lif_bwd_kernel",
+                     "algorithmic_bytes_per_launch": bwd_bytes, "avg_launch_us": bwd_t * 1e6},
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(os.cpu_count() or 1)
+        bs = min(B, args.cpu_sample_batch)
+        xc = x[:bs].float().cpu().requires_grad_(True)
+        gc = gs[:bs].float().cpu()
+        times = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            torch.autograd.grad(L.lif_loop(xc), xc, gc)
+            times.append(time.perf_counter() - t1)
+        med = statistics.median(times[1:])
+        out["cpu_baseline"] = {
+            "value": bs * T / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"B={bs} of {B}, T={T}, C={C}, fp32 eager LIF loop (language.py:813-840, "
+                       f"908-918) forward+autograd backward, median of 2 after 1 warmup; host "
+                       f"{_cpu_model()}"),
+        }
+    return out
+
+
 def bench_e2e(steps: int, warmup: int) -> dict:
     """The 41M SpikeGPT training step: 12 layers, 512 embedding, byte vocab
     (256), B=64, T=1024, random init, synthetic tokens, bf16 autocast, fused
@@ -477,7 +567,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--event-every", type=int, default=10,
                     help="time the dominant launch with HIP events on every N-th timed step")
-    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7", "e2e41m"])
+    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7", "lif", "e2e41m"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=20,
@@ -507,6 +597,8 @@ def main() -> int:
         out = bench_decode(args)
     elif args.workload == "wkv7":
         out = bench_wkv7(args)
+    elif args.workload == "lif":
+        out = bench_lif(args)
     elif args.workload == "e2e41m":
         out = bench_e2e(args.steps, args.warmup)
     else:

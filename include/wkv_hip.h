@@ -192,6 +192,37 @@ int lif_backward(const void* x, const void* grad_spikes, const float* membrane_c
                  void* grad_x, int64_t B, int64_t T, int64_t C, float decay, float threshold,
                  float reset, float slope, int dtype, void* stream);
 
+/* Bytes of device workspace token_shift_mix_backward needs for n mixing
+ * vectors (per-(batch, 64-step chunk) partial sums, fp32). */
+size_t token_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int64_t C);
+
+/* Fused token-shift mixing (the time-mix and channel-mix prologue).
+ *
+ * Replaces the eager _time_shift / _mix_with_previous of
+ * src/spikegpt/language.py:344-353 as SpikeTimeMix.forward (:1016-1018, n =
+ * 3: k, v, r) and SpikeChannelMix.forward (:1190-1191, n = 2: k, r) call it,
+ * together with autocast's cast of the result: for j < n,
+ *   out_j[b,t,c] = x[b,t,c] * mix[j][c] + x[b,t-1,c] * (1 - mix[j][c]),
+ * x[b,-1,c] = 0, in fp32 (products, then the sum), rounded once to
+ * out_dtype.  x [B,T,C] in x_dtype; mix [n][C] fp32; out0..out{n-1} [B,T,C]
+ * (unused ones NULL).  dtype pairs: (f32 -> f32|bf16|f16), (bf16 -> bf16),
+ * (f16 -> f16). */
+int token_shift_mix_forward(const void* x, int x_dtype, const float* mix, int64_t n, void* out0,
+                            void* out1, void* out2, int out_dtype, int64_t B, int64_t T,
+                            int64_t C, void* stream);
+
+/* Backward of token_shift_mix_forward: grad_x [B,T,C] in x_dtype,
+ *   grad_x[b,t,c] = sum_j g_j[b,t,c] mix[j][c] + g_j[b,t+1,c] (1 - mix[j][c]),
+ * and grad_mix [n][C] fp32, grad_mix[j][c] = sum_{b,t} g_j (x[t] - x[t-1])
+ * (summed in a fixed order).  grad0..grad{n-1} [B,T,C] in g_dtype (the
+ * output type of the forward, or x_dtype).  `workspace` must hold
+ * token_shift_mix_workspace_bytes() bytes. */
+int token_shift_mix_backward(const void* x, int x_dtype, const float* mix, int64_t n,
+                             const void* grad0, const void* grad1, const void* grad2, int g_dtype,
+                             void* grad_x, float* grad_mix, void* workspace,
+                             size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                             void* stream);
+
 /* Measurement hook; no counterpart in the reference.  Arms two HIP events
  * (hipEvent_t, created with timing enabled; either may be NULL) for the next
  * entry point called on this thread: its first kernel dispatch records

@@ -11,7 +11,9 @@ spikegpt_myelin_amd.build``):
 * ``myelin::wkv7_forward`` / ``myelin::wkv7_backward`` -- RWKV-7 DPLR
   recurrence (the forward is differentiable);
 * ``myelin::lif_sequence_forward`` / ``myelin::lif_sequence_backward`` -- the
-  sequence LIF spiking activation (differentiable).
+  sequence LIF spiking activation (differentiable);
+* ``myelin::token_shift_mix`` / ``myelin::token_shift_mix_backward`` -- the
+  fused token-shift mixing that feeds the block projections (differentiable).
 
 :mod:`spikegpt_myelin_amd.model` holds the SpikeGPT model built on them.
 """
@@ -19,6 +21,7 @@ spikegpt_myelin_amd.build``):
 from .decode import initial_wkv_state, wkv_decode_step
 from .language import validate_wkv_inputs, weighted_key_value
 from .lif import lif_sequence
+from .timemix import token_shift_mix
 from .wkv import (
     weighted_key_value_hip,
     weighted_key_value_hip_bf16io,
@@ -30,6 +33,7 @@ from .wkv7 import wkv7_backward, wkv7_forward
 __all__ = [
     "initial_wkv_state",
     "lif_sequence",
+    "token_shift_mix",
     "validate_wkv_inputs",
     "weighted_key_value",
     "weighted_key_value_hip",

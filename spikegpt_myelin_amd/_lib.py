@@ -72,6 +72,15 @@ SIGNATURES = {
         _INT,
         [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
     ),
+    "token_shift_mix_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "token_shift_mix_forward": (
+        _INT,
+        [_P, _INT, _P, _I64, _P, _P, _P, _INT, _I64, _I64, _I64, _P],
+    ),
+    "token_shift_mix_backward": (
+        _INT,
+        [_P, _INT, _P, _I64, _P, _P, _P, _INT, _P, _P, _P, _SZ, _I64, _I64, _I64, _P],
+    ),
     "wkv_time_next_call": (_INT, [_P, _P]),
     "wkv_last_error_string": (ctypes.c_char_p, []),
     "wkv_version": (ctypes.c_char_p, []),

@@ -92,6 +92,11 @@ int wkv7_backward_ck_impl(const void*, const void*, const void*, const void*, co
                           void*, void*, void*, void*, float*, int, int, int, int, hipStream_t);
 size_t wkv7_checkpoint_floats(int64_t, int64_t, int64_t);
 size_t lif_checkpoint_floats(int64_t, int64_t, int64_t);
+size_t shift_mix_partial_floats(int64_t, int64_t, int64_t, int64_t);
+int shift_mix_forward_impl(const void*, int, const float*, void* const*, int, int, int, int, int,
+                           hipStream_t);
+int shift_mix_backward_impl(const void*, int, const float*, const void* const*, int, void*, float*,
+                            float*, int, int, int, int, hipStream_t);
 int lif_forward_impl(const void*, void*, float*, int, int, int, float, float, float, float, int,
                      hipStream_t);
 int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
@@ -415,6 +420,76 @@ int lif_backward(const void* x, const void* grad_spikes, const float* membrane_c
   return lif_backward_impl(x, grad_spikes, membrane_checkpoint, grad_x, int(B), int(T), int(C),
                            decay, threshold, reset, slope, dtype,
                            static_cast<hipStream_t>(stream));
+}
+
+size_t token_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int64_t C) {
+  if (n < 1 || n > 3 || !dims_ok(B, T, C)) return 0;
+  return shift_mix_partial_floats(n, B, T, C) * sizeof(float);
+}
+
+int token_shift_mix_forward(const void* x, int x_dtype, const float* mix, int64_t n, void* out0,
+                            void* out1, void* out2, int out_dtype, int64_t B, int64_t T,
+                            int64_t C, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: unknown dtype");
+  if (n < 1 || n > 3)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: 1 to 3 mixing vectors");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: bad sizes");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  void* const out[3] = {out0, out1, out2};
+  if (!x || !mix) return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: null pointer");
+  for (int j = 0; j < n; ++j) {
+    if (!out[j]) return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: null pointer");
+    if (!aligned16({out[j]}))
+      return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: tensors must be 16-byte aligned");
+  }
+  if (!aligned16({x, mix}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_forward: tensors must be 16-byte aligned");
+  return shift_mix_forward_impl(x, x_dtype, mix, out, out_dtype, int(n), int(B), int(T), int(C),
+                                static_cast<hipStream_t>(stream));
+}
+
+int token_shift_mix_backward(const void* x, int x_dtype, const float* mix, int64_t n,
+                             const void* grad0, const void* grad1, const void* grad2, int g_dtype,
+                             void* grad_x, float* grad_mix, void* workspace,
+                             size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                             void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(x_dtype) || !dtype_ok(g_dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: unknown dtype");
+  if (n < 1 || n > 3)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: 1 to 3 mixing vectors");
+  if (!dims_ok(B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: bad sizes");
+  if (C == 0) return WKV_OK;
+  if (B == 0 || T == 0) {
+    if (!grad_mix) return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: null pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int j = 0; j < n; j += 2) {
+      const int rc = wkv4_zero_param_grads(grad_mix + j * C, grad_mix + (j + 1 < n ? j + 1 : j) * C,
+                                           int(C), s);
+      if (rc) return rc;
+    }
+    return WKV_OK;
+  }
+  const void* const g[3] = {grad0, grad1, grad2};
+  if (!x || !mix || !grad_x || !grad_mix || !workspace)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: null pointer");
+  for (int j = 0; j < n; ++j) {
+    if (!g[j]) return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: null pointer");
+    if (!aligned16({g[j]}))
+      return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: tensors must be 16-byte aligned");
+  }
+  if (workspace_bytes < shift_mix_partial_floats(n, B, T, C) * sizeof(float))
+    return fail(WKV_ERR_WORKSPACE_TOO_SMALL, "token_shift_mix_backward: workspace too small");
+  if (!aligned16({x, mix, grad_x, grad_mix, workspace}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "token_shift_mix_backward: tensors must be 16-byte aligned");
+  return shift_mix_backward_impl(x, x_dtype, mix, g, g_dtype, grad_x,
+                                 static_cast<float*>(workspace), grad_mix, int(n), int(B), int(T),
+                                 int(C), static_cast<hipStream_t>(stream));
 }
 
 int wkv_time_next_call(void* start_event, void* stop_event) {

@@ -223,6 +223,233 @@ __global__ __launch_bounds__(64) void lif_bwd_kernel(const typename E::raw* __re
   }
 }
 
+// --------------------------------------------------- staged wide I/O ----
+// The kernels above issue one load per step per lane, so a wave has at most
+// ~63 row reads in flight (the vector-memory counter), about 4 MB over the
+// whole chip at B*C = 32768 -- too little to cover HBM latency.  The staged
+// kernels below keep one channel per lane for the arithmetic but move data
+// in 16-byte pieces: one wave instruction reads SPI consecutive steps of the
+// wave's 64-channel row (1 KiB), the pieces of P blocks ahead wait in
+// registers, and each 32-step block goes through LDS once to turn
+// [step][piece] into [channel][step] order (and back for the outputs).  A
+// wave then has P blocks (128-192 steps) in flight.  Requires C to be a
+// multiple of 16 / sizeof(element) (a piece never straddles two rows).
+// Byte offset beyond any descriptor the staged kernels build (their spans
+// are below 2^31 bytes, checked on the host): accesses there read zero and
+// stores are dropped.
+constexpr unsigned kOutOfRange = 0x80000000u;
+
+template <typename E>
+struct Staged {
+  using raw = typename E::raw;
+  static constexpr int kEs = int(sizeof(raw));
+  static constexpr int kLps = 4 * kEs;           // lanes (16-byte pieces) per step row
+  static constexpr int kSpi = 64 / kLps;         // steps per wave instruction
+  static constexpr int kInstr = kLifBlock / kSpi;  // instructions per block
+  // Blocks in flight (the vector-memory counter caps a wave at 63
+  // outstanding operations: per block the forward issues 2*kInstr + 1 and
+  // the backward 3*kInstr + 1).
+  static constexpr int kPf = kEs == 2 ? 6 : 3;
+  static constexpr int kPb = kEs == 2 ? 4 : 2;
+
+  // Per-lane byte offset of the lane's piece inside an instruction's span;
+  // pieces past the last channel get an out-of-range offset, so that their
+  // loads read zero and their stores are dropped by the descriptor check.
+  __device__ static __forceinline__ unsigned lane_off(int lane, int C, int cg) {
+    if (cg * 64 + (lane % kLps) * (16 / kEs) >= C) return kOutOfRange;
+    return unsigned(lane / kLps) * unsigned(C) * unsigned(kEs) + unsigned(lane % kLps) * 16u;
+  }
+
+  // Loads the kInstr pieces of block `blk` (steps past T, and blocks outside
+  // [0, nblk), read as zero).
+  __device__ static __forceinline__ void load(u32x4 (&st)[kInstr], const raw* __restrict__ p,
+                                              size_t row_base, size_t row_tail, unsigned loff,
+                                              int blk, int nblk, int C) {
+    const bool in = blk >= 0 && blk < nblk;
+    const int t0 = in ? blk * kLifBlock : 0;
+    const uint32_t bytes = in ? span_bytes(row_tail, t0, C, kEs) : 0u;
+    const rsrc_t r = make_rsrc(p + row_base + size_t(t0) * C, bytes);
+    const unsigned stride = unsigned(kSpi) * unsigned(C) * unsigned(kEs);
+#pragma unroll
+    for (int j = 0; j < kInstr; ++j)
+      st[j] = __builtin_amdgcn_raw_buffer_load_b128(r, loff, unsigned(j) * stride, 0);
+  }
+
+  __device__ static __forceinline__ void to_lds(u32x4* __restrict__ lds, const u32x4 (&st)[kInstr],
+                                                int lane) {
+#pragma unroll
+    for (int j = 0; j < kInstr; ++j) lds[j * 64 + lane] = st[j];
+  }
+
+  __device__ static __forceinline__ float get(const u32x4* __restrict__ lds, int s, int c) {
+    const raw v = reinterpret_cast<const raw*>(lds)[s * 64 + c];
+    if constexpr (__is_same(E, F32)) {
+      return v;
+    } else if constexpr (__is_same(E, BF16)) {
+      return bf16_bits_to_float(v);
+    } else {
+      return f16_bits_to_float(v);
+    }
+  }
+
+  __device__ static __forceinline__ void put(u32x4* __restrict__ lds, int s, int c, float v) {
+    store_scalar<E>(reinterpret_cast<raw*>(lds) + s * 64 + c, v);
+  }
+
+  // Writes block `blk` of an output from LDS (steps past T and pieces past
+  // C fall outside the descriptor and are dropped).
+  __device__ static __forceinline__ void store(raw* __restrict__ p, const u32x4* __restrict__ lds,
+                                               size_t row_base, size_t row_tail, unsigned loff,
+                                               int blk, int C, int lane) {
+    const int t0 = blk * kLifBlock;
+    const rsrc_t r = make_rsrc(p + row_base + size_t(t0) * C, span_bytes(row_tail, t0, C, kEs));
+    const unsigned stride = unsigned(kSpi) * unsigned(C) * unsigned(kEs);
+#pragma unroll
+    for (int j = 0; j < kInstr; ++j)
+      __builtin_amdgcn_raw_buffer_store_b128(lds[j * 64 + lane], r, loff, unsigned(j) * stride,
+                                             kAuxNT);
+  }
+};
+
+template <typename E, bool CK>
+__global__ __launch_bounds__(64) void lif_fwd_staged_kernel(const typename E::raw* __restrict__ x,
+                                                            typename E::raw* __restrict__ spk,
+                                                            float* __restrict__ ck, int T, int C,
+                                                            LifParams P) {
+  using S = Staged<E>;
+  constexpr int PF = S::kPf;
+  __shared__ u32x4 xs[S::kInstr * 64];
+  __shared__ u32x4 os[S::kInstr * 64];
+  const int n_cg = (C + 63) / 64;
+  const int b = blockIdx.x / n_cg;
+  const int cg = blockIdx.x - b * n_cg;
+  const int lane = threadIdx.x;
+  const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
+  const unsigned loff = S::lane_off(lane, C, cg);
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  // Membrane records through a descriptor over this group's records; lanes
+  // past C get an out-of-range offset (their stores are dropped).
+  const size_t ck_base = size_t(b) * nblk * C + size_t(cg) * 64;
+  const rsrc_t rck = make_rsrc(CK ? ck + ck_base : ck, CK ? uint32_t(((size_t(nblk) - 1) * C + 64) * 4) : 0u);
+  const unsigned ck_off = cg * 64 + lane < C ? unsigned(lane) * 4u : kOutOfRange;
+
+  float m = 0.f;
+  // Inputs P blocks ahead wait in registers; every block issues the same
+  // loads and stores (past the end the descriptors are empty), so the
+  // compiler's wait before a block's LDS write covers only that block.
+  auto block = [&](u32x4 (&st)[S::kInstr], int blk) {
+    S::to_lds(xs, st, lane);
+    S::load(st, x, row_base, row_tail, loff, blk + PF, nblk, C);
+    if constexpr (CK)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rck, ck_off,
+                                            unsigned(blk) * unsigned(C) * 4u, kAuxNT);
+#pragma unroll
+    for (int s = 0; s < kLifBlock; ++s) {
+      const float h = m * P.decay + S::get(xs, s, lane);
+      const float sp = P.slope * (h - P.threshold) >= 0.f ? 1.f : 0.f;
+      m = h * (1.f - sp) + P.reset * sp;
+      S::put(os, s, lane, sp);
+    }
+    S::store(spk, os, row_base, row_tail, loff, blk, C, lane);
+  };
+
+  u32x4 st[PF][S::kInstr];
+#pragma unroll
+  for (int q = 0; q < PF; ++q) S::load(st[q], x, row_base, row_tail, loff, q, nblk, C);
+  const int nfull = nblk - nblk % PF;
+  for (int base = 0; base < nfull; base += PF) {
+#pragma unroll
+    for (int q = 0; q < PF; ++q) block(st[q], base + q);
+  }
+#pragma unroll
+  for (int q = 0; q < PF - 1; ++q)
+    if (nfull + q < nblk) block(st[q], nfull + q);
+}
+
+template <typename E>
+__global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::raw* __restrict__ x,
+                                                            const typename E::raw* __restrict__ gs,
+                                                            const float* __restrict__ ck,
+                                                            typename E::raw* __restrict__ gx,
+                                                            int T, int C, LifParams P) {
+  using S = Staged<E>;
+  constexpr int PB = S::kPb;
+  constexpr float kHalfPi = 1.5707963267948966f;
+  __shared__ u32x4 xs[S::kInstr * 64];
+  __shared__ u32x4 gl[S::kInstr * 64];
+  __shared__ u32x4 os[S::kInstr * 64];
+  const int n_cg = (C + 63) / 64;
+  const int b = blockIdx.x / n_cg;
+  const int cg = blockIdx.x - b * n_cg;
+  const int lane = threadIdx.x;
+  const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
+  const unsigned loff = S::lane_off(lane, C, cg);
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  // Membrane records (lanes past C read as zero and never store).
+  const rsrc_t rck = make_rsrc(ck + size_t(b) * nblk * C + size_t(cg) * 64,
+                               uint32_t(((size_t(nblk) - 1) * C + 64) * 4));
+  const unsigned ck_off = cg * 64 + lane < C ? unsigned(lane) * 4u : kOutOfRange;
+  auto rec = [&](int blk) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        rck, ck_off, unsigned(max(blk, 0)) * unsigned(C) * 4u, 0));
+  };
+
+  float gm = 0.f;
+  // Blocks are visited last to first; the inputs PB blocks ahead (earlier in
+  // time) wait in registers.  Blocks before 0 read as zero.
+  auto block = [&](u32x4 (&sx)[S::kInstr], u32x4 (&sg)[S::kInstr], float& sm, int blk) {
+    S::to_lds(xs, sx, lane);
+    S::to_lds(gl, sg, lane);
+    float m = sm;
+    S::load(sx, x, row_base, row_tail, loff, blk - PB, nblk, C);
+    S::load(sg, gs, row_base, row_tail, loff, blk - PB, nblk, C);
+    sm = rec(blk - PB);
+    // Recompute the block's pre-spike membranes.
+    float h[kLifBlock];
+#pragma unroll
+    for (int s = 0; s < kLifBlock; ++s) {
+      const float hh = m * P.decay + S::get(xs, s, lane);
+      const float sp = P.slope * (hh - P.threshold) >= 0.f ? 1.f : 0.f;
+      m = hh * (1.f - sp) + P.reset * sp;
+      h[s] = hh;
+    }
+    // Reverse recurrence; steps past T have x = g = 0 and a zero carry.
+#pragma unroll
+    for (int s = kLifBlock - 1; s >= 0; --s) {
+      const float cc = P.slope * (h[s] - P.threshold);
+      const float sp = cc >= 0.f ? 1.f : 0.f;
+      const float q2 = kHalfPi * cc;
+      const float dsdh = P.slope * (0.5f / (1.f + q2 * q2));
+      const float gh = S::get(gl, s, lane) * dsdh + gm * ((1.f - sp) + (P.reset - h[s]) * dsdh);
+      gm = P.decay * gh;
+      S::put(os, s, lane, gh);
+    }
+    S::store(gx, os, row_base, row_tail, loff, blk, C, lane);
+  };
+
+  u32x4 sx[PB][S::kInstr], sg[PB][S::kInstr];
+  float sm[PB];
+#pragma unroll
+  for (int q = 0; q < PB; ++q) {
+    const int blk = nblk - 1 - q;
+    S::load(sx[q], x, row_base, row_tail, loff, blk, nblk, C);
+    S::load(sg[q], gs, row_base, row_tail, loff, blk, nblk, C);
+    sm[q] = rec(blk);
+  }
+  const int nfull = nblk - nblk % PB;
+  int blk = nblk - 1;
+  for (int i = 0; i < nfull; i += PB) {
+#pragma unroll
+    for (int q = 0; q < PB; ++q) block(sx[q], sg[q], sm[q], blk - q);
+    blk -= PB;
+  }
+#pragma unroll
+  for (int q = 0; q < PB - 1; ++q)
+    if (q < nblk - nfull) block(sx[q], sg[q], sm[q], blk - q);
+}
+
 }  // namespace wkv
 
 // ------------------------------------------------------------ launchers ----
@@ -264,9 +491,30 @@ static int lif_bwd_launch(const void* x, const void* gs, const float* ck, void* 
   return check_launch("lif_bwd_kernel");
 }
 
+// The staged kernels need whole 16-byte pieces per row (C a multiple of
+// 16 / element size) and per-batch spans below 2^31 bytes (their
+// out-of-range offset); other shapes take the per-step kernels.
+template <typename E>
+static bool lif_staged_ok(int T, int C) {
+  const size_t span = size_t(T) * size_t(C) * sizeof(typename E::raw);
+  return C % (16 / int(sizeof(typename E::raw))) == 0 && span < (size_t(1) << 31);
+}
+
 template <typename E>
 static int lif_fwd_dispatch(const void* x, void* spk, float* ck, int B, int T, int C,
                             const wkv::LifParams& P, hipStream_t stream) {
+  using raw = typename E::raw;
+  if (lif_staged_ok<E>(T, C)) {
+    const dim3 grid(unsigned(B) * unsigned((C + 63) / 64));
+    if (ck != nullptr) {
+      launch(wkv::lif_fwd_staged_kernel<E, true>, grid, dim3(64), stream, true,
+             static_cast<const raw*>(x), static_cast<raw*>(spk), ck, T, C, P);
+    } else {
+      launch(wkv::lif_fwd_staged_kernel<E, false>, grid, dim3(64), stream, true,
+             static_cast<const raw*>(x), static_cast<raw*>(spk), ck, T, C, P);
+    }
+    return check_launch("lif_fwd_staged_kernel");
+  }
   return lif_vec(B, C, int(sizeof(typename E::raw))) == 2 ? lif_fwd_launch<E, 2>(x, spk, ck, B, T, C, P, stream)
                             : lif_fwd_launch<E, 1>(x, spk, ck, B, T, C, P, stream);
 }
@@ -274,6 +522,13 @@ static int lif_fwd_dispatch(const void* x, void* spk, float* ck, int B, int T, i
 template <typename E>
 static int lif_bwd_dispatch(const void* x, const void* gs, const float* ck, void* gx, int B,
                             int T, int C, const wkv::LifParams& P, hipStream_t stream) {
+  using raw = typename E::raw;
+  if (lif_staged_ok<E>(T, C)) {
+    launch(wkv::lif_bwd_staged_kernel<E>, dim3(unsigned(B) * unsigned((C + 63) / 64)), dim3(64),
+           stream, true, static_cast<const raw*>(x), static_cast<const raw*>(gs), ck,
+           static_cast<raw*>(gx), T, C, P);
+    return check_launch("lif_bwd_staged_kernel");
+  }
   return lif_vec(B, C, int(sizeof(typename E::raw))) == 2 ? lif_bwd_launch<E, 2>(x, gs, ck, gx, B, T, C, P, stream)
                             : lif_bwd_launch<E, 1>(x, gs, ck, gx, B, T, C, P, stream);
 }

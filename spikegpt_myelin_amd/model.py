@@ -7,7 +7,9 @@ two.  Every sequential recurrence runs in the gfx950 kernels -- the WKV time
 mix through ``myelin::wkv_forward{,_bf16io}`` (``SpikeTimeMix.forward``,
 ``language.py:1015-1036``) and the spiking activations through
 ``myelin::lif_sequence_forward`` (``SpikingSequenceLIF.forward``,
-``language.py:848-918``); linear layers, layer norms and the loss are
+``language.py:848-918``), and the token-shift mixes that feed the
+projections through one fused ``myelin::token_shift_mix`` pass per block
+half (``language.py:344-353``); linear layers, layer norms and the loss are
 PyTorch-ROCm (hipBLASLt GEMMs).
 
 Supported configuration: ``model_type="rwkv"``, ``attention="rwkv"``,
@@ -25,6 +27,7 @@ from torch import Tensor, nn
 
 from .language import weighted_key_value
 from .lif import lif_sequence
+from .timemix import token_shift_mix
 
 
 @dataclass
@@ -85,16 +88,6 @@ class _HeavisideAtan(torch.autograd.Function):
         return (grad.float() * (0.5 / (1.0 + q * q))).to(grad.dtype)
 
 
-def _time_shift(inputs: Tensor) -> Tensor:
-    """``language.py:344-345``: the previous token's features (zeros at t=0)."""
-    return F.pad(inputs[:, :-1], (0, 0, 1, 0))
-
-
-def _mix_with_previous(inputs: Tensor, mix: Tensor) -> Tensor:
-    """``language.py:348-353``."""
-    return inputs * mix + _time_shift(inputs) * (1.0 - mix)
-
-
 class SpikingSequenceLIF(nn.Module):
     """``language.py:766-918``: LIF over ``[B, T, C]`` in one HIP kernel."""
 
@@ -149,9 +142,12 @@ class SpikeTimeMix(nn.Module):
         self.output = nn.Linear(attn, n_embd, bias=False)
 
     def forward(self, inputs: Tensor) -> Tensor:
-        key = self.key(_mix_with_previous(inputs, self.time_mix_k))
-        value = self.value(_mix_with_previous(inputs, self.time_mix_v))
-        receptance = torch.sigmoid(self.receptance(_mix_with_previous(inputs, self.time_mix_r)))
+        mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_v.view(-1),
+                             self.time_mix_r.view(-1)])
+        k_in, v_in, r_in = token_shift_mix(inputs, mixes)
+        key = self.key(k_in)
+        value = self.value(v_in)
+        receptance = torch.sigmoid(self.receptance(r_in))
         wkv = weighted_key_value(key, value, self.time_decay, self.time_first)
         return self.output(receptance * wkv)
 
@@ -170,8 +166,10 @@ class SpikeChannelMix(nn.Module):
         self.value = nn.Linear(4 * n_embd, n_embd, bias=False)
 
     def forward(self, inputs: Tensor) -> Tensor:
-        key = torch.relu(self.key(_mix_with_previous(inputs, self.time_mix_k))).square()
-        receptance = torch.sigmoid(self.receptance(_mix_with_previous(inputs, self.time_mix_r)))
+        mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_r.view(-1)])
+        k_in, r_in = token_shift_mix(inputs, mixes)
+        key = torch.relu(self.key(k_in)).square()
+        receptance = torch.sigmoid(self.receptance(r_in))
         return receptance * self.value(key)
 
 

@@ -1,0 +1,120 @@
+"""Fused token-shift mixing as custom ops served by a gfx950 HIP kernel.
+
+The reference forms every projection input of the time mix and the channel
+mix with the eager expression ``x * mix + shift(x) * (1 - mix)``
+(``src/spikegpt/language.py:344-353``; three mixing vectors at :1016-1018,
+two at :1190-1191), each a handful of full passes over ``[B, T, C]`` in fp32
+plus autocast's cast to bf16 for the projection.  Here:
+
+``myelin::token_shift_mix(Tensor x, Tensor mix, ScalarType out_dtype) ->
+Tensor[]`` -- one pass: reads ``x`` once and writes the ``n = mix.shape[0]``
+mixed tensors, rounded once to ``out_dtype``, with the
+reference's fp32 arithmetic and operation order, so the values equal the
+eager expression followed by the cast.
+
+``myelin::token_shift_mix_backward(Tensor[] grads, Tensor x, Tensor mix) ->
+(Tensor grad_x, Tensor grad_mix)`` -- one pass for ``grad_x`` plus a fixed-
+order reduction for ``grad_mix`` ``[n, C]``.
+
+:func:`token_shift_mix` picks ``out_dtype`` from the active CUDA autocast
+dtype, as the projections would cast their inputs.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_NATIVE = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _check(x: Tensor, mix: Tensor) -> None:
+    if x.ndim != 3:
+        raise ValueError(f"inputs must have shape [B, T, C]; got {x.shape}")
+    if mix.ndim != 2 or mix.shape[1] != x.shape[2] or not 1 <= mix.shape[0] <= 3:
+        raise ValueError(f"mix must have shape [n, {x.shape[2]}] with 1 <= n <= 3; got {mix.shape}")
+
+
+@torch.library.custom_op("myelin::token_shift_mix", mutates_args=())
+def _shift_mix(x: Tensor, mix: Tensor, out_dtype: torch.dtype) -> list[Tensor]:
+    _lib.require_gpu(x, mix)
+    _check(x, mix)
+    xs = _lib.aligned(x if x.dtype in _NATIVE else x.float())
+    od = out_dtype
+    mx = _lib.aligned(mix.float())
+    n = mx.shape[0]
+    b, t, c = xs.shape
+    outs = [torch.empty(xs.shape, dtype=od, device=x.device) for _ in range(n)]
+    ptrs = [o.data_ptr() for o in outs] + [None] * (3 - n)
+    lib = _lib.load()
+    rc = _lib.timed("token_shift_mix", x.device, lambda: lib.token_shift_mix_forward(
+        xs.data_ptr(), _lib.dtype_code(xs.dtype), mx.data_ptr(), n, *ptrs, _lib.dtype_code(od),
+        b, t, c, _lib.stream_of(xs),
+    ))
+    _lib.check(rc, "token_shift_mix_forward")
+    return outs
+
+
+@_shift_mix.register_fake
+def _(x, mix, out_dtype):
+    return [torch.empty(x.shape, dtype=out_dtype, device=x.device) for _ in range(mix.shape[0])]
+
+
+@torch.library.custom_op("myelin::token_shift_mix_backward", mutates_args=())
+def _shift_mix_backward(grads: list[Tensor], x: Tensor, mix: Tensor) -> tuple[Tensor, Tensor]:
+    _lib.require_gpu(x, mix, *grads)
+    xs = _lib.aligned(x if x.dtype in _NATIVE else x.float())
+    mx = _lib.aligned(mix.float())
+    n = mx.shape[0]
+    b, t, c = xs.shape
+    gdt = grads[0].dtype if grads[0].dtype in _NATIVE else torch.float32
+    if gdt != xs.dtype and xs.dtype != torch.float32:
+        gdt = xs.dtype
+    gs = [_lib.aligned(g.to(gdt)) for g in grads]
+    gx = torch.empty_like(xs)
+    gmix = torch.empty((n, c), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.token_shift_mix_workspace_bytes(n, b, t, c)), 16),
+                     dtype=torch.uint8, device=x.device)
+    ptrs = [g.data_ptr() for g in gs] + [None] * (3 - n)
+    rc = _lib.timed("token_shift_mix_backward", x.device, lambda: lib.token_shift_mix_backward(
+        xs.data_ptr(), _lib.dtype_code(xs.dtype), mx.data_ptr(), n, *ptrs, _lib.dtype_code(gdt),
+        gx.data_ptr(), gmix.data_ptr(), ws.data_ptr(), ws.numel(), b, t, c, _lib.stream_of(xs),
+    ))
+    _lib.check(rc, "token_shift_mix_backward")
+    return gx, gmix
+
+
+@_shift_mix_backward.register_fake
+def _(grads, x, mix):
+    dt = x.dtype if x.dtype in _NATIVE else torch.float32
+    return (torch.empty(x.shape, dtype=dt, device=x.device),
+            torch.empty(mix.shape, dtype=torch.float32, device=x.device))
+
+
+def _setup_context(ctx, inputs, output):
+    x, mix, _ = inputs
+    ctx.save_for_backward(x, mix)
+
+
+def _backward(ctx, grads):
+    x, mix = ctx.saved_tensors
+    grads = [torch.zeros_like(x) if g is None else g for g in grads]
+    gx, gmix = torch.ops.myelin.token_shift_mix_backward(grads, x, mix)
+    return gx.to(x.dtype), gmix.to(mix.dtype), None
+
+
+_shift_mix.register_autograd(_backward, setup_context=_setup_context)
+
+
+def token_shift_mix(x: Tensor, mix: Tensor) -> list[Tensor]:
+    """``[x * mix[j] + shift(x) * (1 - mix[j]) for j]`` in the autocast dtype
+    when CUDA autocast is on (the projections' input type), else in
+    ``x.dtype``."""
+    if torch.is_autocast_enabled("cuda"):
+        out_dtype = torch.get_autocast_dtype("cuda")
+    else:
+        out_dtype = x.dtype if x.dtype in _NATIVE else torch.float32
+    return torch.ops.myelin.token_shift_mix(x, mix, out_dtype)

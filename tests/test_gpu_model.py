@@ -1,6 +1,6 @@
-"""End-model parity: the SpikeGPT model on the HIP WKV and LIF kernels against
-the same model (identical weights and batch) with both recurrences replaced
-by the CPU oracle's formulations.
+"""End-model parity: the SpikeGPT model on the HIP WKV, LIF and token-shift
+kernels against the same model (identical weights and batch) with all three
+replaced by the CPU oracle's formulations.
 
 Bars: loss within 0.2 % relative (the end-model bar), under bf16 autocast
 and in fp32; parameter gradients in fp32 with cosine similarity > 0.999 (the
@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import lif as L
+from oracle import timemix as TM
 from oracle import wkv4 as O
 
 pytestmark = pytest.mark.gpu
@@ -48,6 +49,13 @@ def _oracle_lif(x, *, tau, threshold, reset, surrogate_slope):
     return L.lif_loop(x.cpu(), tau, threshold, reset, surrogate_slope).to(x.device)
 
 
+def _oracle_mix(x, mixes):
+    od = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+    with torch.autocast("cuda", enabled=False):
+        outs = TM.shift_mix(x.float().cpu(), mixes.float().cpu(), od)
+    return [o.to(x.device) for o in outs]
+
+
 def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
     import spikegpt_myelin_amd.model as M
 
@@ -55,6 +63,7 @@ def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
         if oracle:
             mp.setattr(M, "weighted_key_value", _oracle_wkv)
             mp.setattr(M, "lif_sequence", _oracle_lif)
+            mp.setattr(M, "token_shift_mix", _oracle_mix)
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
             loss, _ = model(ids, tgt)
     return loss
