@@ -12,10 +12,16 @@
 //   gu   = sum_t z_t e^{u+k_t} (v_t - y_t)
 //   gw   = sum_t e^{k_t} (v_t G'_t - H'_t)        (d/dw of e^{(t-1-i)w})
 // and the reverse sums obey G_{t-1} = e^w G_t + z_t,
-// G'_{t-1} = e^w (G'_t + G_t) (same for H with z_t y_t).  The reference
-// accumulates gw in its forward replay (dpdw/dqdw); accumulating it in the
-// reverse sweep instead needs no extra forward state, so the forward can be
-// recomputed from the small checkpoint records the forward kernel writes.
+// G'_{t-1} = e^w (G'_t + G_t) (same for H with z_t y_t).  G_t and -H_t are
+// the adjoints of the forward state (A_{t+1}, B_{t+1}) of the recurrence
+// A_{t+1} = e^w A_t + e^{k_t} v_t, so the w-gradient is also
+//   gw   = e^w sum_t (G_t A_t - H_t B_t)
+// (expand both sides: each pair i < s is counted s-1-i times).  The reverse
+// sweep uses this form: it needs the forward states the sweep recomputes
+// anyway and no G', H' sums.  The reference accumulates gw in its forward
+// replay (dpdw/dqdw); accumulating it in the reverse sweep needs no extra
+// forward state, so the forward can be recomputed from the small checkpoint
+// records the forward kernel writes.
 //
 // One reverse sweep (segments last to first; rows, chunks and segments as in
 // the forward kernel).  Per segment each wave:
@@ -23,10 +29,10 @@
 //     prefetched with the segment's k, v, gy;
 //   * computes 2^{k log2e} and its chunk's forward summary; after one
 //     barrier, an LDS Horner gives its chunk's forward carry;
-//   * recomputes the chunk's forward keeping z~ = gy/den~ and y in registers
-//     and reduces its chunk's reverse sums from a zero state; after a second
-//     barrier, a reverse LDS Horner (G <- G_j + e^{Lw} G,
-//     G' <- G'_j + e^{Lw}(G' + L G)) gives the carry at its chunk's end;
+//   * recomputes the chunk's forward keeping z = gy/den, z y and the states
+//     (A_t, B_t) in registers and reduces its chunk's reverse sums from a zero
+//     state; after a second barrier, a reverse LDS Horner
+//     (G <- G_j + e^{Lw} G) gives the carry at its chunk's end;
 //   * runs the reverse recurrence with that carry, writing gk and gv and
 //     accumulating gw and gu.
 // k, v, gy are read once and gk, gv written once.  gw/gu are reduced over the
@@ -156,14 +162,12 @@ struct Bwd {
     float q[VEC][W][64];
     float G[VEC][W][64];
     float H[VEC][W][64];
-    float Gp[VEC][W][64];
-    float Hp[VEC][W][64];
-    float rcarry[2][4][VEC][64];  // reverse segment carry (G, H, G', H')
+    float rcarry[2][2][VEC][64];  // reverse segment carry (G, H)
   };
 
-  // Per channel: e^{iw} (d0[i-1]) and i e^{iw} (d1[i-1]) for i = 1..L-1.
+  // Per channel: e^{iw} (d0[i-1]) for i = 1..L-1.
   struct Weights {
-    float d0[L - 1][VEC], d1[L - 1][VEC];
+    float d0[L - 1][VEC];
   };
 
   // Forward state at a segment's start.
@@ -250,8 +254,9 @@ struct Bwd {
         Q[c] = fmaf(Q[c], DL[c], sm.q[c][w][lane]);
       }
     }
-    // Forward recompute: keep z = gy/den and z y (zero past the end).
-    float zz[L][VEC], zy[L][VEC];
+    // Forward recompute: keep z = gy/den, z y (zero past the end) and the
+    // states (A_t, B_t) = (P, Q) before step t.
+    float zz[L][VEC], zy[L][VEC], pa[L][VEC], qa[L][VEC];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const bool valid = FULL || (t0 + i) < T;
@@ -265,39 +270,33 @@ struct Bwd {
         const float y = fmaf(e1, vv, P[c]) * r;
         zz[i][c] = FULL || valid ? z : 0.f;
         zy[i][c] = FULL || valid ? z * y : 0.f;
+        pa[i][c] = P[c];
+        qa[i][c] = Q[c];
         P[c] = fmaf(e, vv, P[c] * D[c]);
         Q[c] = fmaf(Q[c], D[c], e);
       }
     }
     // Reverse summary of this chunk from a zero state at its end, as dot
-    // products with the weights e^{iw} and i e^{iw} of step i:
-    // G = sum_i e^{iw} z_i, G' = sum_i i e^{iw} z_i (likewise H, H' with z y).
-    float G[VEC], H[VEC], Gp[VEC], Hp[VEC];
+    // products with the weights e^{iw} of step i: G = sum_i e^{iw} z_i
+    // (likewise H with z y).
+    float G[VEC], H[VEC];
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       G[c] = zz[0][c];
       H[c] = zy[0][c];
-      Gp[c] = zz[1][c] * Wt.d1[0][c];
-      Hp[c] = zy[1][c] * Wt.d1[0][c];
-      G[c] = fmaf(zz[1][c], Wt.d0[0][c], G[c]);
-      H[c] = fmaf(zy[1][c], Wt.d0[0][c], H[c]);
     }
 #pragma unroll
-    for (int i = 2; i < L; ++i) {
+    for (int i = 1; i < L; ++i) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
         G[c] = fmaf(zz[i][c], Wt.d0[i - 1][c], G[c]);
         H[c] = fmaf(zy[i][c], Wt.d0[i - 1][c], H[c]);
-        Gp[c] = fmaf(zz[i][c], Wt.d1[i - 1][c], Gp[c]);
-        Hp[c] = fmaf(zy[i][c], Wt.d1[i - 1][c], Hp[c]);
       }
     }
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       sm.G[c][wave][lane] = G[c];
       sm.H[c][wave][lane] = H[c];
-      sm.Gp[c][wave][lane] = Gp[c];
-      sm.Hp[c][wave][lane] = Hp[c];
     }
     __syncthreads();
     // Carry at this chunk's end: the later segment's carry, then the later
@@ -308,14 +307,10 @@ struct Bwd {
       const bool later = seg + 1 < nseg;
       G[c] = later ? sm.rcarry[sl][0][c][lane] : 0.f;
       H[c] = later ? sm.rcarry[sl][1][c][lane] : 0.f;
-      Gp[c] = later ? sm.rcarry[sl][2][c][lane] : 0.f;
-      Hp[c] = later ? sm.rcarry[sl][3][c][lane] : 0.f;
     }
     for (int w = W - 1; w > wave; --w) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
-        Gp[c] = fmaf(DL[c], fmaf(float(L), G[c], Gp[c]), sm.Gp[c][w][lane]);
-        Hp[c] = fmaf(DL[c], fmaf(float(L), H[c], Hp[c]), sm.Hp[c][w][lane]);
         G[c] = fmaf(DL[c], G[c], sm.G[c][w][lane]);
         H[c] = fmaf(DL[c], H[c], sm.H[c][w][lane]);
       }
@@ -338,9 +333,8 @@ struct Bwd {
         gvo[c] = e * a;
         gko[c] = e * fmaf(vv, a, -bb);
         gu[c] = fmaf(e, fmaf(z, vv, -zy[i][c]), gu[c]);
-        gw[c] = fmaf(e, fmaf(vv, Gp[c], -Hp[c]), gw[c]);
-        Gp[c] = (Gp[c] + G[c]) * D[c];
-        Hp[c] = (Hp[c] + H[c]) * D[c];
+        // gw accumulates G_t A_t - H_t B_t (times e^w once at the end).
+        gw[c] = fmaf(G[c], pa[i][c], fmaf(-H[c], qa[i][c], gw[c]));
         G[c] = fmaf(G[c], D[c], z);
         H[c] = fmaf(H[c], D[c], zy[i][c]);
       }
@@ -366,8 +360,6 @@ struct Bwd {
       for (int c = 0; c < VEC; ++c) {
         sm.rcarry[sl][0][c][lane] = G[c];
         sm.rcarry[sl][1][c][lane] = H[c];
-        sm.rcarry[sl][2][c][lane] = Gp[c];
-        sm.rcarry[sl][3][c][lane] = Hp[c];
       }
     }
   }
@@ -420,7 +412,6 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
 #pragma unroll
     for (int i = 1; i < L; ++i) {
       Wt.d0[i - 1][c] = pw;
-      Wt.d1[i - 1][c] = float(i) * pw;
       pw *= D[c];
     }
   }
@@ -477,7 +468,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      sm.G[c][wave][lane] = gw[c];
+      sm.G[c][wave][lane] = gw[c] * D[c];
       sm.H[c][wave][lane] = gu[c] * U[c];
     }
     __syncthreads();
@@ -565,7 +556,8 @@ struct TileCfg { int vec, L, W; };
 // Tile configurations compiled into the library (selectable with
 // WKV_BWD_CFG="vec,L,W" for measurement).  SEG = W*L must be a multiple of
 // the 64-step checkpoint block.  Defaults: (2,8,8) for 16-bit tensors with
-// enough rows of 128 channels to fill the chip, else (1,16,8); the W=16
+// enough rows of 128 channels to fill the chip, else (1,8,8) (fastest measured
+// for the few-row shapes, no spills); the W=16
 // configurations are capped at 128 VGPRs and spill.
 static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}, {1, 8, 8},
                                         {1, 16, 4}, {2, 16, 4}};
@@ -582,7 +574,7 @@ static TileCfg pick_bwd_cfg(int64_t B, int64_t C, int elem_bytes) {
       if (c.vec == vec && c.L == L && c.W == W && (vec == 1 || C % 2 == 0)) return c;
   }
   if (elem_bytes == 2 && pick_vec(B, C) == 2) return TileCfg{2, 8, 8};
-  return TileCfg{1, 16, 8};
+  return TileCfg{1, 8, 8};
 }
 
 size_t wkv4_checkpoint_floats(int64_t B, int64_t T, int64_t C) {
