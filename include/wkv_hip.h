@@ -126,7 +126,7 @@ int wkv7_forward(const void* r, const void* w, const void* k, const void* v, con
                  int64_t H, int64_t N, int dtype, void* stream);
 
 /* Bytes of the RWKV-7 state checkpoints: the 64x64 fp32 state at the start of
- * every 16-step block, [B*H][ceil(T/16)][64][64]. */
+ * every 8-step block, [B*H][ceil(T/8)][64][64]. */
 size_t wkv7_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int64_t N);
 
 /* wkv7_forward that also writes the state checkpoints (y and s_out may be

@@ -29,11 +29,11 @@
 // vector ALUs; no matrix cores.
 //
 // Checkpoints.  The forward can write the state at the start of every
-// KC-step block ([B*H][ceil(T/KC)][64][64] fp32; block 0 holds the initial
-// state).  The backward walks the blocks last to first; for each block it
-// recomputes the forward of sub-chunks of KS steps from the block's
-// checkpoint, holding S_{t-1} and sa_t of the sub-chunk in registers, and
-// then runs the reverse recurrence over the sub-chunk.
+// KS-step sub-chunk ([B*H][ceil(T/KS)][64][64] fp32; record 0 holds the
+// initial state).  The backward walks the blocks last to first and, inside
+// each, the sub-chunks last to first; each sub-chunk's forward is recomputed
+// from its own record (no replay), holding S_{t-1} and sa_t in registers,
+// then the reverse recurrence runs over it.
 //
 // The reference's RWKV-7 code was deleted
 // (benchmarks/results/optimizer_wkv_experiments_5090.md:3); the output
@@ -46,8 +46,8 @@ namespace w7 {
 
 constexpr int kN = 64;          // head size
 constexpr int kThreads = 256;   // threads per (batch, head)
-constexpr int kKC = 16;         // steps per staged block / checkpoint
-constexpr int kKS = 8;          // steps per backward sub-chunk (registers)
+constexpr int kKC = 16;         // steps per staged block
+constexpr int kKS = 8;          // steps per checkpoint / backward sub-chunk (registers)
 constexpr int kNSub = kKC / kKS;
 
 __device__ __forceinline__ float as_f(unsigned u) { return __uint_as_float(u); }
@@ -261,8 +261,8 @@ __device__ __forceinline__ void store_steps(typename E::raw* out, const float* b
 
 // ------------------------------------------------------------- forward ----
 // One workgroup per (batch, head).  ck (optional): state at the start of
-// every kKC-step block, [B*H][ceil(T/kKC)][64][64].  y may be null (records
-// only).
+// every kKS-step sub-chunk, [B*H][ceil(T/kKS)][64][64].  y may be null
+// (records only).
 template <typename E>
 __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
     w7::Vecs<E, 6> in, const float* __restrict__ s0, typename E::raw* __restrict__ y,
@@ -285,6 +285,7 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
       for (int c = 0; c < 4; ++c) S[r][c] = 0.f;
   }
   const int nblk = (T + kKC - 1) / kKC;
+  const int nrec = (T + kKS - 1) / kKS;
   Stager<E, 6> st;
   if (nblk > 0) {
     st.load(in, bi, h, 0, T, H);
@@ -294,13 +295,14 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
   for (int blk = 0; blk < nblk; ++blk) {
     const int t0 = blk * kKC;
     const int n = min(kKC, T - t0);
-    if (ck) store_state(ck + (size_t(bh) * nblk + blk) * kN * kN, S, L);
     if (blk + 1 < nblk) st.load(in, bi, h, t0 + kKC, T, H);
     const float* sg = stage[blk & 1];
     float* yb = ybuf[blk & 1];
 #pragma unroll
     for (int s = 0; s < kKC; ++s) {
       if (s < n) {
+        if (ck && s % kKS == 0)
+          store_state(ck + (size_t(bh) * nrec + blk * kNSub + s / kKS) * kN * kN, S, L);
         float sa[4];
         fwd_step(S, sg, s, L, sa);
         const float4 r4 = lds4(sg, QR, s, L.j0);
@@ -336,8 +338,9 @@ struct BwdSmem {
 };
 
 // Recompute + reverse over one sub-chunk of cnt steps starting at staged
-// step sl (FULL: cnt == kKS, no per-step guards).  Leaves the per-step
-// partial sums in sm.red / sm.dvb and advances G to before the sub-chunk.
+// step sl, from the sub-chunk's state record ckb (FULL: cnt == kKS, no
+// per-step guards).  Leaves the per-step partial sums in sm.red / sm.dvb and
+// advances G to before the sub-chunk.
 template <bool FULL>
 __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const float* ckb,
                                              int sl, int cnt, const Lane& L, float (&G)[4][4]) {
@@ -345,9 +348,6 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
   const int col = L.j0 + L.rg;  // column this lane holds after rows4_sum
   float S[4][4];
   load_state(S, ckb, L);
-  float sa[4];
-#pragma unroll 1
-  for (int s = 0; s < sl; ++s) fwd_step(S, sg, s, L, sa);
   // Recompute the sub-chunk keeping S_{t-1} and sa_t.
   float Sp[KS][4][4], sas[KS][4];
 #pragma unroll
@@ -448,8 +448,8 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
 }  // namespace w7
 
 // One workgroup per (batch, head); blocks of kKC steps last to first, each
-// in sub-chunks of kKS steps (last to first) recomputed from the block's
-// checkpoint.  ds_T (optional): gradient of the final state; ds0 (optional):
+// in sub-chunks of kKS steps (last to first) recomputed from their
+// checkpoint records.  ds_T (optional): gradient of the final state; ds0 (optional):
 // gradient of the initial state.
 template <typename E>
 __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
@@ -475,6 +475,7 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
       for (int c = 0; c < 4; ++c) G[r][c] = 0.f;
   }
   const int nblk = (T + kKC - 1) / kKC;
+  const int nrec = (T + kKS - 1) / kKS;
   Stager<E, 7> st;
   if (nblk > 0) {
     st.load(in, bi, h, (nblk - 1) * kKC, T, H);
@@ -486,12 +487,12 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
     const int n = min(kKC, T - t0);
     if (blk > 0) st.load(in, bi, h, t0 - kKC, T, H);
     const float* sg = sm.stage[blk & 1];
-    const float* ckb = ck + (size_t(bh) * nblk + blk) * kN * kN;
 #pragma unroll 1
     for (int m = kNSub - 1; m >= 0; --m) {
       const int sl = m * kKS;
       if (sl >= n) continue;
       const int cnt = min(kKS, n - sl);
+      const float* ckb = ck + (size_t(bh) * nrec + blk * kNSub + m) * kN * kN;
       if (cnt == kKS) {
         bwd_subchunk<true>(sm, sg, ckb, sl, cnt, L, G);
       } else {
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
 namespace wkv_host {
 
 size_t wkv7_checkpoint_floats(int64_t B, int64_t T, int64_t H) {
-  return size_t(B) * size_t(H) * size_t((T + wkv::w7::kKC - 1) / wkv::w7::kKC) * 64 * 64;
+  return size_t(B) * size_t(H) * size_t((T + wkv::w7::kKS - 1) / wkv::w7::kKS) * 64 * 64;
 }
 
 template <typename E>

@@ -16,7 +16,7 @@ out).
 
 Autograd.  The public forward is a composite of the private op
 ``myelin::wkv7_forward_train``, which also returns the 64x64 state at the
-start of every 16-step block; its registered backward
+start of every 8-step block; its registered backward
 (``myelin::wkv7_backward_train``) recomputes each block from its checkpoint
 instead of replaying the sequence.
 
@@ -35,7 +35,7 @@ from torch import Tensor
 from . import _lib
 
 HEAD_SIZE = 64
-CKPT_STEPS = 16  # steps per state checkpoint
+CKPT_STEPS = 8  # steps per state checkpoint
 _NATIVE = (torch.float32, torch.bfloat16, torch.float16)
 
 

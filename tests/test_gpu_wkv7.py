@@ -108,10 +108,11 @@ def test_forward_without_checkpoints_equals_training_forward():
     y1, s1 = wkv7_forward_no_checkpoint(*xd, s0.to(DEV))
     y2, s2, ck = ops.wkv7_forward_train(*xd, s0.to(DEV))
     assert torch.equal(y1, y2) and torch.equal(s1, s2)
-    # checkpoint 0 is the initial state, checkpoint j the state after 16 j steps
+    # checkpoint 0 is the initial state, checkpoint j the state after 8 j steps
     assert torch.equal(ck[:, :, 0], s0.to(DEV))
-    _, s16 = wkv7_forward_no_checkpoint(*(x[:, :16] for x in xd), s0.to(DEV))
-    assert torch.equal(ck[:, :, 1], s16)
+    for j in (1, 2, 4):
+        _, sj = wkv7_forward_no_checkpoint(*(x[:, :8 * j] for x in xd), s0.to(DEV))
+        assert torch.equal(ck[:, :, j], sj), f"checkpoint {j}"
 
 
 def test_deterministic():
