@@ -88,6 +88,57 @@ class _HeavisideAtan(torch.autograd.Function):
         return (grad.float() * (0.5 / (1.0 + q * q))).to(grad.dtype)
 
 
+class _SplitKLinearFn(torch.autograd.Function):
+    """``x @ weight.T`` whose weight gradient sums S independent GEMMs over
+    slices of the B*T rows (fp32 outputs, then an fp32 sum).  With
+    B*T = 65536 rows and a 512x512 weight, the one-GEMM weight gradient has
+    only a few dozen output tiles for 256 CUs; S slices give S times as many.
+    Forward and input gradient are the ordinary GEMMs; the computation dtype
+    is the active CUDA autocast dtype, as ``nn.Linear`` under autocast."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, splits: int) -> Tensor:  # noqa: D102
+        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else x.dtype
+        with torch.autocast("cuda", enabled=False):
+            xc, wc = x.to(dt), weight.to(dt)
+            y = torch.matmul(xc, wc.t())
+        ctx.save_for_backward(xc, wc)
+        ctx.splits = splits
+        ctx.weight_dtype = weight.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):  # noqa: D102
+        xc, wc = ctx.saved_tensors
+        grad = grad.to(wc.dtype)
+        with torch.autocast("cuda", enabled=False):
+            gx = torch.matmul(grad, wc)
+            rows = grad.numel() // grad.shape[-1]
+            s = ctx.splits
+            g3 = grad.reshape(s, rows // s, grad.shape[-1])
+            x3 = xc.reshape(s, rows // s, xc.shape[-1])
+            # [S, out, in] = g3^T @ x3: the transposed view is the left
+            # operand; the right one is contiguous.
+            gw = torch.bmm(g3.transpose(1, 2), x3, out_dtype=torch.float32).sum(0)
+        return gx, gw.to(ctx.weight_dtype), None
+
+
+class SplitKLinear(nn.Linear):
+    """``nn.Linear`` (same parameters and state-dict names) with the split-K
+    weight gradient of :class:`_SplitKLinearFn` when the input has enough
+    rows; falls back to ``nn.Linear`` otherwise (and on non-CUDA tensors)."""
+
+    min_rows_per_split = 2048
+    splits = 16
+
+    def forward(self, x: Tensor) -> Tensor:
+        rows = x.numel() // x.shape[-1]
+        if (self.bias is not None or not x.is_cuda or not torch.is_grad_enabled()
+                or rows % self.splits != 0 or rows // self.splits < self.min_rows_per_split):
+            return super().forward(x)
+        return _SplitKLinearFn.apply(x, self.weight, self.splits)
+
+
 class SpikingSequenceLIF(nn.Module):
     """``language.py:766-918``: LIF over ``[B, T, C]`` in one HIP kernel."""
 
@@ -136,10 +187,10 @@ class SpikeTimeMix(nn.Module):
             (torch.pow(position, ratio_1_to_almost0) + 0.3 * ratio_0_to_1).view(1, 1, -1)
         )
         self.time_mix_r = nn.Parameter(torch.pow(position, 0.5 * ratio_1_to_almost0).view(1, 1, -1))
-        self.key = nn.Linear(n_embd, attn, bias=False)
-        self.value = nn.Linear(n_embd, attn, bias=False)
-        self.receptance = nn.Linear(n_embd, attn, bias=False)
-        self.output = nn.Linear(attn, n_embd, bias=False)
+        self.key = SplitKLinear(n_embd, attn, bias=False)
+        self.value = SplitKLinear(n_embd, attn, bias=False)
+        self.receptance = SplitKLinear(n_embd, attn, bias=False)
+        self.output = SplitKLinear(attn, n_embd, bias=False)
 
     def forward(self, inputs: Tensor) -> Tensor:
         mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_v.view(-1),
@@ -161,9 +212,9 @@ class SpikeChannelMix(nn.Module):
         position = torch.arange(n_embd, dtype=torch.float32) / n_embd
         self.time_mix_k = nn.Parameter(torch.pow(position, ratio_1_to_almost0).view(1, 1, -1))
         self.time_mix_r = nn.Parameter(torch.pow(position, ratio_1_to_almost0).view(1, 1, -1))
-        self.key = nn.Linear(n_embd, 4 * n_embd, bias=False)
-        self.receptance = nn.Linear(n_embd, n_embd, bias=False)
-        self.value = nn.Linear(4 * n_embd, n_embd, bias=False)
+        self.key = SplitKLinear(n_embd, 4 * n_embd, bias=False)
+        self.receptance = SplitKLinear(n_embd, n_embd, bias=False)
+        self.value = SplitKLinear(4 * n_embd, n_embd, bias=False)
 
     def forward(self, inputs: Tensor) -> Tensor:
         mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_r.view(-1)])
@@ -214,7 +265,7 @@ class SpikeLanguageModel(nn.Module):
         self.embedding = nn.Embedding(config.vocab_size, config.n_embd)
         self.blocks = nn.ModuleList(SpikeGPTBlock(config, i) for i in range(config.n_layer))
         self.ln_out = nn.LayerNorm(config.n_embd)
-        self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
+        self.head = SplitKLinear(config.n_embd, config.vocab_size, bias=False)
         self.apply(self._init_weights)
 
     @staticmethod

@@ -119,3 +119,30 @@ def test_training_steps_reduce_the_loss():
         losses.append(float(loss))
     assert all(torch.isfinite(torch.tensor(losses)))
     assert losses[-1] < losses[0] - 0.5, losses
+
+
+@pytest.mark.parametrize("autocast", [True, False])
+def test_split_k_linear_matches_linear(autocast):
+    from spikegpt_myelin_amd.model import SplitKLinear
+
+    torch.manual_seed(3)
+    ref = torch.nn.Linear(512, 384, bias=False).to(DEV)
+    lin = SplitKLinear(512, 384, bias=False).to(DEV)
+    lin.load_state_dict(ref.state_dict())
+    x = torch.randn(4, 8192, 512, device=DEV)  # 32768 rows: 16 slices of 2048
+    gy = torch.randn(4, 8192, 384, device=DEV)
+    outs = []
+    for m in (ref, lin):
+        xi = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            y = m(xi)
+        y.backward(gy.to(y.dtype))
+        outs.append((y.detach().float(), xi.grad.float(), m.weight.grad.float()))
+    (y0, gx0, gw0), (y1, gx1, gw1) = outs
+    # Forward and input gradient run the same GEMMs; the weight gradient sums
+    # 16 fp32 slices instead of one fp32 accumulation.
+    tol = dict(rtol=2e-2, atol=2e-2) if autocast else dict(rtol=1e-4, atol=1e-4)
+    assert torch.allclose(y1, y0, **tol)
+    assert torch.allclose(gx1, gx0, **tol)
+    rel = float((gw1 - gw0).norm() / gw0.norm())
+    assert rel < (1e-2 if autocast else 1e-5), rel
