@@ -223,6 +223,28 @@ int token_shift_mix_backward(const void* x, int x_dtype, const float* mix, int64
                              size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
                              void* stream);
 
+/* Squared ReLU of the channel mix, y = max(x, 0)^2, computed in fp32 and
+ * rounded once to `dtype`: the values of torch.relu(key).square()
+ * (src/spikegpt/language.py:1192) under autocast, where the square runs in
+ * fp32 and the next projection casts.  n elements, a multiple of 16 bytes of
+ * them (8 bf16/fp16 or 4 fp32). */
+int relu_square_forward(const void* x, void* y, int64_t n, int dtype, void* stream);
+
+/* Backward of relu_square_forward: grad_x = grad_y * 2 max(x, 0). */
+int relu_square_backward(const void* x, const void* grad_y, void* grad_x, int64_t n, int dtype,
+                         void* stream);
+
+/* Receptance gate y = sigmoid(r) * x (language.py:1035 sigmoid(r) * wkv and
+ * :1194 sigmoid(r) * value): sigmoid rounded to `dtype`, then the product
+ * rounded, as the two eager 16-bit kernels do.  n as relu_square_forward. */
+int sigmoid_gate_forward(const void* r, const void* x, void* y, int64_t n, int dtype,
+                         void* stream);
+
+/* Backward of sigmoid_gate_forward: grad_x = g s, grad_r = g x s (1 - s),
+ * s = sigmoid(r) in fp32. */
+int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void* grad_r,
+                          void* grad_x, int64_t n, int dtype, void* stream);
+
 /* Measurement hook; no counterpart in the reference.  Arms two HIP events
  * (hipEvent_t, created with timing enabled; either may be NULL) for the next
  * entry point called on this thread: its first kernel dispatch records

@@ -20,6 +20,7 @@ spikegpt_myelin_amd.build``):
 
 from .decode import initial_wkv_state, wkv_decode_step
 from .language import validate_wkv_inputs, weighted_key_value
+from .gates import relu_square, sigmoid_gate
 from .lif import lif_sequence
 from .timemix import token_shift_mix
 from .wkv import (
@@ -33,6 +34,8 @@ from .wkv7 import wkv7_backward, wkv7_forward
 __all__ = [
     "initial_wkv_state",
     "lif_sequence",
+    "relu_square",
+    "sigmoid_gate",
     "token_shift_mix",
     "validate_wkv_inputs",
     "weighted_key_value",

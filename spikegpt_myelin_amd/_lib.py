@@ -81,6 +81,10 @@ SIGNATURES = {
         _INT,
         [_P, _INT, _P, _I64, _P, _P, _P, _INT, _P, _P, _P, _SZ, _I64, _I64, _I64, _P],
     ),
+    "relu_square_forward": (_INT, [_P, _P, _I64, _INT, _P]),
+    "relu_square_backward": (_INT, [_P, _P, _P, _I64, _INT, _P]),
+    "sigmoid_gate_forward": (_INT, [_P, _P, _P, _I64, _INT, _P]),
+    "sigmoid_gate_backward": (_INT, [_P, _P, _P, _P, _P, _I64, _INT, _P]),
     "wkv_time_next_call": (_INT, [_P, _P]),
     "wkv_last_error_string": (ctypes.c_char_p, []),
     "wkv_version": (ctypes.c_char_p, []),

@@ -101,8 +101,18 @@ int lif_forward_impl(const void*, void*, float*, int, int, int, float, float, fl
                      hipStream_t);
 int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
                       float, float, int, hipStream_t);
+int relu_square_forward_impl(const void*, void*, int64_t, int, hipStream_t);
+int relu_square_backward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
+int sigmoid_gate_forward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
+int sigmoid_gate_backward_impl(const void*, const void*, const void*, void*, void*, int64_t, int,
+                               hipStream_t);
 
 static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }
+
+// Element-wise entry points work on whole 16-byte vectors.
+static bool elementwise_ok(int64_t n, int dtype) {
+  return n >= 0 && n % (dtype == 0 ? 4 : 8) == 0 && n / 8 < (int64_t(1) << 40);
+}
 
 // Tensors are read and written with vector instructions of up to 16 bytes.
 static bool aligned16(std::initializer_list<const void*> ptrs) {
@@ -490,6 +500,71 @@ int token_shift_mix_backward(const void* x, int x_dtype, const float* mix, int64
   return shift_mix_backward_impl(x, x_dtype, mix, g, g_dtype, grad_x,
                                  static_cast<float*>(workspace), grad_mix, int(n), int(B), int(T),
                                  int(C), static_cast<hipStream_t>(stream));
+}
+
+int relu_square_forward(const void* x, void* y, int64_t n, int dtype, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "relu_square_forward: unknown dtype");
+  if (!elementwise_ok(n, dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "relu_square_forward: n must be a multiple of 16 bytes of elements");
+  if (n == 0) return WKV_OK;
+  if (!x || !y) return fail(WKV_ERR_INVALID_ARGUMENT, "relu_square_forward: null pointer");
+  if (!aligned16({x, y}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "relu_square_forward: tensors must be 16-byte aligned");
+  return relu_square_forward_impl(x, y, n, dtype, static_cast<hipStream_t>(stream));
+}
+
+int relu_square_backward(const void* x, const void* grad_y, void* grad_x, int64_t n, int dtype,
+                         void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "relu_square_backward: unknown dtype");
+  if (!elementwise_ok(n, dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "relu_square_backward: n must be a multiple of 16 bytes of elements");
+  if (n == 0) return WKV_OK;
+  if (!x || !grad_y || !grad_x)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "relu_square_backward: null pointer");
+  if (!aligned16({x, grad_y, grad_x}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "relu_square_backward: tensors must be 16-byte aligned");
+  return relu_square_backward_impl(x, grad_y, grad_x, n, dtype, static_cast<hipStream_t>(stream));
+}
+
+int sigmoid_gate_forward(const void* r, const void* x, void* y, int64_t n, int dtype,
+                         void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_forward: unknown dtype");
+  if (!elementwise_ok(n, dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "sigmoid_gate_forward: n must be a multiple of 16 bytes of elements");
+  if (n == 0) return WKV_OK;
+  if (!r || !x || !y) return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_forward: null pointer");
+  if (!aligned16({r, x, y}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_forward: tensors must be 16-byte aligned");
+  return sigmoid_gate_forward_impl(r, x, y, n, dtype, static_cast<hipStream_t>(stream));
+}
+
+int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void* grad_r,
+                          void* grad_x, int64_t n, int dtype, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_backward: unknown dtype");
+  if (!elementwise_ok(n, dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "sigmoid_gate_backward: n must be a multiple of 16 bytes of elements");
+  if (n == 0) return WKV_OK;
+  if (!r || !x || !grad_y || !grad_r || !grad_x)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_backward: null pointer");
+  if (!aligned16({r, x, grad_y, grad_r, grad_x}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_backward: tensors must be 16-byte aligned");
+  return sigmoid_gate_backward_impl(r, x, grad_y, grad_r, grad_x, n, dtype,
+                                    static_cast<hipStream_t>(stream));
 }
 
 int wkv_time_next_call(void* start_event, void* stop_event) {

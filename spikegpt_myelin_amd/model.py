@@ -9,8 +9,10 @@ mix through ``myelin::wkv_forward{,_bf16io}`` (``SpikeTimeMix.forward``,
 ``myelin::lif_sequence_forward`` (``SpikingSequenceLIF.forward``,
 ``language.py:848-918``), and the token-shift mixes that feed the
 projections through one fused ``myelin::token_shift_mix`` pass per block
-half (``language.py:344-353``); linear layers, layer norms and the loss are
-PyTorch-ROCm (hipBLASLt GEMMs).
+half (``language.py:344-353``), and the squared ReLU and receptance gates
+through ``myelin::relu_square`` / ``myelin::sigmoid_gate``; linear layers
+(with split-K weight gradients), layer norms and the loss are PyTorch-ROCm
+(hipBLASLt GEMMs).
 
 Supported configuration: ``model_type="rwkv"``, ``attention="rwkv"``,
 ``spike_input=False`` (the reference defaults, ``language.py:234-256``).
@@ -25,6 +27,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from .gates import relu_square, sigmoid_gate
 from .language import weighted_key_value
 from .lif import lif_sequence
 from .timemix import token_shift_mix
@@ -198,9 +201,8 @@ class SpikeTimeMix(nn.Module):
         k_in, v_in, r_in = token_shift_mix(inputs, mixes)
         key = self.key(k_in)
         value = self.value(v_in)
-        receptance = torch.sigmoid(self.receptance(r_in))
         wkv = weighted_key_value(key, value, self.time_decay, self.time_first)
-        return self.output(receptance * wkv)
+        return self.output(sigmoid_gate(self.receptance(r_in), wkv))
 
 
 class SpikeChannelMix(nn.Module):
@@ -219,9 +221,8 @@ class SpikeChannelMix(nn.Module):
     def forward(self, inputs: Tensor) -> Tensor:
         mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_r.view(-1)])
         k_in, r_in = token_shift_mix(inputs, mixes)
-        key = torch.relu(self.key(k_in)).square()
-        receptance = torch.sigmoid(self.receptance(r_in))
-        return receptance * self.value(key)
+        key = relu_square(self.key(k_in))
+        return sigmoid_gate(self.receptance(r_in), self.value(key))
 
 
 class SpikeGPTBlock(nn.Module):

@@ -1,0 +1,79 @@
+"""GPU parity of the fused squared ReLU and receptance gate.
+
+Bars: forward of ``relu_square`` bit-exact against ``relu(x).square()`` in
+fp32 rounded once (the autocast values); ``sigmoid_gate`` forward within one
+unit in the last place of the element type of torch's own two-kernel result
+(the kernels evaluate the same fp32 expression; the exponential's last bit
+may differ) and equal on at least 99.9 % of elements; backward against
+float64 autograd with ``rtol=1e-5`` (fp32) or ``rtol=2e-2, atol=1e-2``
+(16-bit).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _ops():
+    import spikegpt_myelin_amd  # noqa: F401
+
+    return torch.ops.myelin
+
+
+def _tol(dt):
+    return dict(rtol=1e-5, atol=1e-6) if dt == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("shape", [(8,), (3, 7, 64), (64, 1024, 128)])
+def test_relu_square(dt, shape):
+    g = torch.Generator().manual_seed(1)
+    x = (torch.randn(shape, generator=g) * 3).to(dt)
+    gy = torch.randn(shape, generator=g).to(dt)
+    y = _ops().relu_square(x.to(DEV))
+    ref = (torch.relu(x.float()) ** 2).to(dt)
+    assert torch.equal(y.cpu(), ref)
+    gx = _ops().relu_square_backward(gy.to(DEV), x.to(DEV))
+    xr = x.double().requires_grad_(True)
+    (rg,) = torch.autograd.grad(torch.relu(xr) ** 2, xr, gy.double())
+    assert torch.allclose(gx.double().cpu(), rg, **_tol(dt))
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("shape", [(16,), (5, 33, 96), (64, 1024, 64)])
+def test_sigmoid_gate(dt, shape):
+    g = torch.Generator().manual_seed(2)
+    r = (torch.randn(shape, generator=g) * 4).to(dt)
+    x = torch.randn(shape, generator=g).to(dt)
+    gy = torch.randn(shape, generator=g).to(dt)
+    rd, xd = r.to(DEV), x.to(DEV)
+    y = _ops().sigmoid_gate(rd, xd)
+    eager = torch.sigmoid(rd) * xd
+    diff = (y.float() - eager.float()).abs()
+    ulp = torch.finfo(dt).eps * eager.float().abs().clamp_min(torch.finfo(dt).tiny)
+    assert bool((diff <= ulp).all()), float(diff.max())
+    assert float((y == eager).float().mean()) >= 0.999
+    gr, gx = _ops().sigmoid_gate_backward(gy.to(DEV), rd, xd)
+    rr = r.double().requires_grad_(True)
+    xr = x.double().requires_grad_(True)
+    grr, gxr = torch.autograd.grad(torch.sigmoid(rr) * xr, [rr, xr], gy.double())
+    assert torch.allclose(gr.double().cpu(), grr, **_tol(dt))
+    assert torch.allclose(gx.double().cpu(), gxr, **_tol(dt))
+
+
+def test_module_functions_route_and_differentiate():
+    from spikegpt_myelin_amd import relu_square, sigmoid_gate
+
+    x = torch.randn(4, 32, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    r = torch.randn(4, 32, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    (sigmoid_gate(r, relu_square(x)).float().sum()).backward()
+    assert x.grad is not None and r.grad is not None
+    # odd sizes take the eager expression
+    z = torch.randn(3, 5, device=DEV, dtype=torch.bfloat16)
+    assert torch.equal(relu_square(z), torch.relu(z).square())

@@ -64,6 +64,8 @@ def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
             mp.setattr(M, "weighted_key_value", _oracle_wkv)
             mp.setattr(M, "lif_sequence", _oracle_lif)
             mp.setattr(M, "token_shift_mix", _oracle_mix)
+            mp.setattr(M, "relu_square", lambda x: torch.relu(x).square())
+            mp.setattr(M, "sigmoid_gate", lambda r, x: torch.sigmoid(r) * x)
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
             loss, _ = model(ids, tgt)
     return loss
