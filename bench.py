@@ -29,6 +29,7 @@ Other workloads (``--workload``): ``long`` (B=24, T=3072, C=512), ``216m``
 (B=16, T=1024, C=768, 18 layers), ``decode`` (B=256, C=768, 18 layers, fp32
 state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward + backward), ``c0``
 (fp32 forward B=2, T=128, C=512), ``lif`` (sequence LIF forward + backward, B=64, T=1024, C=512 bf16),
+``timemix`` (fused token-shift mix, three vectors, same shape),
 ``e2e41m`` (the whole 41M SpikeGPT
 training step, 12 layers x 512, vocab 256, B=64, T=1024; the default run
 also reports it as ``e2e_train_step``).
@@ -516,6 +517,99 @@ def bench_lif(args) -> dict:
     return out
 
 
+def bench_timemix(args) -> dict:
+    """Fused token-shift mix of the time-mix block (three mixing vectors,
+    fp32 input, bf16 outputs) forward + backward through the C ABI on
+    preallocated buffers: B=64, T=1024, C=512."""
+    import spikegpt_myelin_amd  # noqa: F401
+    from spikegpt_myelin_amd import _lib
+    from oracle import timemix as TM
+
+    B, T, C, n = 64, 1024, 512, 3
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(B, T, C, generator=g).to(dev)
+    mix = torch.rand(n, C, generator=g).to(dev)
+    outs = [torch.empty(B, T, C, dtype=torch.bfloat16, device=dev) for _ in range(n)]
+    grads = [torch.randn(B, T, C, generator=g).to(torch.bfloat16).to(dev) for _ in range(n)]
+    gx = torch.empty_like(x)
+    gmix = torch.empty(n, C, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws = torch.empty(int(lib.token_shift_mix_workspace_bytes(n, B, T, C)), dtype=torch.uint8,
+                     device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    f32, bf16 = _lib.dtype_code(torch.float32), _lib.dtype_code(torch.bfloat16)
+    xp, mp = x.data_ptr(), mix.data_ptr()
+    op = [o.data_ptr() for o in outs]
+    gp = [q.data_ptr() for q in grads]
+
+    def fwd():
+        _lib.check(lib.token_shift_mix_forward(xp, f32, mp, n, *op, bf16, B, T, C, sp), "mix fwd")
+
+    def bwd():
+        _lib.check(lib.token_shift_mix_backward(xp, f32, mp, n, *gp, bf16, gx.data_ptr(),
+                                                gmix.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                B, T, C, sp), "mix bwd")
+
+    pool = EventPool(4 * args.steps, stream)
+    for _ in range(args.warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    evs = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        fwd()
+        if i % args.event_every == 0:
+            s_ev, e_ev = pool.take(), pool.take()
+            _lib.arm_events(s_ev, e_ev)
+            bwd()
+            evs.append((s_ev, e_ev))
+        else:
+            bwd()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    bwd_t = statistics.mean(s.elapsed_time(e) * 1e-3 for s, e in evs)
+    step_s = elapsed / args.steps
+    ne = B * T * C
+    fwd_bytes, bwd_bytes = (4 + 2 * n) * ne, (4 + 2 * n + 4) * ne
+    achieved = bwd_bytes / bwd_t / 1e9
+    out = {
+        "metric": "fused token-shift mix (3 vectors) fwd+bwd tokens/sec, B=64 T=1024 C=512 "
+                  "fp32 in / bf16 out",
+        "value": B * T / step_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "token_shift_mix_fwd_bwd", "B": B, "T": T, "C": C, "n": n},
+        "hbm_gbps_algorithmic": (fwd_bytes + bwd_bytes) / step_s / 1e9,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "shift_mix_bwd_kernel + column_sum_kernel",
+                     "algorithmic_bytes_per_launch": bwd_bytes, "avg_launch_us": bwd_t * 1e6},
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(os.cpu_count() or 1)
+        bs = min(B, args.cpu_sample_batch)
+        xc = x[:bs].cpu().requires_grad_(True)
+        mc = mix.cpu().requires_grad_(True)
+        gc = [q[:bs].float().cpu() for q in grads]
+        times = []
+        for _ in range(3):
+            t1 = time.perf_counter()
+            torch.autograd.grad(TM.shift_mix(xc, mc, torch.bfloat16), [xc, mc], gc)
+            times.append(time.perf_counter() - t1)
+        med = statistics.median(times[1:])
+        out["cpu_baseline"] = {
+            "value": bs * T / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"B={bs} of {B}, T={T}, C={C}, eager token shift + 3 mixes + bf16 cast "
+                       f"(language.py:344-353) forward+autograd backward, median of 2 after 1 "
+                       f"warmup; host {_cpu_model()}"),
+        }
+    return out
+
+
 def bench_e2e(steps: int, warmup: int) -> dict:
     """The 41M SpikeGPT training step: 12 layers, 512 embedding, byte vocab
     (256), B=64, T=1024, random init, synthetic tokens, bf16 autocast, fused
@@ -567,7 +661,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--event-every", type=int, default=10,
                     help="time the dominant launch with HIP events on every N-th timed step")
-    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7", "lif", "e2e41m"])
+    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7", "lif", "timemix", "e2e41m"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=20,
@@ -599,6 +693,8 @@ def main() -> int:
         out = bench_wkv7(args)
     elif args.workload == "lif":
         out = bench_lif(args)
+    elif args.workload == "timemix":
+        out = bench_timemix(args)
     elif args.workload == "e2e41m":
         out = bench_e2e(args.steps, args.warmup)
     else:

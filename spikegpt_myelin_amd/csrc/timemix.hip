@@ -129,7 +129,9 @@ __global__ __launch_bounds__(256) void shift_mix_bwd_kernel(const typename EI::r
                                                             typename EI::raw* __restrict__ gx,
                                                             float* __restrict__ partial, int B,
                                                             int T, int C) {
-  constexpr int U = 8;
+  // Steps loaded ahead: fewer for several gradients at four channels per
+  // lane, where eight would leave one or two waves per SIMD.
+  constexpr int U = (N >= 2 && VEC == 4) ? 4 : 8;
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
   const int n_tc = (T + kTmChunk - 1) / kTmChunk;
   const int wave = threadIdx.x >> 6;
