@@ -28,7 +28,8 @@ Reported beside the throughput:
 Other workloads (``--workload``): ``long`` (B=24, T=3072, C=512), ``216m``
 (B=16, T=1024, C=768, 18 layers), ``decode`` (B=256, C=768, 18 layers, fp32
 state), ``wkv7`` (RWKV-7 B=16, T=1024, H=12, N=64 forward + backward), ``c0``
-(fp32 forward B=2, T=128, C=512), ``lif`` (sequence LIF forward + backward, B=64, T=1024, C=512 bf16),
+(fp32 forward B=2, T=128, C=512), ``block_decode`` (whole 216M model one-token
+decode, B=256, fused block step in one HIP graph), ``lif`` (sequence LIF forward + backward, B=64, T=1024, C=512 bf16),
 ``timemix`` (fused token-shift mix, three vectors, same shape),
 ``e2e41m`` (the whole 41M SpikeGPT
 training step, 12 layers x 512, vocab 256, B=64, T=1024; the default run
@@ -349,6 +350,74 @@ def bench_decode(args) -> dict:
     }
 
 
+def bench_block_decode(args) -> dict:
+    """Whole-model one-token decode of the 216M SpikeGPT (18 layers x 768,
+    BPE vocab 50277, fp32 weights and state) at batch 256: the fused block-step
+    kernels and the projections, captured in one HIP graph per token
+    (spikegpt_myelin_amd.generation.StepGraph), random init, synthetic ids."""
+    from spikegpt_myelin_amd.generation import StepGraph
+    from spikegpt_myelin_amd.model import SpikeGPTConfig, SpikeLanguageModel
+
+    B, C, layers, vocab = 256, 768, 18, 50277
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    cfg = SpikeGPTConfig(vocab_size=vocab, context_length=1024, n_layer=layers, n_embd=C,
+                         dropout=0.0)
+    model = SpikeLanguageModel(cfg).to(dev).eval()
+    graph = StepGraph(model, B)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(0, vocab, (args.steps + args.warmup, B), device=dev, generator=gen)
+    for i in range(args.warmup):
+        graph.step(ids[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        graph.step(ids[args.warmup + i])
+    e1.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    step_s = e0.elapsed_time(e1) / 1e3 / args.steps
+    # Multiply-accumulates per token: 13 C^2 per layer (k, v, r, output,
+    # receptance: C^2 each; key and value: 4 C^2 each) plus the head.
+    macs = layers * 13 * C * C + C * vocab
+    flops = 2.0 * B * macs
+    out = {
+        "metric": "SpikeGPT-216M one-token decode tokens/sec (whole model, fused block step, "
+                  "HIP graph), B=256 fp32",
+        "value": B * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "block_decode_216m", "B": B, "C": C, "layers": layers,
+                   "vocab": vocab, "params": sum(p.numel() for p in model.parameters())},
+        "roofline": {"bound": "mfma", "achieved": flops / step_s / 1e12, "peak": 157.3,
+                     "unit": "TFLOP/s", "frac": flops / step_s / 1e12 / 157.3, "traffic": None,
+                     "kernel": "whole step (fp32 projections dominate), HIP-event timed"},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import step as S
+
+        sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+        sc = S.StepConfig.of(cfg)
+        cb = max(1, min(B, args.cpu_sample_batch * 4))
+        state = S.initial_state(sc, cb)
+        cids = ids[:, :cb].cpu()
+        n = 4
+        S.model_forward_step(sd, sc, cids[0], state)
+        t0 = time.perf_counter()
+        for i in range(n):
+            _, state = S.model_forward_step(sd, sc, cids[i + 1], state)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {
+            "value": cb * n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{n} tokens at batch {cb} through the oracle's eager fp32 step of the "
+                      f"same model (language.py:1434-1453 restated), torch CPU"}
+    return out
+
+
 def bench_wkv7(args) -> dict:
     """RWKV-7 DPLR forward (with state checkpoints) + backward through the C
     ABI on preallocated buffers, B=16 T=1024 H=12 N=64, bf16 I/O, fp32 state."""
@@ -661,7 +730,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--event-every", type=int, default=10,
                     help="time the dominant launch with HIP events on every N-th timed step")
-    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "wkv7", "lif", "timemix", "e2e41m"])
+    ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "block_decode", "wkv7", "lif",
+                             "timemix", "e2e41m"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=20,
@@ -689,6 +759,8 @@ def main() -> int:
         del src, dst
     if args.workload == "decode":
         out = bench_decode(args)
+    elif args.workload == "block_decode":
+        out = bench_block_decode(args)
     elif args.workload == "wkv7":
         out = bench_wkv7(args)
     elif args.workload == "lif":

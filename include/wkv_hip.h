@@ -245,6 +245,71 @@ int sigmoid_gate_forward(const void* r, const void* x, void* y, int64_t n, int d
 int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void* grad_r,
                           void* grad_x, int64_t n, int dtype, void* stream);
 
+/* ---- One-token block step (generation) ------------------------------------
+ *
+ * Replace the eager element-wise work of SpikeGPTBlock.step
+ * (src/spikegpt/language.py:1301-1335) between its projections; the caller
+ * runs the projections (GEMMs).  All tensors fp32 [B][C] unless noted; state
+ * is read from *_in and written to *_out, which may be the same buffer. */
+
+/* Pre-operation of block_step_row. */
+enum wkv_step_pre {
+  /* residual = [ln0](spike(embedding[ids]))  (language.py:1386-1394, 1317) */
+  WKV_STEP_PRE_EMBED = 0,
+  /* residual += LIF(add)  (first LIF of the block, language.py:1326-1327) */
+  WKV_STEP_PRE_LIF = 1,
+  /* residual += LIF(sigmoid(gate) * add)  (channel-mix gate :1187, second
+   * LIF :1329-1330) */
+  WKV_STEP_PRE_GATE_LIF = 2,
+  /* residual = [ln0](residual): a block's own input (language.py:1317) */
+  WKV_STEP_PRE_NONE = 3
+};
+
+typedef struct wkv_step_row_args {
+  const int64_t* ids;          /* EMBED: token ids [B] */
+  const float* embedding;      /* EMBED: [vocab][C] */
+  int64_t vocab;               /* EMBED: rows of embedding; an id outside
+                                  [0, vocab) gives a NaN row (no read) */
+  float embedding_slope;       /* EMBED: spike = [slope * e >= 0] */
+  int embedding_spike;         /* EMBED: 0 = raw embedding (spike_embedding off) */
+  const float* ln0_weight;     /* EMBED, NONE: layer 0's ln0 (NULL: none) */
+  const float* ln0_bias;
+  const float* add;            /* LIF / GATE_LIF input */
+  const float* gate;           /* GATE_LIF: receptance logits */
+  const float* membrane_in;    /* LIF membrane state */
+  float* membrane_out;
+  float lif_decay, lif_threshold, lif_reset, lif_slope;
+  int spiking;                 /* 0: LIF is the identity (config.spiking off) */
+  float* residual;             /* written (EMBED) or updated (LIF, GATE_LIF) */
+  const float* ln_weight;      /* layer norm applied to the new residual
+                                  (NULL with n_mix 0: residual update only) */
+  const float* ln_bias;
+  float ln_eps;                /* also used for ln0 */
+  const float* mix[3];         /* n_mix token-shift mixing vectors, [C] each */
+  int n_mix;                   /* 3 (time mix k, v, r), 2 (channel mix k, r),
+                                  0 (out[0] = the layer norm itself) */
+  const float* previous_in;    /* token-shift state: the previous token's
+                                  layer-norm output */
+  float* previous_out;
+  float* out[3];               /* out[j] = ln * mix[j] + previous * (1 - mix[j]) */
+  int64_t batch, channels;     /* C <= 4096 */
+} wkv_step_row_args;
+
+/* One workgroup per batch row: the pre-operation, the residual write, a
+ * layer norm, and the token-shift mixes (SpikeTimeMix.step :996-998,
+ * SpikeChannelMix.step :1181-1182), in one launch. */
+int block_step_row(int pre, const wkv_step_row_args* args, void* stream);
+
+/* WKV state update and receptance gate of SpikeTimeMix.step
+ * (language.py:999-1012): out = sigmoid(receptance) * wkv, state (numerator,
+ * denominator, log_scale) in the reference's natural-log units; time_decay and
+ * time_first [C] raw parameters (decay = -exp(time_decay)). */
+int block_step_wkv(const float* key, const float* value, const float* receptance,
+                   const float* time_decay, const float* time_first, const float* num_in,
+                   const float* den_in, const float* log_scale_in, float* num_out,
+                   float* den_out, float* log_scale_out, float* out, int64_t B, int64_t C,
+                   void* stream);
+
 /* Measurement hook; no counterpart in the reference.  Arms two HIP events
  * (hipEvent_t, created with timing enabled; either may be NULL) for the next
  * entry point called on this thread: its first kernel dispatch records

@@ -27,8 +27,28 @@ _TORCH_TO_CODE = {
     torch.float16: DTYPE_F16,
 }
 
-# Every exported entry point: name -> (restype, argtypes).
 _P = ctypes.c_void_p
+
+
+class StepRowArgs(ctypes.Structure):
+    """``wkv_step_row_args`` of ``include/wkv_hip.h`` (argument block of
+    ``block_step_row``); pointer fields hold device addresses as ints."""
+
+    _fields_ = [
+        ("ids", _P), ("embedding", _P), ("vocab", ctypes.c_int64),
+        ("embedding_slope", ctypes.c_float), ("embedding_spike", ctypes.c_int),
+        ("ln0_weight", _P), ("ln0_bias", _P),
+        ("add", _P), ("gate", _P), ("membrane_in", _P), ("membrane_out", _P),
+        ("lif_decay", ctypes.c_float), ("lif_threshold", ctypes.c_float),
+        ("lif_reset", ctypes.c_float), ("lif_slope", ctypes.c_float),
+        ("spiking", ctypes.c_int),
+        ("residual", _P), ("ln_weight", _P), ("ln_bias", _P), ("ln_eps", ctypes.c_float),
+        ("mix", _P * 3), ("n_mix", ctypes.c_int), ("previous_in", _P), ("previous_out", _P),
+        ("out", _P * 3), ("batch", ctypes.c_int64), ("channels", ctypes.c_int64),
+    ]
+
+
+# Every exported entry point: name -> (restype, argtypes).
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
@@ -85,6 +105,8 @@ SIGNATURES = {
     "relu_square_backward": (_INT, [_P, _P, _P, _I64, _INT, _P]),
     "sigmoid_gate_forward": (_INT, [_P, _P, _P, _I64, _INT, _P]),
     "sigmoid_gate_backward": (_INT, [_P, _P, _P, _P, _P, _I64, _INT, _P]),
+    "block_step_row": (_INT, [_INT, ctypes.POINTER(StepRowArgs), _P]),
+    "block_step_wkv": (_INT, [_P] * 12 + [_I64, _I64, _P]),
     "wkv_time_next_call": (_INT, [_P, _P]),
     "wkv_last_error_string": (ctypes.c_char_p, []),
     "wkv_version": (ctypes.c_char_p, []),

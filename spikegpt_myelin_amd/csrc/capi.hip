@@ -106,6 +106,10 @@ int relu_square_backward_impl(const void*, const void*, void*, int64_t, int, hip
 int sigmoid_gate_forward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
 int sigmoid_gate_backward_impl(const void*, const void*, const void*, void*, void*, int64_t, int,
                                hipStream_t);
+int block_step_row_impl(int, const wkv_step_row_args&, hipStream_t);
+int block_step_wkv_impl(const float*, const float*, const float*, const float*, const float*,
+                        const float*, const float*, const float*, float*, float*, float*, float*,
+                        int64_t, int64_t, hipStream_t);
 
 static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }
 
@@ -565,6 +569,62 @@ int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void
     return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_backward: tensors must be 16-byte aligned");
   return sigmoid_gate_backward_impl(r, x, grad_y, grad_r, grad_x, n, dtype,
                                     static_cast<hipStream_t>(stream));
+}
+
+int block_step_row(int pre, const wkv_step_row_args* a, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!a) return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null args");
+  if (pre < WKV_STEP_PRE_EMBED || pre > WKV_STEP_PRE_NONE)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: unknown pre-operation");
+  if (a->batch < 0 || a->batch >= (int64_t(1) << 31) || a->channels < 1 || a->channels > 4096)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: batch >= 0 and 1 <= channels <= 4096");
+  if (a->n_mix != 0 && a->n_mix != 2 && a->n_mix != 3)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: n_mix must be 0, 2 or 3");
+  if (a->batch == 0) return WKV_OK;
+  if (!a->residual) return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null residual");
+  if (a->ln_weight == nullptr && a->n_mix != 0)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: token shift needs the layer norm");
+  if (a->ln_weight != nullptr && (!a->ln_bias || !a->out[0]))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null layer-norm bias or output");
+  for (int j = 1; j < a->n_mix; ++j)
+    if (!a->out[j]) return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null output");
+  if (a->n_mix > 0 && (!a->previous_in || !a->previous_out))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null token-shift state");
+  for (int j = 0; j < a->n_mix; ++j)
+    if (!a->mix[j]) return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null mixing vector");
+  if (pre == WKV_STEP_PRE_EMBED || pre == WKV_STEP_PRE_NONE) {
+    if (pre == WKV_STEP_PRE_EMBED && (!a->ids || !a->embedding || a->vocab < 1))
+      return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null ids or embedding");
+    if ((a->ln0_weight == nullptr) != (a->ln0_bias == nullptr))
+      return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: ln0 weight and bias go together");
+  } else {
+    if (!a->add || !a->membrane_in || !a->membrane_out)
+      return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null LIF input or membrane");
+    if (pre == WKV_STEP_PRE_GATE_LIF && !a->gate)
+      return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: null gate");
+  }
+  if (!(a->ln_eps > 0.f)) return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_row: ln_eps > 0");
+  return block_step_row_impl(pre, *a, static_cast<hipStream_t>(stream));
+}
+
+int block_step_wkv(const float* key, const float* value, const float* receptance,
+                   const float* time_decay, const float* time_first, const float* num_in,
+                   const float* den_in, const float* log_scale_in, float* num_out,
+                   float* den_out, float* log_scale_out, float* out, int64_t B, int64_t C,
+                   void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (B < 0 || C < 0 || B >= (int64_t(1) << 31) || C >= (int64_t(1) << 31) ||
+      B * C >= (int64_t(1) << 40))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_wkv: bad sizes");
+  if (B == 0 || C == 0) return WKV_OK;
+  if (!key || !value || !receptance || !time_decay || !time_first || !num_in || !den_in ||
+      !log_scale_in || !num_out || !den_out || !log_scale_out || !out)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "block_step_wkv: null pointer");
+  return block_step_wkv_impl(key, value, receptance, time_decay, time_first, num_in, den_in,
+                             log_scale_in, num_out, den_out, log_scale_out, out, B, C,
+                             static_cast<hipStream_t>(stream));
 }
 
 int wkv_time_next_call(void* start_event, void* stop_event) {

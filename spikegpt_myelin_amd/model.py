@@ -27,7 +27,11 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
+from . import generation
 from .gates import relu_square, sigmoid_gate
+from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguageModelState,
+                         SpikeTimeMixState, SpikingSequenceLIFState, StepWorkspace, block_step,
+                         initial_packed, pack_state, state_from_packed)
 from .language import weighted_key_value
 from .lif import lif_sequence
 from .timemix import token_shift_mix
@@ -249,6 +253,25 @@ class SpikeGPTBlock(nn.Module):
         self.lif2 = make_lif()
         self.dropout = nn.Dropout(config.dropout)
 
+    def initial_state(self, *, batch_size: int, device: torch.device | None = None,
+                      dtype: torch.dtype | None = None) -> SpikeGPTBlockState:
+        """``language.py:1270-1299``: zero state, log-scale at finfo(fp32).min
+        (fp32 whatever ``dtype`` says)."""
+        dev = self.ln1.weight.device if device is None else torch.device(device)
+        return state_from_packed(initial_packed(1, batch_size, self.config.n_embd, dev)).blocks[0]
+
+    def step(self, inputs: Tensor, state: SpikeGPTBlockState) -> tuple[Tensor, SpikeGPTBlockState]:
+        """``language.py:1301-1335``: one token through the block (the fused
+        block-step kernels, fp32, eval semantics)."""
+        if inputs.ndim != 2:
+            raise ValueError(f"inputs must have shape [B, C]; got {inputs.shape}")
+        src = pack_state(SpikeLanguageModelState(blocks=(state,)))[0]
+        dst = torch.empty_like(src)
+        ws = StepWorkspace(inputs.shape[0], self.config.n_embd, self.ffn.key.out_features, 1,
+                           inputs.device)
+        out = block_step(self, inputs.float().contiguous(), src, dst, ws)
+        return out.clone(), state_from_packed(dst.unsqueeze(0)).blocks[0]
+
     def forward(self, inputs: Tensor) -> Tensor:
         residual = self.ln0(inputs) if self.ln0 is not None else inputs
         residual = residual + self.lif1(self.att(self.ln1(residual)))
@@ -305,3 +328,60 @@ class SpikeLanguageModel(nn.Module):
         logits = self.head(self.ln_out(hidden))
         loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1))
         return loss, logits
+
+    # ------------------------------------------------ recurrent generation --
+    def initial_state(self, *, batch_size: int, device: torch.device | None = None,
+                      dtype: torch.dtype | None = None) -> SpikeLanguageModelState:
+        """``language.py:1410-1432`` (fp32 state whatever ``dtype`` says)."""
+        return generation.initial_state(self, batch_size=batch_size, device=device, dtype=dtype)
+
+    def forward_step(self, input_ids: Tensor,
+                     state: SpikeLanguageModelState) -> tuple[Tensor, SpikeLanguageModelState]:
+        """``language.py:1434-1453``: one token for every batch row through
+        the fused block-step kernels; returns logits [B, vocab] and the new
+        state (the given state is not modified)."""
+        return generation.forward_step(self, input_ids, state)
+
+    @torch.no_grad()
+    def generate(self, input_ids: Tensor, *, max_new_tokens: int, temperature: float = 1.0,
+                 top_k: int | None = None, sampling: str = "multinomial",
+                 use_cache: bool = True, use_graph: bool = True) -> Tensor:
+        """``language.py:1455-1524``.  ``use_cache`` runs the recurrent state
+        (``use_graph``: one captured HIP graph per token); otherwise the
+        context window is recomputed with the sequence forward each token."""
+        was_training = self.training
+        self.eval()
+        try:
+            if use_cache:
+                new = list(generation.generate_tokens(
+                    self, input_ids, max_new_tokens=max_new_tokens, temperature=temperature,
+                    top_k=top_k, sampling=sampling, use_graph=use_graph))
+                return torch.cat([input_ids, *new], dim=1)
+            generation._check_generate_args(input_ids, max_new_tokens, temperature, top_k,
+                                            sampling)
+            output = input_ids
+            for _ in range(max_new_tokens):
+                logits = self(output[:, -self.config.context_length:])
+                nxt = generation.sample_next_token(logits[:, -1], temperature=temperature,
+                                                   top_k=top_k, sampling=sampling)
+                output = torch.cat((output, nxt), dim=1)
+            return output
+        finally:
+            if was_training:
+                self.train()
+
+    def generate_stream(self, input_ids: Tensor, *, max_new_tokens: int,
+                        temperature: float = 1.0, top_k: int | None = None,
+                        sampling: str = "multinomial", use_graph: bool = True):
+        """``language.py:1526-1573``: yields one [B, 1] token per step, sampled
+        as :meth:`generate` with ``use_cache=True``."""
+        was_training = self.training
+        self.eval()
+        try:
+            with torch.no_grad():
+                yield from generation.generate_tokens(
+                    self, input_ids, max_new_tokens=max_new_tokens, temperature=temperature,
+                    top_k=top_k, sampling=sampling, use_graph=use_graph)
+        finally:
+            if was_training:
+                self.train()

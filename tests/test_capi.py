@@ -77,3 +77,51 @@ def test_backward_workspace_size_and_check(lib):
     rc = lib.wkv4_backward(addr, addr, addr, addr, addr, addr, addr, addr, addr, addr, 16,
                            2, 8, 8, 1, None)
     assert rc == 3 and b"workspace" in lib.wkv_last_error_string()
+
+
+def test_step_row_args_layout_matches_header(tmp_path):
+    # The ctypes mirror of wkv_step_row_args has the C struct's size and field
+    # offsets (compiled with the host C compiler from the header).
+    import shutil
+    import subprocess
+
+    from spikegpt_myelin_amd import _lib
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    fields = [f for f, _ in _lib.StepRowArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("%zu\\n", offsetof(wkv_step_row_args, {f}));\n' for f in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "wkv_hip.h"\n'
+                   "int main(void) {\n" + body +
+                   '  printf("%zu\\n", sizeof(wkv_step_row_args));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    want = [getattr(_lib.StepRowArgs, f).offset for f in fields] + [ctypes.sizeof(_lib.StepRowArgs)]
+    assert got == want
+
+
+def test_block_step_argument_errors(lib):
+    from spikegpt_myelin_amd import _lib
+
+    a = _lib.StepRowArgs()
+    a.batch, a.channels = 2, 8
+    assert lib.block_step_row(0, ctypes.byref(a), None) == 1  # null residual
+    a.residual = 16
+    a.channels = 5000
+    assert lib.block_step_row(1, ctypes.byref(a), None) == 1
+    assert b"4096" in lib.wkv_last_error_string()
+    a.channels, a.n_mix = 8, 1
+    assert lib.block_step_row(1, ctypes.byref(a), None) == 1
+    assert b"n_mix" in lib.wkv_last_error_string()
+    a.n_mix = 2  # token shift without a layer norm
+    assert lib.block_step_row(1, ctypes.byref(a), None) == 1
+    assert lib.block_step_row(9, ctypes.byref(a), None) == 1
+    a.batch = 0
+    a.n_mix = 0
+    assert lib.block_step_row(1, ctypes.byref(a), None) == 0  # empty batch: no-op
+    assert lib.block_step_wkv(*([None] * 12), 2, 8, None) == 1
+    assert lib.block_step_wkv(*([None] * 12), 0, 8, None) == 0
