@@ -15,7 +15,11 @@ spikegpt_myelin_amd.build``):
 * ``myelin::token_shift_mix`` / ``myelin::token_shift_mix_backward`` -- the
   fused token-shift mixing that feeds the block projections (differentiable).
 
-:mod:`spikegpt_myelin_amd.model` holds the SpikeGPT model built on them.
+:mod:`spikegpt_myelin_amd.model` holds the SpikeGPT model built on them;
+:mod:`spikegpt_myelin_amd.generation` its recurrent one-token step (the fused
+block-step kernels, optionally captured in a HIP graph) and
+:mod:`spikegpt_myelin_amd.checkpoint` the reference's checkpoint format
+(``myelin.spike_language_checkpoint.v1``) and vocabularies.
 """
 
 from .decode import initial_wkv_state, wkv_decode_step

@@ -150,3 +150,19 @@ def test_generate_cached_graph_eager_and_uncached_agree():
     assert torch.equal(a, b) and torch.equal(a, c)
     streamed = torch.cat(list(model.generate_stream(ids, max_new_tokens=6, sampling="greedy")), 1)
     assert torch.equal(streamed, a[:, 4:])
+
+
+def test_checkpoint_round_trip_runs_the_same_model(tmp_path):
+    from spikegpt_myelin_amd import checkpoint as K
+
+    model = _model(64, layers=2, ctx=12, vocab=20)
+    vocab = K.CharacterVocabulary(tokens=tuple(chr(97 + i) for i in range(20)))
+    path = tmp_path / "m.pt"
+    K.save_spike_language_checkpoint(path, model, vocab, metadata={"note": "gpu"})
+    ck = K.load_spike_language_checkpoint(path, map_location="cpu")
+    loaded = ck.model.to(DEV).eval()
+    ids = vocab.encode("abcdefgh").view(2, 4).to(DEV)
+    with torch.no_grad():
+        torch.testing.assert_close(loaded(ids), model(ids), atol=0, rtol=0)
+    assert torch.equal(loaded.generate(ids, max_new_tokens=4, sampling="greedy"),
+                       model.generate(ids, max_new_tokens=4, sampling="greedy"))
