@@ -245,6 +245,34 @@ int sigmoid_gate_forward(const void* r, const void* x, void* y, int64_t n, int d
 int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void* grad_r,
                           void* grad_x, int64_t n, int dtype, void* stream);
 
+/* ---- Layer norm fused into the token-shift mix -----------------------------
+ *
+ * Replaces a block half's layer norm followed by its token-shift mixes,
+ * self.att(self.ln1(x)) / self.ffn(self.ln2(x)) with _mix_with_previous
+ * (src/spikegpt/language.py:1341-1356, 344-353): per row, F.layer_norm with
+ * weight and bias, then out_j = y mu_j + y[t-1] (1 - mu_j), rounded once to
+ * out_dtype.  x fp32 [B,T,C] with C = 256 or 512; weight, bias fp32 [C]; mix
+ * fp32 [n][C], n = 2 or 3; out0..out{n-1} [B,T,C]; mean, rstd fp32 [B*T]
+ * (saved for the backward). */
+int layer_norm_shift_mix_forward(const float* x, const float* weight, const float* bias,
+                                 float eps, const float* mix, int64_t n, void* out0, void* out1,
+                                 void* out2, int out_dtype, float* mean, float* rstd, int64_t B,
+                                 int64_t T, int64_t C, void* stream);
+
+/* Bytes of workspace layer_norm_shift_mix_backward needs (column partial
+ * sums), 0 for unsupported sizes. */
+size_t layer_norm_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int64_t C);
+
+/* Backward: grad0..grad{n-1} [B,T,C] in g_dtype; writes grad_x fp32 [B,T,C]
+ * and grad_params fp32 [n + 2][C] = (grad_mix_0 .. grad_mix_{n-1},
+ * grad_weight, grad_bias), each summed over all rows in a fixed order. */
+int layer_norm_shift_mix_backward(const float* x, const float* weight, const float* bias,
+                                  const float* mix, int64_t n, const float* mean,
+                                  const float* rstd, const void* grad0, const void* grad1,
+                                  const void* grad2, int g_dtype, float* grad_x,
+                                  float* grad_params, void* workspace, size_t workspace_bytes,
+                                  int64_t B, int64_t T, int64_t C, void* stream);
+
 /* ---- One-token block step (generation) ------------------------------------
  *
  * Replace the eager element-wise work of SpikeGPTBlock.step

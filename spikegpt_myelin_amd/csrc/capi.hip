@@ -107,6 +107,12 @@ int sigmoid_gate_forward_impl(const void*, const void*, void*, int64_t, int, hip
 int sigmoid_gate_backward_impl(const void*, const void*, const void*, void*, void*, int64_t, int,
                                hipStream_t);
 int block_step_row_impl(int, const wkv_step_row_args&, hipStream_t);
+int ln_mix_forward_impl(const float*, const float*, const float*, const float*, int, void* const*,
+                        int, float*, float*, int, int, int, float, hipStream_t);
+int ln_mix_backward_impl(const float*, const float*, const float*, const float*, int,
+                         const float*, const float*, const void* const*, int, float*, float*,
+                         float*, int, int, int, hipStream_t);
+int64_t ln_mix_workgroups(int64_t, int64_t);
 int block_step_wkv_impl(const float*, const float*, const float*, const float*, const float*,
                         const float*, const float*, const float*, float*, float*, float*, float*,
                         int64_t, int64_t, hipStream_t);
@@ -569,6 +575,74 @@ int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void
     return fail(WKV_ERR_INVALID_ARGUMENT, "sigmoid_gate_backward: tensors must be 16-byte aligned");
   return sigmoid_gate_backward_impl(r, x, grad_y, grad_r, grad_x, n, dtype,
                                     static_cast<hipStream_t>(stream));
+}
+
+static bool ln_mix_dims_ok(int64_t n, int64_t B, int64_t T, int64_t C) {
+  return (n == 2 || n == 3) && (C == 256 || C == 512) && dims_ok(B, T, C) &&
+         B * T < (int64_t(1) << 31);
+}
+
+int layer_norm_shift_mix_forward(const float* x, const float* weight, const float* bias,
+                                 float eps, const float* mix, int64_t n, void* out0, void* out1,
+                                 void* out2, int out_dtype, float* mean, float* rstd, int64_t B,
+                                 int64_t T, int64_t C, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(out_dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "layer_norm_shift_mix_forward: unknown dtype");
+  if (!ln_mix_dims_ok(n, B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "layer_norm_shift_mix_forward: n in {2, 3}, C in {256, 512}, valid sizes");
+  if (!(eps > 0.f)) return fail(WKV_ERR_INVALID_ARGUMENT, "layer_norm_shift_mix_forward: eps > 0");
+  if (B == 0 || T == 0) return WKV_OK;
+  void* const out[3] = {out0, out1, out2};
+  if (!x || !weight || !bias || !mix || !mean || !rstd)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "layer_norm_shift_mix_forward: null pointer");
+  for (int j = 0; j < n; ++j)
+    if (!out[j] || !aligned16({out[j]}))
+      return fail(WKV_ERR_INVALID_ARGUMENT,
+                  "layer_norm_shift_mix_forward: null or unaligned output");
+  if (!aligned16({x, weight, bias, mix}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "layer_norm_shift_mix_forward: tensors must be 16-byte aligned");
+  return ln_mix_forward_impl(x, weight, bias, mix, int(n), out, out_dtype, mean, rstd, int(B),
+                             int(T), int(C), eps, static_cast<hipStream_t>(stream));
+}
+
+size_t layer_norm_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int64_t C) {
+  if (!ln_mix_dims_ok(n, B, T, C)) return 0;
+  return size_t(n + 2) * size_t(ln_mix_workgroups(B, T)) * size_t(C) * sizeof(float);
+}
+
+int layer_norm_shift_mix_backward(const float* x, const float* weight, const float* bias,
+                                  const float* mix, int64_t n, const float* mean,
+                                  const float* rstd, const void* grad0, const void* grad1,
+                                  const void* grad2, int g_dtype, float* grad_x,
+                                  float* grad_params, void* workspace, size_t workspace_bytes,
+                                  int64_t B, int64_t T, int64_t C, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(g_dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "layer_norm_shift_mix_backward: unknown dtype");
+  if (!ln_mix_dims_ok(n, B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "layer_norm_shift_mix_backward: n in {2, 3}, C in {256, 512}, valid sizes");
+  if (B == 0 || T == 0) return WKV_OK;  // the caller zero-fills grad_params
+  const void* const g[3] = {grad0, grad1, grad2};
+  if (!x || !weight || !bias || !mix || !mean || !rstd || !grad_x || !grad_params || !workspace)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "layer_norm_shift_mix_backward: null pointer");
+  for (int j = 0; j < n; ++j)
+    if (!g[j] || !aligned16({g[j]}))
+      return fail(WKV_ERR_INVALID_ARGUMENT,
+                  "layer_norm_shift_mix_backward: null or unaligned gradient");
+  if (!aligned16({x, weight, bias, mix, grad_x, workspace}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "layer_norm_shift_mix_backward: tensors must be 16-byte aligned");
+  if (workspace_bytes < layer_norm_shift_mix_workspace_bytes(n, B, T, C))
+    return fail(WKV_ERR_WORKSPACE_TOO_SMALL, "layer_norm_shift_mix_backward: workspace too small");
+  return ln_mix_backward_impl(x, weight, bias, mix, int(n), mean, rstd, g, g_dtype, grad_x,
+                              static_cast<float*>(workspace), grad_params, int(B), int(T),
+                              int(C), static_cast<hipStream_t>(stream));
 }
 
 int block_step_row(int pre, const wkv_step_row_args* a, void* stream) {

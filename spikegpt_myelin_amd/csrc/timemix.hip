@@ -217,30 +217,6 @@ __global__ __launch_bounds__(256) void shift_mix_bwd_kernel(const typename EI::r
   }
 }
 
-// out[r][c] = sum_p partial[r][p][c] over P partial rows, fixed order: 16
-// threads per channel each sum every 16th row, then a fixed LDS tree.
-__global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restrict__ partial,
-                                                          float* __restrict__ out, int P, int C) {
-  constexpr int G = 16;
-  __shared__ float sh[G][64];
-  const int lane = threadIdx.x & 63;
-  const int grp = threadIdx.x >> 6;
-  const int r = blockIdx.y;
-  const int c = blockIdx.x * 64 + lane;
-  float a = 0.f;
-  if (c < C) {
-    const float* src = partial + size_t(r) * P * C + c;
-    for (int p = grp; p < P; p += G) a += src[size_t(p) * C];
-  }
-  sh[grp][lane] = a;
-  __syncthreads();
-  for (int h = G / 2; h > 0; h >>= 1) {
-    if (grp < h) sh[grp][lane] += sh[grp + h][lane];
-    __syncthreads();
-  }
-  if (grp == 0 && c < C) out[size_t(r) * C + c] = sh[0][lane];
-}
-
 }  // namespace wkv
 
 // ------------------------------------------------------------ launchers ----
@@ -309,7 +285,7 @@ static int bwd_launch(const void* x, const float* mix, const void* const* g, voi
   int rc = check_launch("shift_mix_bwd_kernel");
   if (rc) return rc;
   const int P = B * ((T + wkv::kTmChunk - 1) / wkv::kTmChunk);
-  launch(wkv::column_sum_kernel, dim3(unsigned((C + 63) / 64), unsigned(N)), dim3(1024), stream,
+  launch(wkv::column_sum_kernel<16>, dim3(unsigned((C + 63) / 64), unsigned(N)), dim3(1024), stream,
          true, static_cast<const float*>(partial), gmix, P, C);
   return check_launch("column_sum_kernel");
 }

@@ -378,4 +378,30 @@ __device__ __forceinline__ void store_buf(const OutPack<E, VEC>& o, rsrc_t r, un
   }
 }
 
+// out[r][c] = sum_p partial[r][p][c] over P partial rows in a fixed order:
+// G threads per channel (G x 64 = the workgroup) each sum every G-th row,
+// then a fixed LDS tree.  A template so that each translation unit that
+// launches it holds its own copy.
+template <int G>
+__global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restrict__ partial,
+                                                          float* __restrict__ out, int P, int C) {
+  __shared__ float sh[G][64];
+  const int lane = threadIdx.x & 63;
+  const int grp = threadIdx.x >> 6;
+  const int r = blockIdx.y;
+  const int c = blockIdx.x * 64 + lane;
+  float a = 0.f;
+  if (c < C) {
+    const float* src = partial + size_t(r) * P * C + c;
+    for (int p = grp; p < P; p += G) a += src[size_t(p) * C];
+  }
+  sh[grp][lane] = a;
+  __syncthreads();
+  for (int h = G / 2; h > 0; h >>= 1) {
+    if (grp < h) sh[grp][lane] += sh[grp + h][lane];
+    __syncthreads();
+  }
+  if (grp == 0 && c < C) out[size_t(r) * C + c] = sh[0][lane];
+}
+
 }  // namespace wkv

@@ -8,11 +8,12 @@ mix through ``myelin::wkv_forward{,_bf16io}`` (``SpikeTimeMix.forward``,
 ``language.py:1015-1036``) and the spiking activations through
 ``myelin::lif_sequence_forward`` (``SpikingSequenceLIF.forward``,
 ``language.py:848-918``), and the token-shift mixes that feed the
-projections through one fused ``myelin::token_shift_mix`` pass per block
-half (``language.py:344-353``), and the squared ReLU and receptance gates
+projections through one fused ``myelin::layer_norm_shift_mix`` pass per
+block half (the half's layer norm and its token-shift mixes,
+``language.py:344-353, 1341-1356``), and the squared ReLU and receptance gates
 through ``myelin::relu_square`` / ``myelin::sigmoid_gate``; linear layers
-(with split-K weight gradients), layer norms and the loss are PyTorch-ROCm
-(hipBLASLt GEMMs).
+(with split-K weight gradients), the first block's ``ln0``, ``ln_out`` and
+the loss are PyTorch-ROCm (hipBLASLt GEMMs).
 
 Supported configuration: ``model_type="rwkv"``, ``attention="rwkv"``,
 ``spike_input=False`` (the reference defaults, ``language.py:234-256``).
@@ -34,7 +35,7 @@ from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguage
                          initial_packed, pack_state, state_from_packed)
 from .language import weighted_key_value
 from .lif import lif_sequence
-from .timemix import token_shift_mix
+from .timemix import layer_norm_shift_mix, token_shift_mix
 
 
 @dataclass
@@ -199,10 +200,16 @@ class SpikeTimeMix(nn.Module):
         self.receptance = SplitKLinear(n_embd, attn, bias=False)
         self.output = SplitKLinear(attn, n_embd, bias=False)
 
+    def mixes(self) -> Tensor:
+        """The k, v, r mixing vectors stacked ``[3, C]``."""
+        return torch.stack([self.time_mix_k.view(-1), self.time_mix_v.view(-1),
+                            self.time_mix_r.view(-1)])
+
     def forward(self, inputs: Tensor) -> Tensor:
-        mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_v.view(-1),
-                             self.time_mix_r.view(-1)])
-        k_in, v_in, r_in = token_shift_mix(inputs, mixes)
+        return self.project(*token_shift_mix(inputs, self.mixes()))
+
+    def project(self, k_in: Tensor, v_in: Tensor, r_in: Tensor) -> Tensor:
+        """Everything after the token-shift mixes (``language.py:1019-1036``)."""
         key = self.key(k_in)
         value = self.value(v_in)
         wkv = weighted_key_value(key, value, self.time_decay, self.time_first)
@@ -222,9 +229,15 @@ class SpikeChannelMix(nn.Module):
         self.receptance = SplitKLinear(n_embd, n_embd, bias=False)
         self.value = SplitKLinear(4 * n_embd, n_embd, bias=False)
 
+    def mixes(self) -> Tensor:
+        """The k, r mixing vectors stacked ``[2, C]``."""
+        return torch.stack([self.time_mix_k.view(-1), self.time_mix_r.view(-1)])
+
     def forward(self, inputs: Tensor) -> Tensor:
-        mixes = torch.stack([self.time_mix_k.view(-1), self.time_mix_r.view(-1)])
-        k_in, r_in = token_shift_mix(inputs, mixes)
+        return self.project(*token_shift_mix(inputs, self.mixes()))
+
+    def project(self, k_in: Tensor, r_in: Tensor) -> Tensor:
+        """Everything after the token-shift mixes (``language.py:1192-1196``)."""
         key = relu_square(self.key(k_in))
         return sigmoid_gate(self.receptance(r_in), self.value(key))
 
@@ -273,9 +286,13 @@ class SpikeGPTBlock(nn.Module):
         return out.clone(), state_from_packed(dst.unsqueeze(0)).blocks[0]
 
     def forward(self, inputs: Tensor) -> Tensor:
+        # att(ln1(x)) and ffn(ln2(x)) with each layer norm folded into the
+        # half's token-shift kernel (layer_norm_shift_mix).
         residual = self.ln0(inputs) if self.ln0 is not None else inputs
-        residual = residual + self.lif1(self.att(self.ln1(residual)))
-        residual = residual + self.lif2(self.ffn(self.ln2(residual)))
+        att = self.att.project(*layer_norm_shift_mix(residual, self.ln1, self.att.mixes()))
+        residual = residual + self.lif1(att)
+        ffn = self.ffn.project(*layer_norm_shift_mix(residual, self.ln2, self.ffn.mixes()))
+        residual = residual + self.lif2(ffn)
         return self.dropout(residual)
 
 

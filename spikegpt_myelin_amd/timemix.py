@@ -118,3 +118,118 @@ def token_shift_mix(x: Tensor, mix: Tensor) -> list[Tensor]:
     else:
         out_dtype = x.dtype if x.dtype in _NATIVE else torch.float32
     return torch.ops.myelin.token_shift_mix(x, mix, out_dtype)
+
+
+# ------------------------------------------------ layer norm + token shift --
+# myelin::layer_norm_shift_mix(Tensor x, Tensor weight, Tensor bias, Tensor mix,
+#     float eps, ScalarType out_dtype) -> Tensor[]
+# returns the n mixed tensors followed by the per-row mean and rstd [B*T]
+# (saved for the backward): a block half's F.layer_norm and token-shift mixes
+# (language.py:1341-1356, 344-353) in one pass over x.
+LN_MIX_CHANNELS = (256, 512)
+
+
+@torch.library.custom_op("myelin::layer_norm_shift_mix", mutates_args=())
+def _ln_shift_mix(x: Tensor, weight: Tensor, bias: Tensor, mix: Tensor, eps: float,
+                  out_dtype: torch.dtype) -> list[Tensor]:
+    _lib.require_gpu(x, weight, bias, mix)
+    _check(x, mix)
+    b, t, c = x.shape
+    if x.dtype != torch.float32 or c not in LN_MIX_CHANNELS or mix.shape[0] < 2:
+        raise ValueError("layer_norm_shift_mix takes fp32 x with C in (256, 512) and 2-3 mixes")
+    xs = _lib.aligned(x)
+    w, bb = _lib.aligned(weight.float()), _lib.aligned(bias.float())
+    mx = _lib.aligned(mix.float())
+    n = mx.shape[0]
+    outs = [torch.empty(xs.shape, dtype=out_dtype, device=x.device) for _ in range(n)]
+    mean = torch.empty(b * t, dtype=torch.float32, device=x.device)
+    rstd = torch.empty_like(mean)
+    ptrs = [o.data_ptr() for o in outs] + [None] * (3 - n)
+    lib = _lib.load()
+    rc = _lib.timed("layer_norm_shift_mix", x.device, lambda: lib.layer_norm_shift_mix_forward(
+        xs.data_ptr(), w.data_ptr(), bb.data_ptr(), eps, mx.data_ptr(), n, *ptrs,
+        _lib.dtype_code(out_dtype), mean.data_ptr(), rstd.data_ptr(), b, t, c,
+        _lib.stream_of(xs)))
+    _lib.check(rc, "layer_norm_shift_mix_forward")
+    return outs + [mean, rstd]
+
+
+@_ln_shift_mix.register_fake
+def _(x, weight, bias, mix, eps, out_dtype):
+    b, t, _ = x.shape
+    return ([torch.empty(x.shape, dtype=out_dtype, device=x.device) for _ in range(mix.shape[0])]
+            + [x.new_empty(b * t, dtype=torch.float32), x.new_empty(b * t, dtype=torch.float32)])
+
+
+@torch.library.custom_op("myelin::layer_norm_shift_mix_backward", mutates_args=())
+def _ln_shift_mix_backward(grads: list[Tensor], x: Tensor, weight: Tensor, bias: Tensor,
+                           mix: Tensor, mean: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
+    """Returns ``grad_x`` [B, T, C] fp32 and ``[n + 2, C]`` fp32 parameter
+    gradients (the n mixing vectors, the weight, the bias)."""
+    _lib.require_gpu(x, weight, bias, mix, mean, rstd, *grads)
+    b, t, c = x.shape
+    n = mix.shape[0]
+    gdt = grads[0].dtype if grads[0].dtype in _NATIVE else torch.float32
+    gs = [_lib.aligned(g.to(gdt)) for g in grads]
+    xs = _lib.aligned(x)
+    w, bb, mx = (_lib.aligned(p.float()) for p in (weight, bias, mix))
+    gx = torch.empty_like(xs)
+    gp = torch.zeros((n + 2, c), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.layer_norm_shift_mix_workspace_bytes(n, b, t, c)), 16),
+                     dtype=torch.uint8, device=x.device)
+    ptrs = [g.data_ptr() for g in gs] + [None] * (3 - n)
+    rc = _lib.timed("layer_norm_shift_mix_backward", x.device,
+                    lambda: lib.layer_norm_shift_mix_backward(
+                        xs.data_ptr(), w.data_ptr(), bb.data_ptr(), mx.data_ptr(), n,
+                        mean.data_ptr(), rstd.data_ptr(), *ptrs, _lib.dtype_code(gdt),
+                        gx.data_ptr(), gp.data_ptr(), ws.data_ptr(), ws.numel(), b, t, c,
+                        _lib.stream_of(xs)))
+    _lib.check(rc, "layer_norm_shift_mix_backward")
+    return gx, gp
+
+
+@_ln_shift_mix_backward.register_fake
+def _(grads, x, weight, bias, mix, mean, rstd):
+    return (torch.empty(x.shape, dtype=torch.float32, device=x.device),
+            x.new_empty((mix.shape[0] + 2, x.shape[2]), dtype=torch.float32))
+
+
+def _ln_setup_context(ctx, inputs, output):
+    x, weight, bias, mix, _, _ = inputs
+    mean, rstd = output[-2], output[-1]
+    ctx.save_for_backward(x, weight, bias, mix, mean, rstd)
+
+
+def _ln_backward(ctx, grads):
+    x, weight, bias, mix, mean, rstd = ctx.saved_tensors
+    n = mix.shape[0]
+    gouts = [torch.zeros(x.shape, dtype=torch.float32, device=x.device) if g is None else g
+             for g in grads[:n]]
+    gx, gp = torch.ops.myelin.layer_norm_shift_mix_backward(gouts, x, weight, bias, mix, mean,
+                                                           rstd)
+    return (gx, gp[n].to(weight.dtype), gp[n + 1].to(bias.dtype), gp[:n].to(mix.dtype), None,
+            None)
+
+
+_ln_shift_mix.register_autograd(_ln_backward, setup_context=_ln_setup_context)
+
+
+def layer_norm_shift_mix(x: Tensor, norm: torch.nn.LayerNorm, mix: Tensor) -> list[Tensor]:
+    """``token_shift_mix(norm(x), mix)`` (values of the eager layer norm and
+    mixes, in the autocast dtype when CUDA autocast is on), fused into one
+    kernel pair when ``x`` is fp32 on the GPU with C in (256, 512) and 2-3
+    mixing vectors; otherwise the layer norm and :func:`token_shift_mix`."""
+    c = x.shape[-1]
+    fusable = (x.is_cuda and x.dtype == torch.float32 and x.ndim == 3 and c in LN_MIX_CHANNELS
+               and mix.ndim == 2 and 2 <= mix.shape[0] <= 3 and norm.weight is not None
+               and norm.bias is not None and tuple(norm.normalized_shape) == (c,))
+    if not fusable:
+        return token_shift_mix(norm(x), mix)
+    if torch.is_autocast_enabled("cuda"):
+        out_dtype = torch.get_autocast_dtype("cuda")
+    else:
+        out_dtype = torch.float32
+    outs = torch.ops.myelin.layer_norm_shift_mix(x, norm.weight, norm.bias, mix, float(norm.eps),
+                                                out_dtype)
+    return list(outs[:-2])

@@ -64,6 +64,11 @@ def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
             mp.setattr(M, "weighted_key_value", _oracle_wkv)
             mp.setattr(M, "lif_sequence", _oracle_lif)
             mp.setattr(M, "token_shift_mix", _oracle_mix)
+            # The block's fused layer norm + mix becomes torch's layer norm
+            # (fp32, as autocast runs it) and the oracle's mix.
+            mp.setattr(M, "layer_norm_shift_mix", lambda x, norm, mix: _oracle_mix(
+                torch.nn.functional.layer_norm(x.float(), norm.normalized_shape, norm.weight,
+                                               norm.bias, norm.eps), mix))
             mp.setattr(M, "relu_square", lambda x: torch.relu(x).square())
             mp.setattr(M, "sigmoid_gate", lambda r, x: torch.sigmoid(r) * x)
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
