@@ -39,6 +39,14 @@ struct LifParams {
   float decay, threshold, reset, slope;
 };
 
+// Arctan surrogate derivative ds/dh = slope * 0.5 / (1 + (pi/2 c)^2) at
+// c = slope (h - threshold), with the hardware reciprocal (1 ulp) in place
+// of an IEEE division (~9 instructions on this recurrence's critical path).
+__device__ __forceinline__ float lif_surrogate(float cc, float slope) {
+  const float q = 1.5707963267948966f * cc;
+  return (0.5f * slope) * __builtin_amdgcn_rcpf(fmaf(q, q, 1.f));
+}
+
 // Loads S steps starting at t0 for the lane (buffer descriptor based at the
 // segment; steps at or past T read as zero).
 template <typename E, int VEC, int S>
@@ -137,7 +145,6 @@ __device__ __forceinline__ void lif_bwd_block(const Pack<E, VEC> (&xb)[kLifBlock
                                               size_t row_tail, unsigned lane_boff, size_t ck_row,
                                               unsigned ck_boff, int t0, int C, bool active) {
   constexpr int S = kLifBlock;
-  constexpr float kHalfPi = 1.5707963267948966f;
   Pack<F32, VEC> m0;
   m0.load(byte_offset(ck + ck_row + size_t(t0 / S) * C, ck_boff));
   float h[S][VEC];
@@ -163,8 +170,7 @@ __device__ __forceinline__ void lif_bwd_block(const Pack<E, VEC> (&xb)[kLifBlock
       const float hh = h[i][c];
       const float cc = P.slope * (hh - P.threshold);
       const float s = cc >= 0.f ? 1.f : 0.f;
-      const float q = kHalfPi * cc;
-      const float dsdh = P.slope * (0.5f / (1.f + q * q));
+      const float dsdh = lif_surrogate(cc, P.slope);
       const float gh = gb[i].get(c) * dsdh + gm[c] * ((1.f - s) + (P.reset - hh) * dsdh);
       gv[c] = gh;
       gm[c] = P.decay * gh;
@@ -375,7 +381,6 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
                                                             int T, int C, LifParams P) {
   using S = Staged<E>;
   constexpr int PB = S::kPb;
-  constexpr float kHalfPi = 1.5707963267948966f;
   __shared__ u32x4 xs[S::kInstr * 64];
   __shared__ u32x4 gl[S::kInstr * 64];
   __shared__ u32x4 os[S::kInstr * 64];
@@ -406,22 +411,25 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
     S::load(sx, x, row_base, row_tail, loff, blk - PB, nblk, C);
     S::load(sg, gs, row_base, row_tail, loff, blk - PB, nblk, C);
     sm = rec(blk - PB);
-    // Recompute the block's pre-spike membranes.
-    float h[kLifBlock];
+    // Recompute the block's pre-spike membranes h and c = slope (h - theta)
+    // (the forward's operations, so the spikes are the forward's; the wave
+    // is alone on its SIMD, so the 64 registers cost no occupancy).
+    float h[kLifBlock], cs[kLifBlock];
 #pragma unroll
     for (int s = 0; s < kLifBlock; ++s) {
       const float hh = m * P.decay + S::get(xs, s, lane);
-      const float sp = P.slope * (hh - P.threshold) >= 0.f ? 1.f : 0.f;
+      const float cc = P.slope * (hh - P.threshold);
+      const float sp = cc >= 0.f ? 1.f : 0.f;
       m = hh * (1.f - sp) + P.reset * sp;
       h[s] = hh;
+      cs[s] = cc;
     }
     // Reverse recurrence; steps past T have x = g = 0 and a zero carry.
 #pragma unroll
     for (int s = kLifBlock - 1; s >= 0; --s) {
-      const float cc = P.slope * (h[s] - P.threshold);
+      const float cc = cs[s];
       const float sp = cc >= 0.f ? 1.f : 0.f;
-      const float q2 = kHalfPi * cc;
-      const float dsdh = P.slope * (0.5f / (1.f + q2 * q2));
+      const float dsdh = lif_surrogate(cc, P.slope);
       const float gh = S::get(gl, s, lane) * dsdh + gm * ((1.f - sp) + (P.reset - h[s]) * dsdh);
       gm = P.decay * gh;
       S::put(os, s, lane, gh);
