@@ -245,6 +245,20 @@ int sigmoid_gate_forward(const void* r, const void* x, void* y, int64_t n, int d
 int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void* grad_r,
                           void* grad_x, int64_t n, int dtype, void* stream);
 
+/* LIF forward fused with the block's residual add (src/spikegpt/language.py:
+ * 1326-1330, residual + lif(...)): out = residual + spikes(x), fp32
+ * [B,T,C]; x in `dtype`; residual fp32 (out may alias it); membrane
+ * checkpoint as lif_forward.  C a multiple of 8, T*C*4 < 2^31. */
+int lif_residual_forward(const void* x, const float* residual, float* out,
+                         float* membrane_checkpoint, int64_t B, int64_t T, int64_t C, float decay,
+                         float threshold, float reset, float slope, int dtype, void* stream);
+
+/* Backward of lif_residual_forward for x: grad_x (`dtype`) from grad_out
+ * (fp32, the gradient of out; the residual's gradient is grad_out itself). */
+int lif_residual_backward(const void* x, const float* grad_out, const float* membrane_checkpoint,
+                          void* grad_x, int64_t B, int64_t T, int64_t C, float decay,
+                          float threshold, float reset, float slope, int dtype, void* stream);
+
 /* ---- Layer norm fused into the token-shift mix -----------------------------
  *
  * Replaces a block half's layer norm followed by its token-shift mixes,

@@ -101,6 +101,11 @@ int lif_forward_impl(const void*, void*, float*, int, int, int, float, float, fl
                      hipStream_t);
 int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
                       float, float, int, hipStream_t);
+int lif_residual_forward_impl(const void*, const float*, float*, float*, int, int, int, float,
+                              float, float, float, int, hipStream_t);
+int lif_residual_backward_impl(const void*, const float*, const float*, void*, int, int, int,
+                               float, float, float, float, int, hipStream_t);
+bool lif_residual_ok(int64_t, int64_t, int);
 int relu_square_forward_impl(const void*, void*, int64_t, int, hipStream_t);
 int relu_square_backward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
 int sigmoid_gate_forward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
@@ -420,6 +425,53 @@ int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, int64_t
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: tensors must be 16-byte aligned");
   return lif_forward_impl(x, spikes, membrane_checkpoint, int(B), int(T), int(C), decay, threshold,
                           reset, slope, dtype, static_cast<hipStream_t>(stream));
+}
+
+int lif_residual_forward(const void* x, const float* residual, float* out,
+                         float* membrane_checkpoint, int64_t B, int64_t T, int64_t C, float decay,
+                         float threshold, float reset, float slope, int dtype, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: bad sizes");
+  if (!lif_params_ok(decay, threshold, reset, slope))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "lif_residual_forward: parameters must be finite and surrogate_slope positive");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!lif_residual_ok(T, C, dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "lif_residual_forward: C must be a multiple of 8 and T*C*4 below 2^31");
+  if (!x || !residual || !out || !membrane_checkpoint)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: null pointer");
+  if (!aligned16({x, residual, out, membrane_checkpoint}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: tensors must be 16-byte aligned");
+  return lif_residual_forward_impl(x, residual, out, membrane_checkpoint, int(B), int(T), int(C),
+                                   decay, threshold, reset, slope, dtype,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int lif_residual_backward(const void* x, const float* grad_out, const float* membrane_checkpoint,
+                          void* grad_x, int64_t B, int64_t T, int64_t C, float decay,
+                          float threshold, float reset, float slope, int dtype, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_backward: unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_backward: bad sizes");
+  if (!lif_params_ok(decay, threshold, reset, slope))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "lif_residual_backward: parameters must be finite and surrogate_slope positive");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!lif_residual_ok(T, C, dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "lif_residual_backward: C must be a multiple of 8 and T*C*4 below 2^31");
+  if (!x || !grad_out || !membrane_checkpoint || !grad_x)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_backward: null pointer");
+  if (!aligned16({x, grad_out, membrane_checkpoint, grad_x}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_backward: tensors must be 16-byte aligned");
+  return lif_residual_backward_impl(x, grad_out, membrane_checkpoint, grad_x, int(B), int(T),
+                                    int(C), decay, threshold, reset, slope, dtype,
+                                    static_cast<hipStream_t>(stream));
 }
 
 int lif_backward(const void* x, const void* grad_spikes, const float* membrane_checkpoint,

@@ -373,16 +373,82 @@ __global__ __launch_bounds__(64) void lif_fwd_staged_kernel(const typename E::ra
     if (nfull + q < nblk) block(st[q], nfull + q);
 }
 
+// Forward with the residual add of the block (language.py:1326-1330,
+// residual + spike): writes out = residual + s_t in fp32 instead of the
+// spikes, from fp32 residual rows staged like x.  out may alias residual
+// (each block is written after its own residual was read).
 template <typename E>
+__global__ __launch_bounds__(64) void lif_fwd_residual_kernel(const typename E::raw* __restrict__ x,
+                                                              const float* res, float* out,
+                                                              float* __restrict__ ck, int T,
+                                                              int C, LifParams P) {
+  using S = Staged<E>;
+  using SF = Staged<F32>;
+  constexpr int PF = 3;  // blocks in flight (x and the wider residual pieces)
+  __shared__ u32x4 xs[S::kInstr * 64];
+  __shared__ u32x4 rs[SF::kInstr * 64];
+  const int n_cg = (C + 63) / 64;
+  const int b = blockIdx.x / n_cg;
+  const int cg = blockIdx.x - b * n_cg;
+  const int lane = threadIdx.x;
+  const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
+  const unsigned loff = S::lane_off(lane, C, cg);
+  const unsigned loffr = SF::lane_off(lane, C, cg);
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const rsrc_t rck = make_rsrc(ck + size_t(b) * nblk * C + size_t(cg) * 64,
+                               uint32_t(((size_t(nblk) - 1) * C + 64) * 4));
+  const unsigned ck_off = cg * 64 + lane < C ? unsigned(lane) * 4u : kOutOfRange;
+
+  float m = 0.f;
+  auto block = [&](u32x4 (&st)[S::kInstr], u32x4 (&sr)[SF::kInstr], int blk) {
+    S::to_lds(xs, st, lane);
+    SF::to_lds(rs, sr, lane);
+    S::load(st, x, row_base, row_tail, loff, blk + PF, nblk, C);
+    SF::load(sr, res, row_base, row_tail, loffr, blk + PF, nblk, C);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rck, ck_off,
+                                          unsigned(blk) * unsigned(C) * 4u, kAuxNT);
+#pragma unroll
+    for (int s = 0; s < kLifBlock; ++s) {
+      const float h = m * P.decay + S::get(xs, s, lane);
+      const float sp = P.slope * (h - P.threshold) >= 0.f ? 1.f : 0.f;
+      m = h * (1.f - sp) + P.reset * sp;
+      SF::put(rs, s, lane, SF::get(rs, s, lane) + sp);
+    }
+    SF::store(out, rs, row_base, row_tail, loffr, blk, C, lane);
+  };
+
+  u32x4 st[PF][S::kInstr], sr[PF][SF::kInstr];
+#pragma unroll
+  for (int q = 0; q < PF; ++q) {
+    S::load(st[q], x, row_base, row_tail, loff, q, nblk, C);
+    SF::load(sr[q], res, row_base, row_tail, loffr, q, nblk, C);
+  }
+  const int nfull = nblk - nblk % PF;
+  for (int base = 0; base < nfull; base += PF) {
+#pragma unroll
+    for (int q = 0; q < PF; ++q) block(st[q], sr[q], base + q);
+  }
+#pragma unroll
+  for (int q = 0; q < PF - 1; ++q)
+    if (nfull + q < nblk) block(st[q], sr[q], nfull + q);
+}
+
+// G is the type of the incoming gradient: E, or fp32 when the spikes were
+// added into an fp32 residual (lif_fwd_residual_kernel), whose gradient
+// arrives in fp32.
+template <typename E, typename G>
 __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::raw* __restrict__ x,
-                                                            const typename E::raw* __restrict__ gs,
+                                                            const typename G::raw* __restrict__ gs,
                                                             const float* __restrict__ ck,
                                                             typename E::raw* __restrict__ gx,
                                                             int T, int C, LifParams P) {
   using S = Staged<E>;
-  constexpr int PB = S::kPb;
+  using SG = Staged<G>;
+  // Blocks in flight: one fewer when the gradient pieces are wider than x's.
+  constexpr int PB = sizeof(typename G::raw) > sizeof(typename E::raw) ? S::kPb - 1 : S::kPb;
   __shared__ u32x4 xs[S::kInstr * 64];
-  __shared__ u32x4 gl[S::kInstr * 64];
+  __shared__ u32x4 gl[SG::kInstr * 64];
   __shared__ u32x4 os[S::kInstr * 64];
   const int n_cg = (C + 63) / 64;
   const int b = blockIdx.x / n_cg;
@@ -391,6 +457,7 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
   const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
   const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
   const unsigned loff = S::lane_off(lane, C, cg);
+  const unsigned loffg = SG::lane_off(lane, C, cg);
   const int nblk = (T + kLifBlock - 1) / kLifBlock;
   // Membrane records (lanes past C read as zero and never store).
   const rsrc_t rck = make_rsrc(ck + size_t(b) * nblk * C + size_t(cg) * 64,
@@ -404,12 +471,12 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
   float gm = 0.f;
   // Blocks are visited last to first; the inputs PB blocks ahead (earlier in
   // time) wait in registers.  Blocks before 0 read as zero.
-  auto block = [&](u32x4 (&sx)[S::kInstr], u32x4 (&sg)[S::kInstr], float& sm, int blk) {
+  auto block = [&](u32x4 (&sx)[S::kInstr], u32x4 (&sg)[SG::kInstr], float& sm, int blk) {
     S::to_lds(xs, sx, lane);
-    S::to_lds(gl, sg, lane);
+    SG::to_lds(gl, sg, lane);
     float m = sm;
     S::load(sx, x, row_base, row_tail, loff, blk - PB, nblk, C);
-    S::load(sg, gs, row_base, row_tail, loff, blk - PB, nblk, C);
+    SG::load(sg, gs, row_base, row_tail, loffg, blk - PB, nblk, C);
     sm = rec(blk - PB);
     // Recompute the block's pre-spike membranes h and c = slope (h - theta)
     // (the forward's operations, so the spikes are the forward's; the wave
@@ -430,20 +497,20 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
       const float cc = cs[s];
       const float sp = cc >= 0.f ? 1.f : 0.f;
       const float dsdh = lif_surrogate(cc, P.slope);
-      const float gh = S::get(gl, s, lane) * dsdh + gm * ((1.f - sp) + (P.reset - h[s]) * dsdh);
+      const float gh = SG::get(gl, s, lane) * dsdh + gm * ((1.f - sp) + (P.reset - h[s]) * dsdh);
       gm = P.decay * gh;
       S::put(os, s, lane, gh);
     }
     S::store(gx, os, row_base, row_tail, loff, blk, C, lane);
   };
 
-  u32x4 sx[PB][S::kInstr], sg[PB][S::kInstr];
+  u32x4 sx[PB][S::kInstr], sg[PB][SG::kInstr];
   float sm[PB];
 #pragma unroll
   for (int q = 0; q < PB; ++q) {
     const int blk = nblk - 1 - q;
     S::load(sx[q], x, row_base, row_tail, loff, blk, nblk, C);
-    S::load(sg[q], gs, row_base, row_tail, loff, blk, nblk, C);
+    SG::load(sg[q], gs, row_base, row_tail, loffg, blk, nblk, C);
     sm[q] = rec(blk);
   }
   const int nfull = nblk - nblk % PB;
@@ -532,13 +599,63 @@ static int lif_bwd_dispatch(const void* x, const void* gs, const float* ck, void
                             int T, int C, const wkv::LifParams& P, hipStream_t stream) {
   using raw = typename E::raw;
   if (lif_staged_ok<E>(T, C)) {
-    launch(wkv::lif_bwd_staged_kernel<E>, dim3(unsigned(B) * unsigned((C + 63) / 64)), dim3(64),
-           stream, true, static_cast<const raw*>(x), static_cast<const raw*>(gs), ck,
+    launch(wkv::lif_bwd_staged_kernel<E, E>, dim3(unsigned(B) * unsigned((C + 63) / 64)),
+           dim3(64), stream, true, static_cast<const raw*>(x), static_cast<const raw*>(gs), ck,
            static_cast<raw*>(gx), T, C, P);
     return check_launch("lif_bwd_staged_kernel");
   }
   return lif_vec(B, C, int(sizeof(typename E::raw))) == 2 ? lif_bwd_launch<E, 2>(x, gs, ck, gx, B, T, C, P, stream)
                             : lif_bwd_launch<E, 1>(x, gs, ck, gx, B, T, C, P, stream);
+}
+
+// Residual variants: staged kernels only (the caller checks lif_residual_ok).
+template <typename E>
+static int lif_residual_fwd(const void* x, const float* res, float* out, float* ck, int B, int T,
+                            int C, const wkv::LifParams& P, hipStream_t stream) {
+  launch(wkv::lif_fwd_residual_kernel<E>, dim3(unsigned(B) * unsigned((C + 63) / 64)), dim3(64),
+         stream, true, static_cast<const typename E::raw*>(x), res, out, ck, T, C, P);
+  return check_launch("lif_fwd_residual_kernel");
+}
+
+template <typename E>
+static int lif_residual_bwd(const void* x, const float* g, const float* ck, void* gx, int B,
+                            int T, int C, const wkv::LifParams& P, hipStream_t stream) {
+  using raw = typename E::raw;
+  launch(wkv::lif_bwd_staged_kernel<E, wkv::F32>, dim3(unsigned(B) * unsigned((C + 63) / 64)),
+         dim3(64), stream, true, static_cast<const raw*>(x), g, ck, static_cast<raw*>(gx), T, C,
+         P);
+  return check_launch("lif_bwd_staged_kernel");
+}
+
+bool lif_residual_ok(int64_t T, int64_t C, int dtype) {
+  const int es = dtype == 0 ? 4 : 2;
+  // x pieces and the fp32 residual pieces both whole, both spans < 2^31.
+  (void)es;
+  return C % 8 == 0 && size_t(T) * size_t(C) * 4 < (size_t(1) << 31);
+}
+
+int lif_residual_forward_impl(const void* x, const float* res, float* out, float* ck, int B,
+                              int T, int C, float decay, float threshold, float reset,
+                              float slope, int dtype, hipStream_t stream) {
+  const wkv::LifParams P{decay, threshold, reset, slope};
+  switch (dtype) {
+    case 0: return lif_residual_fwd<wkv::F32>(x, res, out, ck, B, T, C, P, stream);
+    case 1: return lif_residual_fwd<wkv::BF16>(x, res, out, ck, B, T, C, P, stream);
+    case 2: return lif_residual_fwd<wkv::F16>(x, res, out, ck, B, T, C, P, stream);
+    default: return fail(1, "lif_residual_forward: unknown dtype");
+  }
+}
+
+int lif_residual_backward_impl(const void* x, const float* g, const float* ck, void* gx, int B,
+                               int T, int C, float decay, float threshold, float reset,
+                               float slope, int dtype, hipStream_t stream) {
+  const wkv::LifParams P{decay, threshold, reset, slope};
+  switch (dtype) {
+    case 0: return lif_residual_bwd<wkv::F32>(x, g, ck, gx, B, T, C, P, stream);
+    case 1: return lif_residual_bwd<wkv::BF16>(x, g, ck, gx, B, T, C, P, stream);
+    case 2: return lif_residual_bwd<wkv::F16>(x, g, ck, gx, B, T, C, P, stream);
+    default: return fail(1, "lif_residual_backward: unknown dtype");
+  }
 }
 
 int lif_forward_impl(const void* x, void* spk, float* ck, int B, int T, int C, float decay,

@@ -128,3 +128,102 @@ def lif_sequence(
         x, 1.0 - 1.0 / tau, float(threshold), float(reset), float(surrogate_slope)
     )
     return spikes if spikes.dtype == x.dtype else spikes.to(x.dtype)
+
+
+# ------------------------------------------------------ fused residual add --
+# myelin::lif_residual_forward(Tensor x, Tensor residual, float decay,
+#     float threshold, float reset, float slope) -> (Tensor out, Tensor ck)
+# out = residual + spikes(x) in fp32: the block's `residual + lif(...)`
+# (language.py:1326-1330) with the spikes added as they are produced, so the
+# spikes tensor, the separate add and, in the backward, the cast of the fp32
+# residual gradient to x's dtype disappear.
+
+
+def _residual_ok(x: Tensor, residual: Tensor) -> bool:
+    if x.ndim != 3 or residual.shape != x.shape or residual.dtype != torch.float32:
+        return False
+    b, t, c = x.shape
+    return x.dtype in _NATIVE and c % 8 == 0 and t * c * 4 < (1 << 31)
+
+
+@torch.library.custom_op("myelin::lif_residual_forward", mutates_args=())
+def _lif_res_forward(x: Tensor, residual: Tensor, decay: float, threshold: float, reset: float,
+                     slope: float) -> tuple[Tensor, Tensor]:
+    _lib.require_gpu(x, residual)
+    if not _residual_ok(x, residual):
+        raise ValueError("lif_residual_forward: x [B, T, C] (C % 8 == 0) and an fp32 residual "
+                         f"of the same shape; got {x.shape}/{x.dtype}, {residual.shape}/"
+                         f"{residual.dtype}")
+    b, t, c = x.shape
+    xs = _native(x)
+    rs = _lib.aligned(residual)
+    out = torch.empty_like(rs)
+    ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    rc = _lib.timed("lif_residual_forward", x.device, lambda: lib.lif_residual_forward(
+        xs.data_ptr(), rs.data_ptr(), out.data_ptr(), ck.data_ptr(), b, t, c, decay, threshold,
+        reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs)))
+    _lib.check(rc, "lif_residual_forward")
+    return out, ck
+
+
+@_lif_res_forward.register_fake
+def _(x, residual, decay, threshold, reset, slope):
+    b, t, c = x.shape
+    return (torch.empty(x.shape, dtype=torch.float32, device=x.device),
+            torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=x.device))
+
+
+@torch.library.custom_op("myelin::lif_residual_backward", mutates_args=())
+def _lif_res_backward(grad_out: Tensor, x: Tensor, checkpoint: Tensor, decay: float,
+                      threshold: float, reset: float, slope: float) -> Tensor:
+    _lib.require_gpu(grad_out, x, checkpoint)
+    b, t, c = x.shape
+    xs = _native(x)
+    g = _lib.aligned(grad_out.float())
+    gx = torch.empty_like(xs)
+    lib = _lib.load()
+    rc = _lib.timed("lif_residual_backward", x.device, lambda: lib.lif_residual_backward(
+        xs.data_ptr(), g.data_ptr(), checkpoint.data_ptr(), gx.data_ptr(), b, t, c, decay,
+        threshold, reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs)))
+    _lib.check(rc, "lif_residual_backward")
+    return gx
+
+
+@_lif_res_backward.register_fake
+def _(grad_out, x, checkpoint, decay, threshold, reset, slope):
+    dt = x.dtype if x.dtype in _NATIVE else torch.float32
+    return torch.empty(x.shape, dtype=dt, device=x.device)
+
+
+def _res_setup_context(ctx, inputs, output):
+    x, _residual, decay, threshold, reset, slope = inputs
+    _, ck = output
+    ctx.save_for_backward(x, ck)
+    ctx.params = (decay, threshold, reset, slope)
+    ctx.mark_non_differentiable(ck)
+    ctx.set_materialize_grads(False)
+
+
+def _res_backward(ctx, grad_out, _grad_ck):
+    if grad_out is None:
+        return None, None, None, None, None, None
+    x, ck = ctx.saved_tensors
+    gx = torch.ops.myelin.lif_residual_backward(grad_out, x, ck, *ctx.params)
+    return gx.to(x.dtype), grad_out, None, None, None, None
+
+
+_lif_res_forward.register_autograd(_res_backward, setup_context=_res_setup_context)
+
+
+def lif_residual(residual: Tensor, x: Tensor, *, tau: float = 2.0, threshold: float = 1.0,
+                 reset: float = 0.0, surrogate_slope: float = 2.0) -> Tensor:
+    """``residual + lif_sequence(x, ...)`` (fp32), fused into the LIF kernels
+    for an fp32 residual on the GPU with C a multiple of 8; otherwise the two
+    operations."""
+    if x.is_cuda and residual.is_cuda and _residual_ok(x, residual):
+        out, _ = torch.ops.myelin.lif_residual_forward(
+            x, residual, 1.0 - 1.0 / tau, float(threshold), float(reset), float(surrogate_slope))
+        return out
+    return residual + lif_sequence(x, tau=tau, threshold=threshold, reset=reset,
+                                   surrogate_slope=surrogate_slope)

@@ -34,7 +34,7 @@ from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguage
                          SpikeTimeMixState, SpikingSequenceLIFState, StepWorkspace, block_step,
                          initial_packed, pack_state, state_from_packed)
 from .language import weighted_key_value
-from .lif import lif_sequence
+from .lif import lif_residual, lif_sequence
 from .timemix import layer_norm_shift_mix, token_shift_mix
 
 
@@ -171,6 +171,15 @@ class SpikingSequenceLIF(nn.Module):
                             surrogate_slope=self.surrogate_slope)
 
 
+def _add_lif(residual: Tensor, lif: nn.Module, x: Tensor) -> Tensor:
+    """``residual + lif(x)``; a spiking LIF writes its spikes straight into the
+    fp32 residual (``myelin::lif_residual_forward``)."""
+    if isinstance(lif, SpikingSequenceLIF):
+        return lif_residual(residual, x, tau=lif.tau, threshold=lif.threshold, reset=lif.reset,
+                            surrogate_slope=lif.surrogate_slope)
+    return residual + lif(x)
+
+
 class SpikeTimeMix(nn.Module):
     """``language.py:921-1036``: token-shift mixes, k/v/r projections, WKV,
     ``sigmoid(r) * wkv`` and the output projection."""
@@ -290,9 +299,9 @@ class SpikeGPTBlock(nn.Module):
         # half's token-shift kernel (layer_norm_shift_mix).
         residual = self.ln0(inputs) if self.ln0 is not None else inputs
         att = self.att.project(*layer_norm_shift_mix(residual, self.ln1, self.att.mixes()))
-        residual = residual + self.lif1(att)
+        residual = _add_lif(residual, self.lif1, att)
         ffn = self.ffn.project(*layer_norm_shift_mix(residual, self.ln2, self.ffn.mixes()))
-        residual = residual + self.lif2(ffn)
+        residual = _add_lif(residual, self.lif2, ffn)
         return self.dropout(residual)
 
 

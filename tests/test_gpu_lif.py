@@ -125,3 +125,42 @@ def test_benchmark_shape_full_size():
     assert 0.01 < rate < 0.9
     _check_grad(gx, L.lif_reverse(x.float(), gs.float(), forward_dtype=torch.float32),
                 torch.bfloat16, "grad_x full size")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 100, 64), (3, 257, 256), (1, 5, 8)])
+def test_residual_forward_and_backward(dtype, shape):
+    # out = residual + spikes(x) (exact), d out/d residual = identity,
+    # d out/d x = the LIF backward of an fp32 gradient.
+    from spikegpt_myelin_amd.lif import lif_residual
+
+    b, t, c = shape
+    x, _ = _inputs(b, t, c, dtype, seed=b + t + c)
+    g = torch.Generator().manual_seed(5)
+    residual = torch.randn(b, t, c, generator=g)
+    gout = torch.randn(b, t, c, generator=g)
+    xd = x.to(DEV).requires_grad_(True)
+    rd = residual.to(DEV).requires_grad_(True)
+    out = lif_residual(rd, xd)
+    assert out.dtype == torch.float32
+    spikes = L.lif_loop(x.float())
+    assert torch.equal(out.detach().cpu(), residual + spikes), f"out differs at {shape} {dtype}"
+    gx, gr = torch.autograd.grad(out, (xd, rd), gout.to(DEV))
+    assert torch.equal(gr.cpu(), gout)
+    ref = L.lif_reverse(x.float(), gout, forward_dtype=torch.float32)
+    _check_grad(gx, ref, dtype, f"residual grad_x {shape} {dtype}")
+
+
+def test_residual_full_size():
+    from spikegpt_myelin_amd.lif import lif_residual
+
+    x, _ = _inputs(64, 1024, 512, torch.bfloat16, seed=9, scale=1.0)
+    g = torch.Generator().manual_seed(6)
+    residual = torch.randn(64, 1024, 512, generator=g)
+    gout = torch.randn(64, 1024, 512, generator=g)
+    xd = x.to(DEV).requires_grad_(True)
+    out = lif_residual(residual.to(DEV), xd)
+    assert torch.equal(out.detach().cpu(), residual + L.lif_loop(x.float()))
+    (gx,) = torch.autograd.grad(out, xd, gout.to(DEV))
+    _check_grad(gx, L.lif_reverse(x.float(), gout, forward_dtype=torch.float32),
+                torch.bfloat16, "residual grad_x full size")

@@ -63,6 +63,7 @@ def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
         if oracle:
             mp.setattr(M, "weighted_key_value", _oracle_wkv)
             mp.setattr(M, "lif_sequence", _oracle_lif)
+            mp.setattr(M, "lif_residual", lambda residual, x, **kw: residual + _oracle_lif(x, **kw))
             mp.setattr(M, "token_shift_mix", _oracle_mix)
             # The block's fused layer norm + mix becomes torch's layer norm
             # (fp32, as autocast runs it) and the oracle's mix.
