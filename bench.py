@@ -181,6 +181,29 @@ def bench_wkv4(args, cfg) -> dict:
                                                   gtf.data_ptr(), ws.data_ptr(), ws.numel() * 4,
                                                   B, T, C, code, sp), "backward")
 
+    # The same work through the drop-in op path (torch.library dispatch,
+    # allocation and autograd on every call), for reference; timed first, in
+    # a process with no timing events outstanding.
+    leaves = [x.detach().requires_grad_(True) for x in (k, v, td, tf)]
+    fwd_op = torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32 else torch.ops.myelin.wkv_forward
+
+    def op_step():
+        for _ in range(layers):
+            if fwd_only:
+                with torch.no_grad():
+                    fwd_op(*leaves)
+            else:
+                torch.autograd.grad(fwd_op(*leaves), leaves, dy)
+
+    for _ in range(args.warmup):
+        op_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        op_step()
+    torch.cuda.synchronize()
+    op_step_s = (time.perf_counter() - t0) / args.steps
+
     dom_name = "fwd" if fwd_only else "bwd"
     pool = EventPool(4 * args.steps * layers, stream)
 
@@ -227,27 +250,6 @@ def bench_wkv4(args, cfg) -> dict:
     fwd_s = statistics.mean(attr["fwd"])
     bwd_s = statistics.mean(attr["bwd"]) if "bwd" in attr else float("nan")
 
-    # The same work through the drop-in op path (torch.library dispatch,
-    # allocation and autograd on every call), for reference.
-    leaves = [x.detach().requires_grad_(True) for x in (k, v, td, tf)]
-    fwd_op = torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32 else torch.ops.myelin.wkv_forward
-
-    def op_step():
-        for _ in range(layers):
-            if fwd_only:
-                with torch.no_grad():
-                    fwd_op(*leaves)
-            else:
-                torch.autograd.grad(fwd_op(*leaves), leaves, dy)
-
-    for _ in range(args.warmup):
-        op_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        op_step()
-    torch.cuda.synchronize()
-    op_step_s = (time.perf_counter() - t0) / args.steps
 
     esize = torch.finfo(dtype).bits // 8
     n_elem = B * T * C * layers
