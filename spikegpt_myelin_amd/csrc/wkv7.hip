@@ -329,12 +329,19 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
 // ------------------------------------------------------------ backward ----
 namespace w7 {
 
+// Row padding of the per-step reduction buffers: the reader's lanes walk
+// 8 steps x 8 pieces, so a step stride that is a multiple of the bank count
+// puts all 64 lanes of a read on a quarter of the banks; 4 extra floats per
+// step spread them (and keep 16-byte alignment).
+constexpr int kRedPad = 4;
+
 struct BwdSmem {
   float stage[2][7 * kKC * kN];
   // Per sub-chunk step: per-wave partial sums over the wave's 16 rows of the
-  // five key-indexed gradients (dr, dk, dw, da, db), and dv.
-  float red[kKS][4][5][kN];
-  float dvb[kKS][kN];
+  // five key-indexed gradients (dr, dk, dw, da, db) at [(wave * 5 + q) * kN
+  // + column], and dv.
+  float red[kKS][4 * 5 * kN + kRedPad];
+  float dvb[kKS][kN + kRedPad];
 };
 
 // Recompute + reverse over one sub-chunk of cnt steps starting at staged
@@ -429,7 +436,7 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) G[r][c] = fmaf(G[r][c], ww[c], cc[r] * aa[c]);
-      float* rs = &sm.red[s][L.wv][0][0];
+      float* rs = &sm.red[s][L.wv * 5 * kN];
       rs[0 * kN + col] = rows4_sum(pr[0], pr[1], pr[2], pr[3]);
       rs[1 * kN + col] = rows4_sum(pk[0], pk[1], pk[2], pk[3]);
       rs[2 * kN + col] = rows4_sum(pw[0], pw[1], pw[2], pw[3]);
@@ -512,10 +519,11 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
         for (int e = 0; e < EPP; e += 4) {
           float4 x;
           if (q < 5) {
-            x = *reinterpret_cast<const float4*>(&sm.red[s][0][q][pc * EPP + e]);
+            x = *reinterpret_cast<const float4*>(&sm.red[s][q * kN + pc * EPP + e]);
 #pragma unroll
             for (int wv = 1; wv < 4; ++wv) {
-              const float4 z = *reinterpret_cast<const float4*>(&sm.red[s][wv][q][pc * EPP + e]);
+              const float4 z = *reinterpret_cast<const float4*>(
+                  &sm.red[s][(wv * 5 + q) * kN + pc * EPP + e]);
               x.x += z.x; x.y += z.y; x.z += z.z; x.w += z.w;
             }
           } else {
