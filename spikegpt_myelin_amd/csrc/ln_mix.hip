@@ -242,26 +242,47 @@ __global__ __launch_bounds__(256) void ln_mix_bwd_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) prev[j][e] = 0.f;
   }
-  if (active) {
+  // Software pipeline: the row being computed (x, statistics, the next
+  // row's gradients) was loaded one iteration ahead.
+  float xr[J][4], gn[N][J][4];
+  float m_r = 0.f, r_r = 0.f;
+  auto load_or_zero = [&](float (&v)[J][4], const typename EG::raw* p, bool ok) {
+    if (ok) {
+      ln_load_grad<EG, J>(v, p, lane);
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[j][e] = 0.f;
+    }
+  };
+  if (active && t0 < t1) {
 #pragma unroll
     for (int n = 0; n < N; ++n) ln_load_grad<EG, J>(gcur[n], g.p[n] + (seq + t0) * C, lane);
+    ln_load_row<J>(xr, x + (seq + t0) * C, lane);
+    m_r = mean[seq + t0];
+    r_r = rstd[seq + t0];
+#pragma unroll
+    for (int n = 0; n < N; ++n) load_or_zero(gn[n], g.p[n] + (seq + t0 + 1) * C, t0 + 1 < T);
   }
   for (int t = t0; t < t1; ++t) {
     const size_t row = seq + t;
-    float xr[J][4], gn[N][J][4];
-    ln_load_row<J>(xr, x + row * C, lane);
+    const bool more = t + 1 < t1;
+    float xn[J][4], gnn[N][J][4];
+    float m_n = 0.f, r_n = 0.f;
+    if (more) {
+      ln_load_row<J>(xn, x + (row + 1) * C, lane);
+      m_n = mean[row + 1];
+      r_n = rstd[row + 1];
+    } else {
 #pragma unroll
-    for (int n = 0; n < N; ++n) {
-      if (t + 1 < T) {
-        ln_load_grad<EG, J>(gn[n], g.p[n] + (row + 1) * C, lane);
-      } else {
+      for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int j = 0; j < J; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) gn[n][j][e] = 0.f;
-      }
+        for (int e = 0; e < 4; ++e) xn[j][e] = 0.f;
     }
-    const float m = mean[row], r = rstd[row];
+#pragma unroll
+    for (int n = 0; n < N; ++n) load_or_zero(gnn[n], g.p[n] + (row + 2) * C, more && t + 2 < T);
+    const float m = m_r, r = r_r;
     float xh[J][4], a[J][4];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -294,6 +315,16 @@ __global__ __launch_bounds__(256) void ln_mix_bwd_kernel(
       for (int e = 0; e < 4; ++e) o[e] = r * (a[j][e] - m1 - xh[j][e] * m2);
       store_vec<F32, 4>(gx + row * C + 256 * j + 4 * lane, o);
     }
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xr[j][e] = xn[j][e];
+#pragma unroll
+        for (int n = 0; n < N; ++n) gn[n][j][e] = gnn[n][j][e];
+      }
+    m_r = m_n;
+    r_r = r_n;
   }
   // Column partials of the four waves, added in LDS in wave order.
 #pragma unroll 1
