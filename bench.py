@@ -317,12 +317,12 @@ def bench_decode(args) -> dict:
     states = [initial_wkv_state(B, C, dev) for _ in range(layers)]
     ys = [torch.empty_like(k) for k in ks]
     lib = _lib.load()
-    sp = torch.cuda.current_stream(dev).cuda_stream
     code = _lib.dtype_code(torch.float32)
 
     def step():
-        # One token through the 18 layers' state updates (C-ABI launches,
-        # state updated in place, outputs preallocated).
+        # One token through the 18 layers' state updates (C-ABI launches on
+        # the current stream, state updated in place, outputs preallocated).
+        sp = torch.cuda.current_stream(dev).cuda_stream
         for layer in range(layers):
             num, den, ls = states[layer]
             _lib.check(lib.wkv4_decode_step(
@@ -331,24 +331,44 @@ def bench_decode(args) -> dict:
                 ys[layer].data_ptr(), num.data_ptr(), den.data_ptr(), ls.data_ptr(), B, C, code, sp),
                 "decode")
 
-    for _ in range(args.warmup):
+    def timed(fn) -> float:
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    eager = timed(step)
+    # The same 18 launches captured once in a HIP graph and replayed per token
+    # (what a generation loop does: see spikegpt_myelin_amd.generation).
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
         step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    elapsed = timed(graph.replay)
     per_layer = elapsed / args.steps / layers
-    alg = 36 * B * C
+    alg = 36 * B * C  # k, v read (8 B); state read and written (24 B); y written (4 B)
+    achieved = alg / per_layer / 1e9
     return {
         "metric": "WKV decode state update tokens/sec, B=256 C=768 x18 layers fp32 state",
         "value": B * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "wkv4_decode_step", "B": B, "C": C, "layers": layers},
+        "config": {"workload": "wkv4_decode_step", "B": B, "C": C, "layers": layers,
+                   "launch": "18 launches per token captured in one HIP graph"},
         "us_per_layer_step": per_layer * 1e6,
-        "hbm_gbps_algorithmic": alg / per_layer / 1e9,
+        "eager_us_per_layer_step": eager / args.steps / layers * 1e6,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "wkv4_decode_kernel (per-layer graph time, dispatch gaps included)",
+                     "algorithmic_bytes_per_launch": alg},
     }
 
 

@@ -211,6 +211,8 @@ __global__ __launch_bounds__(256) void block_step_wkv_kernel(
 // ------------------------------------------------------------ launchers ----
 namespace wkv_host {
 
+int decode_vec(int64_t n, int64_t C);
+
 template <int PRE, int N, int EPT>
 static int row_launch(const wkv::StepRowArgs& a, hipStream_t s) {
   launch(wkv::block_step_row_kernel<PRE, N, EPT>, dim3(unsigned(a.batch)), dim3(wkv::kStepThreads),
@@ -254,7 +256,7 @@ int block_step_wkv_impl(const float* k, const float* v, const float* r, const fl
                         const float* ls_in, float* num_out, float* den_out, float* ls_out,
                         float* out, int64_t B, int64_t C, hipStream_t s) {
   const int64_t n = B * C;
-  bool vec4 = C % 4 == 0;
+  bool vec4 = decode_vec(n, C) == 4;
   for (const void* p : {static_cast<const void*>(k), static_cast<const void*>(v),
                         static_cast<const void*>(r), static_cast<const void*>(num_in),
                         static_cast<const void*>(den_in), static_cast<const void*>(ls_in),
