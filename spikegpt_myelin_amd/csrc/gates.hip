@@ -50,24 +50,6 @@ __device__ __forceinline__ u32x4 pack16(const float (&f)[Vec16<E>::N]) {
   return u32x4{o.u[0], o.u[1], o.u[2], o.u[3]};
 }
 
-// Rounds x to the element type and back (the value a 16-bit tensor holds).
-template <typename E>
-__device__ __forceinline__ float round_to(float x) {
-  if constexpr (__is_same(E, F32)) {
-    return x;
-  } else if constexpr (__is_same(E, BF16)) {
-    return bf16_bits_to_float(float_to_bf16_bits(x));
-  } else {
-    return f16_bits_to_float(float_to_f16_bits(x));
-  }
-}
-
-__device__ __forceinline__ float sigmoidf_(float r) {
-  // The expression torch's sigmoid kernel evaluates in fp32 (accurate expf,
-  // IEEE division), so the rounded gate values agree with the eager path.
-  return 1.f / (1.f + expf(-r));
-}
-
 // Elements [i*N, i*N + N) per thread; n is a multiple of N (checked on the
 // host), so no tail.
 template <typename E>
@@ -112,7 +94,7 @@ __global__ __launch_bounds__(256) void sigmoid_gate_fwd_kernel(const u32x4* __re
   unpack16<E>(__builtin_nontemporal_load(r + i), fr);
   unpack16<E>(__builtin_nontemporal_load(x + i), fx);
 #pragma unroll
-  for (int j = 0; j < N; ++j) fr[j] = round_to<E>(sigmoidf_(fr[j])) * fx[j];
+  for (int j = 0; j < N; ++j) fr[j] = round_to<E>(sigmoid_ref(fr[j])) * fx[j];
   __builtin_nontemporal_store(pack16<E>(fr), y + i);
 }
 
@@ -131,7 +113,7 @@ __global__ __launch_bounds__(256) void sigmoid_gate_bwd_kernel(const u32x4* __re
   unpack16<E>(__builtin_nontemporal_load(g + i), fg);
 #pragma unroll
   for (int j = 0; j < N; ++j) {
-    const float s = sigmoidf_(fr[j]);
+    const float s = sigmoid_ref(fr[j]);
     const float a = fg[j] * s;
     fr[j] = a * fx[j] * (1.f - s);
     fx[j] = a;

@@ -89,6 +89,22 @@ __device__ __forceinline__ uint16_t float_to_f16_bits(float x) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+// Rounds x to the element type and back (the value a 16-bit tensor holds).
+template <typename E>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (__is_same(E, F32)) {
+    return x;
+  } else if constexpr (__is_same(E, BF16)) {
+    return bf16_bits_to_float(float_to_bf16_bits(x));
+  } else {
+    return f16_bits_to_float(float_to_f16_bits(x));
+  }
+}
+
+// sigmoid(r) as torch's fp32 kernel evaluates it (accurate expf, IEEE
+// division), so values rounded from it agree with the eager path.
+__device__ __forceinline__ float sigmoid_ref(float r) { return 1.f / (1.f + expf(-r)); }
+
 // Vector of VEC consecutive channels as loaded by one lane in one
 // instruction: raw bits held in 32-bit words.
 template <typename E, int VEC> struct Pack;
