@@ -16,10 +16,13 @@
 //   dw_t   = colsum(G o S_{t-1})             da_t = S_{t-1}^T c
 //   G     <- G diag(w_t) + c a_t^T           (dL/dS_{t-1}; after step 0, dL/dS_0)
 //
-// Layout.  One 256-thread workgroup (4 waves) owns one (batch, head).  Lane
-// (rg, cg) of wave wv (rg = lane / 16 is the 16-lane DPP row, cg = lane % 16)
-// holds the 4x4 block of the state at rows 16 wv + 4 rg .. +3 and columns
-// 4 cg .. +3 in registers.  Sums over j (S a, S r, G k, G b) are in-thread
+// Forward layout.  The rows of a (batch, head) are split over kSplit = 4
+// workgroups of 256 threads; lane (rg, cg) of wave wv (rg = lane / 16 is the
+// 16-lane DPP row, cg = lane % 16) holds one row, columns 4 cg .. +3.
+//
+// Backward layout.  One 256-thread workgroup (4 waves) owns one (batch,
+// head): lane (rg, cg) of wave wv holds the 4x4 block of the state (and of
+// its gradient) at rows 16 wv + 4 rg .. +3 and columns 4 cg .. +3.  Sums over j (S a, S r, G k, G b) are in-thread
 // over 4 columns, then a DPP butterfly across the 16 lanes of a DPP row (no
 // LDS).  Sums over i (the key-indexed gradients) are in-thread over 4 rows,
 // then two gfx950 permlane swaps across the 4 DPP rows of the wave, then LDS
@@ -45,12 +48,19 @@ namespace wkv {
 namespace w7 {
 
 constexpr int kN = 64;          // head size
-constexpr int kThreads = 256;   // threads per (batch, head)
+constexpr int kThreads = 256;   // threads per workgroup
 constexpr int kKC = 16;         // steps per staged block
 constexpr int kKS = 8;          // steps per checkpoint / backward sub-chunk (registers)
 constexpr int kNSub = kKC / kKS;
 
 __device__ __forceinline__ float as_f(unsigned u) { return __uint_as_float(u); }
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt and lgkmcnt fields at their
+// maximum).  Placed after a conditional load of the loop-carried state, so
+// the compiler's wait analysis sees nothing pending at the loop header;
+// otherwise it keeps a vmcnt(0) inside the loop, which then waits for the
+// next block's prefetch every block.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 __device__ __forceinline__ unsigned as_u(float f) { return __float_as_uint(f); }
 
 template <int CTRL>
@@ -90,7 +100,13 @@ __device__ __forceinline__ float rows4_sum(float v0, float v1, float v2, float v
 template <typename E, int NV>
 struct Vecs {
   const typename E::raw* p[NV];
+  // q must be the same in every lane of the wave: it is moved to a scalar
+  // register, so the choice is a scalar select.  A per-lane index would make
+  // the compiler fetch the pointer from the argument block with a vector
+  // load, and the wait for that load would also wait for every store the
+  // wave still has in flight.
   __device__ __forceinline__ const typename E::raw* pick(int q) const {
+    q = __builtin_amdgcn_readfirstlane(q);
     const typename E::raw* r = p[0];
 #pragma unroll
     for (int i = 1; i < NV; ++i) r = (q == i) ? p[i] : r;
@@ -108,6 +124,7 @@ struct Stager {
   static constexpr int PPV = kN / EPP;               // pieces per step vector
   static constexpr int NP = NV * kKC * PPV;
   static constexpr int PPT = (NP + kThreads - 1) / kThreads;
+  static_assert((kKC * PPV) % 64 == 0, "a wave's pieces come from one step vector");
   uint4 buf[PPT];
 
   __device__ __forceinline__ void load(const Vecs<E, NV>& src, int bi, int h, int t0, int T,
@@ -229,101 +246,250 @@ __device__ __forceinline__ void store_state(float* dst, const float (&S)[4][4], 
         make_float4(S[r][0], S[r][1], S[r][2], S[r][3]);
 }
 
-// Writes rows [n][64] of fp32 LDS data to out[(bi, t0 + s, h, :)] in the
-// element type, 16 bytes per thread-iteration.
+// ---- forward layout: the 64 rows of a (batch, head) split over kSplit
+// workgroups.  Rows are independent in the forward, so a workgroup owns
+// kRows of them and needs only its own kRows entries of v and y.  Lane
+// (wave wv, DPP row rg, cg) holds one row, 4 columns:
+//   row = kRows * split + 4 wv + rg,   columns 4 cg .. +3.
+// The per-row sums are the same in-thread 4-column sum and 16-lane DPP
+// butterfly as the backward's recomputation (fwd_step), so both produce the
+// same state bits.  Four times the waves of a 4x4-block layout: at
+// B = 16, H = 12 that is 768 workgroups, three waves on every SIMD.
+constexpr int kSplit = 4;
+constexpr int kRows = kN / kSplit;   // 16 rows per workgroup: 4 waves x 4 DPP rows
+static_assert(kRows == 4 * (kThreads / 64), "one row per DPP row of each wave");
+
+// Staged block: the key-side vectors r, w, k, a, b as fp32 [5][kKC][64],
+// then the workgroup's slice of v as [kKC][kRows].
+enum { KR = 0, KW = 1, KK = 2, KA = 3, KB = 4 };
+constexpr int kRowStage = 5 * kKC * kN + kKC * kRows;
+
 template <typename E>
-__device__ __forceinline__ void store_steps(typename E::raw* out, const float* buf, int bi, int h,
-                                            int t0, int n, int T, int H) {
-  constexpr int EPP = 16 / int(sizeof(typename E::raw));
-  constexpr int PPV = kN / EPP;
-  for (int p = int(threadIdx.x); p < n * PPV; p += kThreads) {
-    const int s = p / PPV;
-    const int pc = p - s * PPV;
-    const float* src = buf + s * kN + pc * EPP;
-    float f[EPP];
+struct RowStager {
+  using raw = typename E::raw;
+  static constexpr int EPP = 16 / int(sizeof(raw));  // elements per 16-byte piece
+  static constexpr int PPV = kN / EPP;               // pieces per key-side vector
+  static constexpr int PPR = kRows / EPP;            // pieces of v per step
+  static constexpr int NK = 5 * kKC * PPV;
+  static constexpr int NP = NK + kKC * PPR;
+  static constexpr int PPT = (NP + kThreads - 1) / kThreads;
+  static_assert((kKC * PPV) % 64 == 0, "a wave's pieces come from one step vector");
+  uint4 buf[PPT];
+
+  // Vecs order is (r, w, k, v, a, b): key-side vector q is input q, or q + 1 past v.
+  __device__ __forceinline__ void load(const Vecs<E, 6>& src, int bi, int h, int i0, int t0,
+                                       int T, int H) {
 #pragma unroll
-    for (int e = 0; e < EPP; e += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(src + e);
-      f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
-    }
-    typename E::raw* dst = out + ((size_t(bi) * T + t0 + s) * H + h) * kN + pc * EPP;
-    if constexpr (EPP == 4) {
-      *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
-    } else {
-      OutPack<E, 8> o;
-      o.set(f);
-      *reinterpret_cast<uint4*>(dst) = make_uint4(o.u[0], o.u[1], o.u[2], o.u[3]);
+    for (int k = 0; k < PPT; ++k) {
+      const int p = int(threadIdx.x) + k * kThreads;
+      if (p < NK) {
+        const int q = p / (kKC * PPV);
+        const int rem = p - q * (kKC * PPV);
+        const int s = rem / PPV;
+        const int pc = rem - s * PPV;
+        const int t = min(t0 + s, T - 1);
+        const raw* base = src.pick(q < 3 ? q : q + 1) + ((size_t(bi) * T + t) * H + h) * kN +
+                          pc * EPP;
+        buf[k] = *reinterpret_cast<const uint4*>(base);
+      } else if (p < NP) {
+        const int s = (p - NK) / PPR;
+        const int pc = (p - NK) - s * PPR;
+        const int t = min(t0 + s, T - 1);
+        const raw* base = src.p[3] + ((size_t(bi) * T + t) * H + h) * kN + i0 + pc * EPP;
+        buf[k] = *reinterpret_cast<const uint4*>(base);
+      }
     }
   }
+
+  __device__ __forceinline__ void store(float* lds) const {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      const int p = int(threadIdx.x) + k * kThreads;
+      float* dst;
+      if (p < NK) {
+        const int q = p / (kKC * PPV);
+        const int rem = p - q * (kKC * PPV);
+        const int s = rem / PPV;
+        const int pc = rem - s * PPV;
+        dst = lds + (q * kKC + s) * kN + pc * EPP;
+      } else if (p < NP) {
+        const int s = (p - NK) / PPR;
+        const int pc = (p - NK) - s * PPR;
+        dst = lds + 5 * kKC * kN + s * kRows + pc * EPP;
+      } else {
+        continue;
+      }
+      const uint32_t w[4] = {buf[k].x, buf[k].y, buf[k].z, buf[k].w};
+      if constexpr (EPP == 4) {
+        *reinterpret_cast<float4*>(dst) =
+            make_float4(as_f(w[0]), as_f(w[1]), as_f(w[2]), as_f(w[3]));
+      } else {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (__is_same(E, BF16)) {
+            f[2 * e] = __uint_as_float(w[e] << 16);
+            f[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+          } else {
+            f[2 * e] = f16_bits_to_float(w[e] & 0xffffu);
+            f[2 * e + 1] = f16_bits_to_float(w[e] >> 16);
+          }
+        }
+        *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+      }
+    }
+  }
+};
+
+// One staged block of a workgroup's rows over n steps.  FULL (n == kKC)
+// drops the per-step guards, so the whole block is one basic block and the
+// LDS reads of later steps are free to overlap earlier steps' arithmetic.
+// CK: copy the state at each kKS-step record start to rec (stored by the
+// caller after the block: no global store is in flight while the block's
+// arithmetic waits on LDS, and the wait for the next block's staging loads
+// finds only old stores ahead of it).
+template <bool FULL, bool CK>
+__device__ __forceinline__ void fwd_rows_block(float (&S)[4], const float* sg, float* yb, int n,
+                                               float (&rec)[kNSub][4], int lr, int j0) {
+#pragma unroll
+  for (int s = 0; s < kKC; ++s) {
+    if (FULL || s < n) {
+      if (CK && s % kKS == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rec[s / kKS][c] = S[c];
+      }
+      const float4 a4 = lds4(sg, KA, s, j0);
+      const float4 w4 = lds4(sg, KW, s, j0);
+      const float4 b4 = lds4(sg, KB, s, j0);
+      const float4 k4 = lds4(sg, KK, s, j0);
+      const float v = sg[5 * kKC * kN + s * kRows + lr];
+      const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+      const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+      const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+      const float k[4] = {k4.x, k4.y, k4.z, k4.w};
+      float x = S[0] * a[0];
+#pragma unroll
+      for (int c = 1; c < 4; ++c) x = fmaf(S[c], a[c], x);
+      const float sa = row16_sum(x);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S[c] = fmaf(S[c], w[c], fmaf(sa, b[c], v * k[c]));
+      const float4 r4 = lds4(sg, KR, s, j0);
+      const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
+      float yv = S[0] * rr[0];
+#pragma unroll
+      for (int c = 1; c < 4; ++c) yv = fmaf(S[c], rr[c], yv);
+      // The 16 lanes of the DPP row hold the same sum and store it to the
+      // same word (no exec-mask branch inside the block).
+      yb[s * kRows + lr] = row16_sum(yv);
+    }
+  }
+}
+
+// Workgroup -> ((batch, head), split).  Consecutive workgroups go to
+// different XCDs (round robin over 8); when the grid is a multiple of 8 the
+// mapping puts the kSplit workgroups of one (batch, head), which read the
+// same key-side vectors, on the same XCD and so the same L2.
+__device__ __forceinline__ int xcd_local_block() {
+  const int g = int(blockIdx.x);
+  const int G = int(gridDim.x);
+  return (G & 7) ? g : (g & 7) * (G >> 3) + (g >> 3);
 }
 
 }  // namespace w7
 
 // ------------------------------------------------------------- forward ----
-// One workgroup per (batch, head).  ck (optional): state at the start of
-// every kKS-step sub-chunk, [B*H][ceil(T/kKS)][64][64].  y may be null
-// (records only).
-template <typename E>
+// kSplit workgroups per (batch, head), kRows state rows each.  ck (optional):
+// state at the start of every kKS-step sub-chunk, [B*H][ceil(T/kKS)][64][64]
+// (each workgroup writes its rows).  y may be null (records only).
+template <typename E, bool CK>
 __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
     w7::Vecs<E, 6> in, const float* __restrict__ s0, typename E::raw* __restrict__ y,
     float* __restrict__ s_out, float* __restrict__ ck, int T, int H) {
   using namespace w7;
-  __shared__ float stage[2][6 * kKC * kN];
-  __shared__ float ybuf[2][kKC * kN];
-  const int bh = blockIdx.x;
+  __shared__ float stage[2][kRowStage];
+  __shared__ float ybuf[2][kKC * kRows];
+  const int g = xcd_local_block();
+  const int bh = g / kSplit;
+  const int i0 = (g - bh * kSplit) * kRows;
   const int bi = bh / H;
   const int h = bh - bi * H;
-  const Lane L;
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int lane = int(threadIdx.x) & 63;
+  const int cg = lane & 15;
+  const int lr = 4 * wv + (lane >> 4);   // row within the workgroup's slice
+  const int row = i0 + lr;
+  const int j0 = 4 * cg;
 
-  float S[4][4];
+  float S[4];
   if (s0) {
-    load_state(S, s0 + state_off(bh, 0, 0), L);
+    const float4 x = *reinterpret_cast<const float4*>(s0 + state_off(bh, row, j0));
+    S[0] = x.x; S[1] = x.y; S[2] = x.z; S[3] = x.w;
   } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) S[r][c] = 0.f;
+    for (int c = 0; c < 4; ++c) S[c] = 0.f;
   }
+  wait_vmem_all();
   const int nblk = (T + kKC - 1) / kKC;
   const int nrec = (T + kKS - 1) / kKS;
-  Stager<E, 6> st;
+  RowStager<E> st;
   if (nblk > 0) {
-    st.load(in, bi, h, 0, T, H);
+    st.load(in, bi, h, i0, 0, T, H);
     st.store(stage[0]);
     __syncthreads();
   }
   for (int blk = 0; blk < nblk; ++blk) {
     const int t0 = blk * kKC;
     const int n = min(kKC, T - t0);
-    if (blk + 1 < nblk) st.load(in, bi, h, t0 + kKC, T, H);
+    if (blk + 1 < nblk) st.load(in, bi, h, i0, t0 + kKC, T, H);
     const float* sg = stage[blk & 1];
     float* yb = ybuf[blk & 1];
-#pragma unroll
-    for (int s = 0; s < kKC; ++s) {
-      if (s < n) {
-        if (ck && s % kKS == 0)
-          store_state(ck + (size_t(bh) * nrec + blk * kNSub + s / kKS) * kN * kN, S, L);
-        float sa[4];
-        fwd_step(S, sg, s, L, sa);
-        const float4 r4 = lds4(sg, QR, s, L.j0);
-        const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
-        float yr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = S[r][0] * rr[0];
-#pragma unroll
-          for (int c = 1; c < 4; ++c) x = fmaf(S[r][c], rr[c], x);
-          yr[r] = row16_sum(x);
-        }
-        if (L.cg == 0)
-          *reinterpret_cast<float4*>(yb + s * kN + L.i0) = make_float4(yr[0], yr[1], yr[2], yr[3]);
-      }
+    float rec[kNSub][4];
+    if (n == kKC) {
+      fwd_rows_block<true, CK>(S, sg, yb, n, rec, lr, j0);
+    } else {
+      fwd_rows_block<false, CK>(S, sg, yb, n, rec, lr, j0);
     }
     if (blk + 1 < nblk) st.store(stage[(blk + 1) & 1]);
+    if (CK) {
+      float* ckr = ck + (size_t(bh) * nrec + blk * kNSub) * kN * kN + row * kN + j0;
+#pragma unroll
+      for (int m = 0; m < kNSub; ++m)
+        if (m * kKS < n)
+          *reinterpret_cast<float4*>(ckr + m * kN * kN) =
+              make_float4(rec[m][0], rec[m][1], rec[m][2], rec[m][3]);
+    }
     __syncthreads();
-    if (y) store_steps<E>(y, yb, bi, h, t0, n, T, H);
+    if (y) {
+      // kRows outputs per step: PPR 16-byte pieces at (bi, t0 + s, h, i0 ..),
+      // one piece per thread.
+      constexpr int EPP = RowStager<E>::EPP;
+      constexpr int PPR = RowStager<E>::PPR;
+      static_assert(kKC * PPR <= kThreads, "one y piece per thread");
+      const int p = int(threadIdx.x);
+      if (p < n * PPR) {
+        const int s = p / PPR;
+        const int pc = p - s * PPR;
+        const float* src = yb + s * kRows + pc * EPP;
+        float f[EPP];
+#pragma unroll
+        for (int e = 0; e < EPP; e += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(src + e);
+          f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
+        }
+        typename E::raw* dst = y + ((size_t(bi) * T + t0 + s) * H + h) * kN + i0 + pc * EPP;
+        if constexpr (EPP == 4) {
+          *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+        } else {
+          OutPack<E, 8> o;
+          o.set(f);
+          *reinterpret_cast<uint4*>(dst) = make_uint4(o.u[0], o.u[1], o.u[2], o.u[3]);
+        }
+      }
+    }
   }
-  if (s_out) store_state(s_out + state_off(bh, 0, 0), S, L);
+  if (s_out)
+    *reinterpret_cast<float4*>(s_out + state_off(bh, row, j0)) = make_float4(S[0], S[1], S[2], S[3]);
 }
 
 // ------------------------------------------------------------ backward ----
@@ -481,6 +647,7 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c) G[r][c] = 0.f;
   }
+  wait_vmem_all();
   const int nblk = (T + kKC - 1) / kKC;
   const int nrec = (T + kKS - 1) / kKS;
   Stager<E, 7> st;
@@ -567,8 +734,14 @@ static int launch_wkv7_fwd(const void* r, const void* w, const void* k, const vo
   wkv::w7::Vecs<E, 6> in{{static_cast<const raw*>(r), static_cast<const raw*>(w),
                           static_cast<const raw*>(k), static_cast<const raw*>(v),
                           static_cast<const raw*>(a), static_cast<const raw*>(b)}};
-  launch(wkv::wkv7_fwd_kernel<E>, dim3(unsigned(B) * H), dim3(wkv::w7::kThreads),
-                     stream, true, in, s0, static_cast<raw*>(y), s_out, ck, T, H);
+  const dim3 grid(unsigned(B) * H * wkv::w7::kSplit);
+  if (ck) {
+    launch(wkv::wkv7_fwd_kernel<E, true>, grid, dim3(wkv::w7::kThreads), stream, true, in, s0,
+           static_cast<raw*>(y), s_out, ck, T, H);
+  } else {
+    launch(wkv::wkv7_fwd_kernel<E, false>, grid, dim3(wkv::w7::kThreads), stream, true, in, s0,
+           static_cast<raw*>(y), s_out, ck, T, H);
+  }
   return check_launch("wkv7_fwd_kernel");
 }
 
