@@ -511,16 +511,19 @@ struct BwdSmem {
 };
 
 // Recompute + reverse over one sub-chunk of cnt steps starting at staged
-// step sl, from the sub-chunk's state record ckb (FULL: cnt == kKS, no
+// step sl, from the sub-chunk's state record S0 (FULL: cnt == kKS, no
 // per-step guards).  Leaves the per-step partial sums in sm.red / sm.dvb and
 // advances G to before the sub-chunk.
 template <bool FULL>
-__device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const float* ckb,
+__device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const float (&S0)[4][4],
                                              int sl, int cnt, const Lane& L, float (&G)[4][4]) {
   constexpr int KS = kKS;
   const int col = L.j0 + L.rg;  // column this lane holds after rows4_sum
   float S[4][4];
-  load_state(S, ckb, L);
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) S[r][c] = S0[r][c];
   // Recompute the sub-chunk keeping S_{t-1} and sa_t.
   float Sp[KS][4][4], sas[KS][4];
 #pragma unroll
@@ -618,6 +621,73 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
   }
 }
 
+// The six gradients of one sub-chunk (dr, dk, dw, da, db from the four
+// waves' partial sums in sm.red, dv from sm.dvb), packed to the element
+// type in registers by collect() and written by flush(), which the caller
+// issues after its next wait on a load.
+template <typename E>
+struct GradStores {
+  using raw = typename E::raw;
+  static constexpr int EPP = 16 / int(sizeof(raw));
+  static constexpr int PPV = kN / EPP;
+  static constexpr int NS = (6 * kKS * PPV + kThreads - 1) / kThreads;
+  uint4 data[NS];
+  raw* dst[NS];
+
+  __device__ __forceinline__ GradStores() {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) dst[k] = nullptr;
+  }
+
+  __device__ __forceinline__ void collect(const BwdSmem& sm, raw* dr, raw* dk, raw* dw, raw* da,
+                                          raw* db, raw* dv, int bi, int h, int t, int cnt, int T,
+                                          int H) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int p = int(threadIdx.x) + k * kThreads;
+      dst[k] = nullptr;
+      if (p < 6 * cnt * PPV) {
+        const int q = p / (cnt * PPV);
+        const int rem = p - q * (cnt * PPV);
+        const int s = rem / PPV;
+        const int pc = rem - s * PPV;
+        float f[EPP];
+#pragma unroll
+        for (int e = 0; e < EPP; e += 4) {
+          float4 x;
+          if (q < 5) {
+            x = *reinterpret_cast<const float4*>(&sm.red[s][q * kN + pc * EPP + e]);
+#pragma unroll
+            for (int wv = 1; wv < 4; ++wv) {
+              const float4 z = *reinterpret_cast<const float4*>(
+                  &sm.red[s][(wv * 5 + q) * kN + pc * EPP + e]);
+              x.x += z.x; x.y += z.y; x.z += z.z; x.w += z.w;
+            }
+          } else {
+            x = *reinterpret_cast<const float4*>(&sm.dvb[s][pc * EPP + e]);
+          }
+          f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
+        }
+        raw* o = q == 0 ? dr : q == 1 ? dk : q == 2 ? dw : q == 3 ? da : q == 4 ? db : dv;
+        dst[k] = o + ((size_t(bi) * T + t + s) * H + h) * kN + pc * EPP;
+        if constexpr (EPP == 4) {
+          data[k] = make_uint4(as_u(f[0]), as_u(f[1]), as_u(f[2]), as_u(f[3]));
+        } else {
+          OutPack<E, 8> o8;
+          o8.set(f);
+          data[k] = make_uint4(o8.u[0], o8.u[1], o8.u[2], o8.u[3]);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void flush() {
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (dst[k]) *reinterpret_cast<uint4*>(dst[k]) = data[k];
+  }
+};
+
 }  // namespace w7
 
 // One workgroup per (batch, head); blocks of kKC steps last to first, each
@@ -650,71 +720,54 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
   wait_vmem_all();
   const int nblk = (T + kKC - 1) / kKC;
   const int nrec = (T + kKS - 1) / kKS;
+  const float* ckh = ck + size_t(bh) * nrec * kN * kN;
   Stager<E, 7> st;
+  // Sub-chunks run last to first as one loop.  Loads and stores are ordered
+  // so that no fresh store is in flight when a load is waited for (the
+  // vector-memory counter counts both, so such a wait would also wait for
+  // the store): the record of the next sub-chunk is fetched one sub-chunk
+  // ahead, a block's staging loads are issued after its first record has
+  // arrived, and each sub-chunk's gradients are held in registers and
+  // stored after the next record has arrived.
+  float Sn[4][4];
   if (nblk > 0) {
     st.load(in, bi, h, (nblk - 1) * kKC, T, H);
+    load_state(Sn, ckh + size_t(nrec - 1) * kN * kN, L);
     st.store(sm.stage[(nblk - 1) & 1]);
     __syncthreads();
   }
-  for (int blk = nblk - 1; blk >= 0; --blk) {
+  GradStores<E> out;
+  for (int sc = nrec - 1; sc >= 0; --sc) {
+    const int blk = sc / kNSub;
+    const int m = sc - blk * kNSub;
     const int t0 = blk * kKC;
     const int n = min(kKC, T - t0);
-    if (blk > 0) st.load(in, bi, h, t0 - kKC, T, H);
+    const int sl = m * kKS;
+    const int cnt = min(kKS, n - sl);
+    float S0[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) S0[r][c] = Sn[r][c];
+    if (sc > 0) load_state(Sn, ckh + size_t(sc - 1) * kN * kN, L);
+    out.flush();
+    // First sub-chunk of this block to run: fetch the previous block.
+    if (blk > 0 && (m == kNSub - 1 || sc == nrec - 1)) st.load(in, bi, h, t0 - kKC, T, H);
     const float* sg = sm.stage[blk & 1];
-#pragma unroll 1
-    for (int m = kNSub - 1; m >= 0; --m) {
-      const int sl = m * kKS;
-      if (sl >= n) continue;
-      const int cnt = min(kKS, n - sl);
-      const float* ckb = ck + (size_t(bh) * nrec + blk * kNSub + m) * kN * kN;
-      if (cnt == kKS) {
-        bwd_subchunk<true>(sm, sg, ckb, sl, cnt, L, G);
-      } else {
-        bwd_subchunk<false>(sm, sg, ckb, sl, cnt, L, G);
-      }
-      __syncthreads();
-      // Sum the four waves' partials and store the sub-chunk's gradients.
-      constexpr int EPP = 16 / int(sizeof(typename E::raw));
-      constexpr int PPV = kN / EPP;
-      for (int p = int(threadIdx.x); p < 6 * cnt * PPV; p += kThreads) {
-        const int q = p / (cnt * PPV);
-        const int rem = p - q * (cnt * PPV);
-        const int s = rem / PPV;
-        const int pc = rem - s * PPV;
-        float f[EPP];
-#pragma unroll
-        for (int e = 0; e < EPP; e += 4) {
-          float4 x;
-          if (q < 5) {
-            x = *reinterpret_cast<const float4*>(&sm.red[s][q * kN + pc * EPP + e]);
-#pragma unroll
-            for (int wv = 1; wv < 4; ++wv) {
-              const float4 z = *reinterpret_cast<const float4*>(
-                  &sm.red[s][(wv * 5 + q) * kN + pc * EPP + e]);
-              x.x += z.x; x.y += z.y; x.z += z.z; x.w += z.w;
-            }
-          } else {
-            x = *reinterpret_cast<const float4*>(&sm.dvb[s][pc * EPP + e]);
-          }
-          f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
-        }
-        typename E::raw* o = q == 0 ? dr : q == 1 ? dk : q == 2 ? dw : q == 3 ? da : q == 4 ? db : dv;
-        typename E::raw* dst = o + ((size_t(bi) * T + t0 + sl + s) * H + h) * kN + pc * EPP;
-        if constexpr (EPP == 4) {
-          *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
-        } else {
-          OutPack<E, 8> o8;
-          o8.set(f);
-          *reinterpret_cast<uint4*>(dst) = make_uint4(o8.u[0], o8.u[1], o8.u[2], o8.u[3]);
-        }
-      }
-      __syncthreads();
+    if (cnt == kKS) {
+      bwd_subchunk<true>(sm, sg, S0, sl, cnt, L, G);
+    } else {
+      bwd_subchunk<false>(sm, sg, S0, sl, cnt, L, G);
     }
-    if (blk > 0) {
+    __syncthreads();
+    out.collect(sm, dr, dk, dw, da, db, dv, bi, h, t0 + sl, cnt, T, H);
+    __syncthreads();
+    if (m == 0 && blk > 0) {
       st.store(sm.stage[(blk - 1) & 1]);
       __syncthreads();
     }
   }
+  out.flush();
   if (ds0) store_state(ds0 + state_off(bh, 0, 0), G, L);
 }
 
