@@ -81,6 +81,26 @@ def test_autograd_matches_oracle(dtype, t):
         _close(got[6], ref[8], dtype, "ds0")
 
 
+@pytest.mark.parametrize("b,h", [(1, 1), (1, 3), (3, 5)])
+def test_batch_head_counts(b, h):
+    # The forward runs four workgroups per (batch, head); with an odd B*H the
+    # grid is not a multiple of 8 and the workgroups map to heads in plain
+    # order instead of grouped by XCD.  T = 19: one full 16-step block and a
+    # partial one holding part of a second checkpoint record.
+    ops = _ops()
+    dtype = torch.bfloat16
+    xs, s0, gy, gs = _case(b, 19, h, seed=20 + b * h, dtype=dtype, with_state=True)
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    sd = s0.to(DEV).requires_grad_(True)
+    y, s = ops.wkv7_forward(*leaves, sd)
+    got = torch.autograd.grad([y, s], leaves + [sd], [gy.to(DEV), gs.to(DEV)])
+    ref = _reference(xs, s0, gy, gs)
+    _close(y, ref[0], dtype, "y")
+    _close(s, ref[1], dtype, "s")
+    for name, g, e in zip((*NAMES, "ds0"), got, ref[2:]):
+        _close(g, e, dtype, name)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_standalone_backward_matches_autograd_path(dtype):
     ops = _ops()
