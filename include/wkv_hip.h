@@ -234,6 +234,14 @@ int relu_square_forward(const void* x, void* y, int64_t n, int dtype, void* stre
 int relu_square_backward(const void* x, const void* grad_y, void* grad_x, int64_t n, int dtype,
                          void* stream);
 
+/* Sum of S fp32 partials: out[n] = sum_{s<S} partial[s][n], added in the
+ * order s = 0, 1, ..., S-1.  partial [S][N], out [N]; N a multiple of 4.
+ * The split-K weight gradients of the model's projections (each a sum of
+ * GEMMs over slices of the B*T rows) end with it; the weight gradient of
+ * the reference's nn.Linear projections (language.py:952-955, 1155-1157) is
+ * one GEMM over all rows. */
+int split_k_sum(const float* partial, float* out, int64_t S, int64_t N, void* stream);
+
 /* Receptance gate y = sigmoid(r) * x (language.py:1035 sigmoid(r) * wkv and
  * :1194 sigmoid(r) * value): sigmoid rounded to `dtype`, then the product
  * rounded, as the two eager 16-bit kernels do.  n as relu_square_forward. */
@@ -279,13 +287,17 @@ size_t layer_norm_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int
 
 /* Backward: grad0..grad{n-1} [B,T,C] in g_dtype; writes grad_x fp32 [B,T,C]
  * and grad_params fp32 [n + 2][C] = (grad_mix_0 .. grad_mix_{n-1},
- * grad_weight, grad_bias), each summed over all rows in a fixed order. */
+ * grad_weight, grad_bias), each summed over all rows in a fixed order.
+ * grad_x_add (optional, NULL for none): fp32 [B,T,C] added to grad_x, the
+ * gradient x receives through its other use (a block's residual stream,
+ * language.py:1326-1330), so no separate add is needed. */
 int layer_norm_shift_mix_backward(const float* x, const float* weight, const float* bias,
                                   const float* mix, int64_t n, const float* mean,
                                   const float* rstd, const void* grad0, const void* grad1,
                                   const void* grad2, int g_dtype, float* grad_x,
-                                  float* grad_params, void* workspace, size_t workspace_bytes,
-                                  int64_t B, int64_t T, int64_t C, void* stream);
+                                  const float* grad_x_add, float* grad_params, void* workspace,
+                                  size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                                  void* stream);
 
 /* ---- One-token block step (generation) ------------------------------------
  *

@@ -105,6 +105,7 @@ SIGNATURES = {
         _INT,
         [_P, _INT, _P, _I64, _P, _P, _P, _INT, _P, _P, _P, _SZ, _I64, _I64, _I64, _P],
     ),
+    "split_k_sum": (_INT, [_P, _P, _I64, _I64, _P]),
     "relu_square_forward": (_INT, [_P, _P, _I64, _INT, _P]),
     "relu_square_backward": (_INT, [_P, _P, _P, _I64, _INT, _P]),
     "sigmoid_gate_forward": (_INT, [_P, _P, _P, _I64, _INT, _P]),
@@ -113,8 +114,8 @@ SIGNATURES = {
         _INT, [_P, _P, _P, _F, _P, _I64, _P, _P, _P, _INT, _P, _P, _I64, _I64, _I64, _P]),
     "layer_norm_shift_mix_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "layer_norm_shift_mix_backward": (
-        _INT, [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _SZ, _I64, _I64, _I64,
-               _P]),
+        _INT, [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _P, _SZ, _I64, _I64,
+               _I64, _P]),
     "block_step_row": (_INT, [_INT, ctypes.POINTER(StepRowArgs), _P]),
     "block_step_wkv": (_INT, [_P] * 12 + [_I64, _I64, _P]),
     "wkv_time_next_call": (_INT, [_P, _P]),

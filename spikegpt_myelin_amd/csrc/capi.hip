@@ -115,9 +115,10 @@ int block_step_row_impl(int, const wkv_step_row_args&, hipStream_t);
 int ln_mix_forward_impl(const float*, const float*, const float*, const float*, int, void* const*,
                         int, float*, float*, int, int, int, float, hipStream_t);
 int ln_mix_backward_impl(const float*, const float*, const float*, const float*, int,
-                         const float*, const float*, const void* const*, int, float*, float*,
-                         float*, int, int, int, hipStream_t);
+                         const float*, const float*, const void* const*, int, float*,
+                         const float*, float*, float*, int, int, int, hipStream_t);
 int64_t ln_mix_workgroups(int64_t, int64_t);
+int split_k_sum_impl(const float*, float*, int64_t, int64_t, hipStream_t);
 int block_step_wkv_impl(const float*, const float*, const float*, const float*, const float*,
                         const float*, const float*, const float*, float*, float*, float*, float*,
                         int64_t, int64_t, hipStream_t);
@@ -578,6 +579,19 @@ int relu_square_forward(const void* x, void* y, int64_t n, int dtype, void* stre
   return relu_square_forward_impl(x, y, n, dtype, static_cast<hipStream_t>(stream));
 }
 
+int split_k_sum(const float* partial, float* out, int64_t S, int64_t N, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (S <= 0 || N < 0 || S > (int64_t(1) << 20) || N > (int64_t(1) << 40))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "split_k_sum: bad sizes");
+  if (N == 0) return WKV_OK;
+  if (!partial || !out) return fail(WKV_ERR_INVALID_ARGUMENT, "split_k_sum: null pointer");
+  if (N % 4 != 0 || !aligned16({partial, out}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "split_k_sum: N must be a multiple of 4 and the tensors 16-byte aligned");
+  return split_k_sum_impl(partial, out, S, N, static_cast<hipStream_t>(stream));
+}
+
 int relu_square_backward(const void* x, const void* grad_y, void* grad_x, int64_t n, int dtype,
                          void* stream) {
   set_error("");
@@ -670,8 +684,9 @@ int layer_norm_shift_mix_backward(const float* x, const float* weight, const flo
                                   const float* mix, int64_t n, const float* mean,
                                   const float* rstd, const void* grad0, const void* grad1,
                                   const void* grad2, int g_dtype, float* grad_x,
-                                  float* grad_params, void* workspace, size_t workspace_bytes,
-                                  int64_t B, int64_t T, int64_t C, void* stream) {
+                                  const float* grad_x_add, float* grad_params, void* workspace,
+                                  size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                                  void* stream) {
   set_error("");
   TimingScope timing;
   if (!dtype_ok(g_dtype))
@@ -687,13 +702,13 @@ int layer_norm_shift_mix_backward(const float* x, const float* weight, const flo
     if (!g[j] || !aligned16({g[j]}))
       return fail(WKV_ERR_INVALID_ARGUMENT,
                   "layer_norm_shift_mix_backward: null or unaligned gradient");
-  if (!aligned16({x, weight, bias, mix, grad_x, workspace}))
+  if (!aligned16({x, weight, bias, mix, grad_x, grad_x_add, workspace}))
     return fail(WKV_ERR_INVALID_ARGUMENT,
                 "layer_norm_shift_mix_backward: tensors must be 16-byte aligned");
   if (workspace_bytes < layer_norm_shift_mix_workspace_bytes(n, B, T, C))
     return fail(WKV_ERR_WORKSPACE_TOO_SMALL, "layer_norm_shift_mix_backward: workspace too small");
   return ln_mix_backward_impl(x, weight, bias, mix, int(n), mean, rstd, g, g_dtype, grad_x,
-                              static_cast<float*>(workspace), grad_params, int(B), int(T),
+                              grad_x_add, static_cast<float*>(workspace), grad_params, int(B), int(T),
                               int(C), static_cast<hipStream_t>(stream));
 }
 

@@ -191,14 +191,16 @@ __global__ __launch_bounds__(256) void ln_mix_fwd_kernel(const float* __restrict
   }
 }
 
-// g_j: [B,T,C] (EG); gx: [B,T,C] fp32; partial: [N + 2][P][C] fp32 with
-// P = number of workgroups (rows: gmu_0..gmu_{N-1}, gw, gbias).
+// g_j: [B,T,C] (EG); gx: [B,T,C] fp32; gadd (optional): [B,T,C] fp32 added
+// to gx (the gradient x receives through its other use, the residual
+// stream); partial: [N + 2][P][C] fp32 with P = number of workgroups (rows:
+// gmu_0..gmu_{N-1}, gw, gbias).
 template <typename EG, int N, int J>
 __global__ __launch_bounds__(256) void ln_mix_bwd_kernel(
     const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ mix, const float* __restrict__ mean,
     const float* __restrict__ rstd, LnPtrs<const typename EG::raw> g, float* __restrict__ gx,
-    float* __restrict__ partial, int B, int T) {
+    const float* __restrict__ gadd, float* __restrict__ partial, int B, int T) {
   constexpr int C = 256 * J;
   constexpr int F = N + 2;  // column-sum fields
   __shared__ float acc_lds[F * C];
@@ -282,6 +284,9 @@ __global__ __launch_bounds__(256) void ln_mix_bwd_kernel(
     }
 #pragma unroll
     for (int n = 0; n < N; ++n) load_or_zero(gnn[n], g.p[n] + (row + 2) * C, more && t + 2 < T);
+    // The added gradient of this row, used only at the store.
+    float ga[J][4];
+    if (gadd) ln_load_row<J>(ga, gadd + row * C, lane);
     const float m = m_r, r = r_r;
     float xh[J][4], a[J][4];
     float s1 = 0.f, s2 = 0.f;
@@ -313,6 +318,10 @@ __global__ __launch_bounds__(256) void ln_mix_bwd_kernel(
       float o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = r * (a[j][e] - m1 - xh[j][e] * m2);
+      if (gadd) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] += ga[j][e];
+      }
       store_vec<F32, 4>(gx + row * C + 256 * j + 4 * lane, o);
     }
 #pragma unroll
@@ -410,12 +419,13 @@ int ln_mix_forward_impl(const float* x, const float* w, const float* bias, const
 template <typename EG, int N, int J>
 static int ln_bwd_launch(const float* x, const float* w, const float* bias, const float* mix,
                          const float* mean, const float* rstd, const void* const* g, float* gx,
-                         float* partial, float* sums, int B, int T, hipStream_t s) {
+                         const float* gadd, float* partial, float* sums, int B, int T,
+                         hipStream_t s) {
   wkv::LnPtrs<const typename EG::raw> gp{};
   for (int n = 0; n < N; ++n) gp.p[n] = static_cast<const typename EG::raw*>(g[n]);
   const int64_t P = ln_mix_workgroups(B, T);
   launch(wkv::ln_mix_bwd_kernel<EG, N, J>, dim3(unsigned(P)), dim3(256), s, false, x, w, bias,
-         mix, mean, rstd, gp, gx, partial, B, T);
+         mix, mean, rstd, gp, gx, gadd, partial, B, T);
   int rc = check_launch("ln_mix_bwd_kernel");
   if (rc) return rc;
   launch(wkv::column_sum_kernel<16>, dim3(unsigned(J * 4), unsigned(N + 2)), dim3(1024), s, true,
@@ -426,10 +436,12 @@ static int ln_bwd_launch(const float* x, const float* w, const float* bias, cons
 template <typename EG, int N>
 static int ln_bwd_j(int J, const float* x, const float* w, const float* bias, const float* mix,
                     const float* mean, const float* rstd, const void* const* g, float* gx,
-                    float* partial, float* sums, int B, int T, hipStream_t s) {
+                    const float* gadd, float* partial, float* sums, int B, int T, hipStream_t s) {
   switch (J) {
-    case 1: return ln_bwd_launch<EG, N, 1>(x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
-    case 2: return ln_bwd_launch<EG, N, 2>(x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
+    case 1:
+      return ln_bwd_launch<EG, N, 1>(x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
+    case 2:
+      return ln_bwd_launch<EG, N, 2>(x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
     default: return fail(1, "layer_norm_shift_mix_backward: C must be 256 or 512");
   }
 }
@@ -437,23 +449,27 @@ static int ln_bwd_j(int J, const float* x, const float* w, const float* bias, co
 template <typename EG>
 static int ln_bwd_n(int n, int J, const float* x, const float* w, const float* bias,
                     const float* mix, const float* mean, const float* rstd, const void* const* g,
-                    float* gx, float* partial, float* sums, int B, int T, hipStream_t s) {
+                    float* gx, const float* gadd, float* partial, float* sums, int B, int T,
+                    hipStream_t s) {
   switch (n) {
-    case 2: return ln_bwd_j<EG, 2>(J, x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
-    case 3: return ln_bwd_j<EG, 3>(J, x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
+    case 2: return ln_bwd_j<EG, 2>(J, x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
+    case 3: return ln_bwd_j<EG, 3>(J, x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
     default: return fail(1, "layer_norm_shift_mix_backward: 2 or 3 mixing vectors");
   }
 }
 
 int ln_mix_backward_impl(const float* x, const float* w, const float* bias, const float* mix,
                          int n, const float* mean, const float* rstd, const void* const* g,
-                         int g_dtype, float* gx, float* partial, float* sums, int B, int T, int C,
-                         hipStream_t s) {
+                         int g_dtype, float* gx, const float* gadd, float* partial, float* sums,
+                         int B, int T, int C, hipStream_t s) {
   const int J = C / 256;
   switch (g_dtype) {
-    case 0: return ln_bwd_n<wkv::F32>(n, J, x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
-    case 1: return ln_bwd_n<wkv::BF16>(n, J, x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
-    case 2: return ln_bwd_n<wkv::F16>(n, J, x, w, bias, mix, mean, rstd, g, gx, partial, sums, B, T, s);
+    case 0:
+      return ln_bwd_n<wkv::F32>(n, J, x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
+    case 1:
+      return ln_bwd_n<wkv::BF16>(n, J, x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
+    case 2:
+      return ln_bwd_n<wkv::F16>(n, J, x, w, bias, mix, mean, rstd, g, gx, gadd, partial, sums, B, T, s);
     default: return fail(1, "layer_norm_shift_mix_backward: unknown gradient dtype");
   }
 }

@@ -35,7 +35,8 @@ from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguage
                          initial_packed, pack_state, state_from_packed)
 from .language import weighted_key_value
 from .lif import lif_residual, lif_sequence
-from .timemix import layer_norm_shift_mix, token_shift_mix
+from .splitk import split_k_sum
+from .timemix import layer_norm_shift_mix, layer_norm_shift_mix_fork, token_shift_mix
 
 
 @dataclass
@@ -98,7 +99,8 @@ class _HeavisideAtan(torch.autograd.Function):
 
 class _SplitKLinearFn(torch.autograd.Function):
     """``x @ weight.T`` whose weight gradient sums S independent GEMMs over
-    slices of the B*T rows (fp32 outputs, then an fp32 sum).  With
+    slices of the B*T rows (fp32 outputs, then the fixed-order fp32 sum of
+    :func:`split_k_sum`).  With
     B*T = 65536 rows and a 512x512 weight, the one-GEMM weight gradient has
     only a few dozen output tiles for 256 CUs; S slices give S times as many.
     Forward and input gradient are the ordinary GEMMs; the computation dtype
@@ -127,8 +129,8 @@ class _SplitKLinearFn(torch.autograd.Function):
             x3 = xc.reshape(s, rows // s, xc.shape[-1])
             # [S, out, in] = g3^T @ x3: the transposed view is the left
             # operand; the right one is contiguous.
-            gw = torch.bmm(g3.transpose(1, 2), x3, out_dtype=torch.float32).sum(0)
-        return gx, gw.to(ctx.weight_dtype), None
+            parts = torch.bmm(g3.transpose(1, 2), x3, out_dtype=torch.float32)
+        return gx, split_k_sum(parts).to(ctx.weight_dtype), None
 
 
 class SplitKLinear(nn.Linear):
@@ -296,12 +298,14 @@ class SpikeGPTBlock(nn.Module):
 
     def forward(self, inputs: Tensor) -> Tensor:
         # att(ln1(x)) and ffn(ln2(x)) with each layer norm folded into the
-        # half's token-shift kernel (layer_norm_shift_mix).
+        # half's token-shift kernel; the residual stream is taken back from
+        # that op (layer_norm_shift_mix_fork), so its two gradients are summed
+        # inside the fused backward kernel.
         residual = self.ln0(inputs) if self.ln0 is not None else inputs
-        att = self.att.project(*layer_norm_shift_mix(residual, self.ln1, self.att.mixes()))
-        residual = _add_lif(residual, self.lif1, att)
-        ffn = self.ffn.project(*layer_norm_shift_mix(residual, self.ln2, self.ffn.mixes()))
-        residual = _add_lif(residual, self.lif2, ffn)
+        *mixed, residual = layer_norm_shift_mix_fork(residual, self.ln1, self.att.mixes())
+        residual = _add_lif(residual, self.lif1, self.att.project(*mixed))
+        *mixed, residual = layer_norm_shift_mix_fork(residual, self.ln2, self.ffn.mixes())
+        residual = _add_lif(residual, self.lif2, self.ffn.project(*mixed))
         return self.dropout(residual)
 
 

@@ -22,6 +22,8 @@ dtype, as the projections would cast their inputs.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 from torch import Tensor
 
@@ -163,10 +165,17 @@ def _(x, weight, bias, mix, eps, out_dtype):
 
 @torch.library.custom_op("myelin::layer_norm_shift_mix_backward", mutates_args=())
 def _ln_shift_mix_backward(grads: list[Tensor], x: Tensor, weight: Tensor, bias: Tensor,
-                           mix: Tensor, mean: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
-    """Returns ``grad_x`` [B, T, C] fp32 and ``[n + 2, C]`` fp32 parameter
-    gradients (the n mixing vectors, the weight, the bias)."""
+                           mix: Tensor, mean: Tensor, rstd: Tensor,
+                           grad_x_add: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
+    """Returns ``grad_x`` [B, T, C] fp32 (plus ``grad_x_add`` when given) and
+    ``[n + 2, C]`` fp32 parameter gradients (the n mixing vectors, the
+    weight, the bias)."""
     _lib.require_gpu(x, weight, bias, mix, mean, rstd, *grads)
+    if grad_x_add is not None:
+        _lib.require_gpu(grad_x_add)
+        if grad_x_add.shape != x.shape:
+            raise ValueError("layer_norm_shift_mix_backward: grad_x_add must have the shape of x")
+        gadd = _lib.aligned(grad_x_add.float().contiguous())
     b, t, c = x.shape
     n = mix.shape[0]
     gdt = grads[0].dtype if grads[0].dtype in _NATIVE else torch.float32
@@ -183,14 +192,15 @@ def _ln_shift_mix_backward(grads: list[Tensor], x: Tensor, weight: Tensor, bias:
                     lambda: lib.layer_norm_shift_mix_backward(
                         xs.data_ptr(), w.data_ptr(), bb.data_ptr(), mx.data_ptr(), n,
                         mean.data_ptr(), rstd.data_ptr(), *ptrs, _lib.dtype_code(gdt),
-                        gx.data_ptr(), gp.data_ptr(), ws.data_ptr(), ws.numel(), b, t, c,
+                        gx.data_ptr(), None if grad_x_add is None else gadd.data_ptr(),
+                        gp.data_ptr(), ws.data_ptr(), ws.numel(), b, t, c,
                         _lib.stream_of(xs)))
     _lib.check(rc, "layer_norm_shift_mix_backward")
     return gx, gp
 
 
 @_ln_shift_mix_backward.register_fake
-def _(grads, x, weight, bias, mix, mean, rstd):
+def _(grads, x, weight, bias, mix, mean, rstd, grad_x_add=None):
     return (torch.empty(x.shape, dtype=torch.float32, device=x.device),
             x.new_empty((mix.shape[0] + 2, x.shape[2]), dtype=torch.float32))
 
@@ -215,21 +225,63 @@ def _ln_backward(ctx, grads):
 _ln_shift_mix.register_autograd(_ln_backward, setup_context=_ln_setup_context)
 
 
+class _LnShiftMixFork(torch.autograd.Function):
+    """``myelin::layer_norm_shift_mix`` that also hands back its input ``x``
+    (the residual stream, ``language.py:1326-1356``).  The gradient that
+    reaches ``x`` through that second use arrives here and is added to
+    ``grad_x`` inside the backward kernel, in place of autograd's separate
+    fp32 add of the two gradients (same values: one fp32 add either way)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, mix, eps, out_dtype):  # noqa: D102
+        outs = torch.ops.myelin.layer_norm_shift_mix(x, weight, bias, mix, eps, out_dtype)
+        ctx.save_for_backward(x, weight, bias, mix, outs[-2], outs[-1])
+        return (*outs[:-2], x)
+
+    @staticmethod
+    def backward(ctx, *grads):  # noqa: D102
+        x, weight, bias, mix, mean, rstd = ctx.saved_tensors
+        n = mix.shape[0]
+        gouts = [torch.zeros(x.shape, dtype=torch.float32, device=x.device) if g is None else g
+                 for g in grads[:n]]
+        gx, gp = torch.ops.myelin.layer_norm_shift_mix_backward(gouts, x, weight, bias, mix,
+                                                               mean, rstd, grads[n])
+        return (gx, gp[n].to(weight.dtype), gp[n + 1].to(bias.dtype), gp[:n].to(mix.dtype),
+                None, None)
+
+
+def _ln_fusable(x: Tensor, norm: torch.nn.LayerNorm, mix: Tensor) -> bool:
+    c = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.float32 and x.ndim == 3 and c in LN_MIX_CHANNELS
+            and mix.ndim == 2 and 2 <= mix.shape[0] <= 3 and norm.weight is not None
+            and norm.bias is not None and tuple(norm.normalized_shape) == (c,))
+
+
+def _ln_out_dtype() -> torch.dtype:
+    if torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return torch.float32
+
+
 def layer_norm_shift_mix(x: Tensor, norm: torch.nn.LayerNorm, mix: Tensor) -> list[Tensor]:
     """``token_shift_mix(norm(x), mix)`` (values of the eager layer norm and
     mixes, in the autocast dtype when CUDA autocast is on), fused into one
     kernel pair when ``x`` is fp32 on the GPU with C in (256, 512) and 2-3
     mixing vectors; otherwise the layer norm and :func:`token_shift_mix`."""
-    c = x.shape[-1]
-    fusable = (x.is_cuda and x.dtype == torch.float32 and x.ndim == 3 and c in LN_MIX_CHANNELS
-               and mix.ndim == 2 and 2 <= mix.shape[0] <= 3 and norm.weight is not None
-               and norm.bias is not None and tuple(norm.normalized_shape) == (c,))
-    if not fusable:
+    if not _ln_fusable(x, norm, mix):
         return token_shift_mix(norm(x), mix)
-    if torch.is_autocast_enabled("cuda"):
-        out_dtype = torch.get_autocast_dtype("cuda")
-    else:
-        out_dtype = torch.float32
     outs = torch.ops.myelin.layer_norm_shift_mix(x, norm.weight, norm.bias, mix, float(norm.eps),
-                                                out_dtype)
+                                                _ln_out_dtype())
     return list(outs[:-2])
+
+
+def layer_norm_shift_mix_fork(x: Tensor, norm: torch.nn.LayerNorm, mix: Tensor) -> list[Tensor]:
+    """:func:`layer_norm_shift_mix` followed by ``x`` itself, for a block half
+    whose residual stream ``x`` is also added to the half's output: use the
+    returned ``x`` for that add, and the gradient it receives joins
+    ``grad_x`` inside the fused backward kernel (same values as autograd's
+    own sum of the two gradients)."""
+    if not _ln_fusable(x, norm, mix):
+        return [*token_shift_mix(norm(x), mix), x]
+    return list(_LnShiftMixFork.apply(x, norm.weight, norm.bias, mix, float(norm.eps),
+                                      _ln_out_dtype()))

@@ -108,3 +108,45 @@ def test_full_size_matches_unfused_kernels():
         scale = w_.abs().max().item()
         err = (g - w_).abs().max().item() / scale
         assert err < 1e-4, f"grad {name}: {err:.2e}"
+
+
+@pytest.mark.parametrize("B,T,C,n", [(2, 70, 256, 3), (3, 33, 512, 2)])
+@pytest.mark.parametrize("residual_grad", [True, False])
+def test_fork_adds_the_residual_gradient(B, T, C, n, residual_grad):
+    # layer_norm_shift_mix_fork returns x again; the gradient of that second
+    # use is added inside the backward kernel.  It must equal the plain op
+    # with autograd summing the two gradients of x (one fp32 add either way).
+    from spikegpt_myelin_amd.timemix import layer_norm_shift_mix_fork
+
+    x, w, b, mix = _inputs(B, T, C, n, seed=40 + T)
+    gen = torch.Generator().manual_seed(41)
+    grads = [torch.randn(B, T, C, generator=gen).to(torch.bfloat16).to(DEV) for _ in range(n)]
+    g_res = torch.randn(B, T, C, generator=gen).to(DEV)
+    print(f"ln_mix fork B={B} T={T} C={C} n={n} residual_grad={residual_grad}", flush=True)
+
+    def norm_module():
+        m = torch.nn.LayerNorm(C).to(DEV)
+        with torch.no_grad():
+            m.weight.copy_(w)
+            m.bias.copy_(b)
+        return m
+
+    n1, n2 = norm_module(), norm_module()
+    x1, x2 = (x.to(DEV).requires_grad_() for _ in range(2))
+    m1, m2 = (mix.to(DEV).requires_grad_() for _ in range(2))
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        *outs1, xr = layer_norm_shift_mix_fork(x1, n1, m1)
+        outs2 = layer_norm_shift_mix(x2, n2, m2)
+    assert xr.data_ptr() == x1.data_ptr() and xr.requires_grad
+    if residual_grad:
+        torch.autograd.backward([*outs1, xr], [*grads, g_res])
+        torch.autograd.backward([*outs2, x2], [*grads, g_res])
+    else:
+        torch.autograd.backward(outs1, grads)
+        torch.autograd.backward(outs2, grads)
+    for a, c in zip(outs1, outs2):
+        assert torch.equal(a, c)
+    assert torch.equal(x1.grad, x2.grad)
+    assert torch.equal(m1.grad, m2.grad)
+    assert torch.equal(n1.weight.grad, n2.weight.grad)
+    assert torch.equal(n1.bias.grad, n2.bias.grad)

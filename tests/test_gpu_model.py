@@ -70,6 +70,9 @@ def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
             mp.setattr(M, "layer_norm_shift_mix", lambda x, norm, mix: _oracle_mix(
                 torch.nn.functional.layer_norm(x.float(), norm.normalized_shape, norm.weight,
                                                norm.bias, norm.eps), mix))
+            mp.setattr(M, "layer_norm_shift_mix_fork", lambda x, norm, mix: [*_oracle_mix(
+                torch.nn.functional.layer_norm(x.float(), norm.normalized_shape, norm.weight,
+                                               norm.bias, norm.eps), mix), x])
             mp.setattr(M, "relu_square", lambda x: torch.relu(x).square())
             mp.setattr(M, "sigmoid_gate", lambda r, x: torch.sigmoid(r) * x)
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
