@@ -150,3 +150,18 @@ def test_fork_adds_the_residual_gradient(B, T, C, n, residual_grad):
     assert torch.equal(m1.grad, m2.grad)
     assert torch.equal(n1.weight.grad, n2.weight.grad)
     assert torch.equal(n1.bias.grad, n2.bias.grad)
+
+
+def test_backward_op_opcheck_with_added_gradient():
+    x, w, b, mix = (t.to(DEV) for t in _inputs(2, 9, 256, 2, seed=3))
+    outs = torch.ops.myelin.layer_norm_shift_mix(x, w, b, mix, 1e-5, torch.bfloat16)
+    grads = [torch.randn_like(o, dtype=torch.float32).to(torch.bfloat16) for o in outs[:2]]
+    gadd = torch.randn_like(x)
+    args = (grads, x, w, b, mix, outs[2], outs[3])
+    torch.library.opcheck(torch.ops.myelin.layer_norm_shift_mix_backward, args,
+                          {"grad_x_add": gadd})
+    torch.library.opcheck(torch.ops.myelin.layer_norm_shift_mix_backward, args)
+    gx_add, gp_add = torch.ops.myelin.layer_norm_shift_mix_backward(*args, grad_x_add=gadd)
+    gx, gp = torch.ops.myelin.layer_norm_shift_mix_backward(*args)
+    assert torch.equal(gx_add, gx + gadd)
+    assert torch.equal(gp_add, gp)

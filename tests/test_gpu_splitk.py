@@ -55,3 +55,9 @@ def test_split_k_linear_weight_gradient():
     scale = want.abs().max().item()
     err = (lin.weight.grad - want).abs().max().item() / scale
     assert err < 1e-5, f"weight grad rel err {err:.2e}"
+
+
+def test_opcheck():
+    # Schema, fake (meta) implementation and dispatch registration.
+    partial = torch.randn(4, 16, 8, device=DEV)
+    torch.library.opcheck(torch.ops.myelin.split_k_sum, (partial,))
