@@ -100,6 +100,29 @@ int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
                                size_t workspace_bytes, int64_t B, int64_t T, int64_t C, int dtype,
                                void* stream);
 
+/* The time mix's receptance gate folded into the WKV kernels
+ * (language.py:1028-1035: sigmoid(r) * wkv): y = sigmoid(r) * wkv(k, v)
+ * with the roundings of the separate ops (wkv and sigmoid(r) each rounded to
+ * the element type, then the product), so y equals wkv4_forward followed by
+ * sigmoid_gate_forward bit for bit.  r [B,T,C] in dtype; y required;
+ * checkpoint optional (NULL: none), as wkv4_forward_checkpointed. */
+int wkv4_forward_gated_checkpointed(const void* k, const void* v, const float* time_decay,
+                                    const float* time_first, const void* r, void* y,
+                                    float* checkpoint, int64_t B, int64_t T, int64_t C, int dtype,
+                                    void* stream);
+
+/* Backward of wkv4_forward_gated_checkpointed from its records: grad_y is
+ * the gradient of the gated output; writes grad_k, grad_v, grad_r (dtype)
+ * and the parameter gradients, equal to sigmoid_gate_backward followed by
+ * wkv4_backward_checkpointed.  Workspace as wkv4_backward_checkpointed. */
+int wkv4_backward_gated_checkpointed(const void* grad_y, const float* time_decay,
+                                     const float* time_first, const void* k, const void* v,
+                                     const void* r, const float* checkpoint, void* grad_k,
+                                     void* grad_v, void* grad_r, float* grad_time_decay,
+                                     float* grad_time_first, void* workspace,
+                                     size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                                     int dtype, void* stream);
+
 /* Single-token WKV decode step for generation.
  *
  * Replaces the eager WKV arithmetic of SpikeTimeMix.step

@@ -28,6 +28,7 @@ from .gates import relu_square, sigmoid_gate
 from .lif import lif_sequence
 from .timemix import token_shift_mix
 from .wkv import (
+    weighted_key_value_gated,
     weighted_key_value_hip,
     weighted_key_value_hip_bf16io,
     weighted_key_value_triton,
@@ -43,6 +44,7 @@ __all__ = [
     "token_shift_mix",
     "validate_wkv_inputs",
     "weighted_key_value",
+    "weighted_key_value_gated",
     "weighted_key_value_hip",
     "weighted_key_value_hip_bf16io",
     "weighted_key_value_triton",

@@ -63,6 +63,10 @@ SIGNATURES = {
     "wkv4_checkpoint_bytes": (_SZ, [_I64, _I64, _I64]),
     "wkv4_forward_checkpointed": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_checkpointed_workspace_bytes": (_SZ, [_I64, _I64]),
+    "wkv4_forward_gated_checkpointed": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT,
+                                                _P]),
+    "wkv4_backward_gated_checkpointed": (
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_checkpointed": (
         _INT,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P],

@@ -77,6 +77,11 @@ int wkv4_backward_impl(const void*, const float*, const float*, const void*, con
 int wkv4_backward_ck_impl(const void*, const float*, int, const float*, const void*, const void*,
                           const float*, void*, void*, float*, float*, float*, int, int, int, int,
                           hipStream_t);
+int wkv4_forward_gated_impl(const void*, const void*, const float*, const float*, const void*,
+                            void*, float*, int, int, int, int, hipStream_t);
+int wkv4_backward_gated_ck_impl(const void*, const float*, const float*, const void*, const void*,
+                                const void*, const float*, void*, void*, void*, float*, float*,
+                                float*, int, int, int, int, hipStream_t);
 size_t wkv4_bwd_workspace_bytes_impl(int64_t, int64_t, int64_t, int);
 size_t wkv4_checkpoint_floats(int64_t, int64_t, int64_t);
 size_t wkv4_partials_floats(int64_t, int64_t);
@@ -252,6 +257,59 @@ int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
   return wkv4_backward_ck_impl(grad_y, time_decay, 0, time_first, k, v, checkpoint, grad_k,
                                grad_v, grad_time_decay, grad_time_first,
                                static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
+}
+
+int wkv4_forward_gated_checkpointed(const void* k, const void* v, const float* time_decay,
+                                    const float* time_first, const void* r, void* y,
+                                    float* checkpoint, int64_t B, int64_t T, int64_t C, int dtype,
+                                    void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_gated_checkpointed: unknown dtype");
+  if (!dims_ok(B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_gated_checkpointed: bad sizes");
+  if (B == 0 || T == 0 || C == 0) return WKV_OK;
+  if (!k || !v || !time_decay || !time_first || !r || !y)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_gated_checkpointed: null pointer");
+  if (!aligned16({k, v, r, y, checkpoint}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv4_forward_gated_checkpointed: tensors must be 16-byte aligned");
+  return wkv4_forward_gated_impl(k, v, time_decay, time_first, r, y, checkpoint, int(B), int(T),
+                                 int(C), dtype, static_cast<hipStream_t>(stream));
+}
+
+int wkv4_backward_gated_checkpointed(const void* grad_y, const float* time_decay,
+                                     const float* time_first, const void* k, const void* v,
+                                     const void* r, const float* checkpoint, void* grad_k,
+                                     void* grad_v, void* grad_r, float* grad_time_decay,
+                                     float* grad_time_first, void* workspace,
+                                     size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
+                                     int dtype, void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_gated_checkpointed: unknown dtype");
+  if (!dims_ok(B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_gated_checkpointed: bad sizes");
+  if (C == 0) return WKV_OK;
+  if (!grad_time_decay || !grad_time_first)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_gated_checkpointed: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0 || T == 0) return wkv4_zero_param_grads(grad_time_decay, grad_time_first, int(C), s);
+  if (!grad_y || !time_decay || !time_first || !k || !v || !r || !checkpoint || !grad_k ||
+      !grad_v || !grad_r || !workspace)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_gated_checkpointed: null pointer");
+  if (workspace_bytes < wkv4_partials_floats(B, C) * sizeof(float))
+    return fail(WKV_ERR_WORKSPACE_TOO_SMALL,
+                "wkv4_backward_gated_checkpointed: workspace too small");
+  if (!aligned16({grad_y, k, v, r, checkpoint, grad_k, grad_v, grad_r, workspace}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv4_backward_gated_checkpointed: tensors must be 16-byte aligned");
+  return wkv4_backward_gated_ck_impl(grad_y, time_decay, time_first, k, v, r, checkpoint, grad_k,
+                                     grad_v, grad_r, grad_time_decay, grad_time_first,
+                                     static_cast<float*>(workspace), int(B), int(T), int(C),
+                                     dtype, s);
 }
 
 int wkv4_decode_step(const void* k, const void* v, const float* time_decay, const float* time_first,

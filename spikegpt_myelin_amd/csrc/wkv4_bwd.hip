@@ -56,12 +56,16 @@ namespace wkv {
 // and output exponent are kept, and the stabilised reverse recurrence
 // (wkv_triton.py:120-142, extended by the G', H' sums for gw) runs over it.
 // Quadratic within a block; only rows outside the shared-frame range take it.
+// r, gr (both null, or both given): the forward was sigmoid(r) * wkv; gy is
+// the gradient of that product and grad_r is written to gr.
 template <typename E, int L>
 __device__ void wkv4_bwd_channel_serial(const typename E::raw* __restrict__ gy,
                                         const typename E::raw* __restrict__ k,
                                         const typename E::raw* __restrict__ v,
+                                        const typename E::raw* __restrict__ r,
                                         typename E::raw* __restrict__ gk,
-                                        typename E::raw* __restrict__ gv, float w2, float u2,
+                                        typename E::raw* __restrict__ gv,
+                                        typename E::raw* __restrict__ gr, float w2, float u2,
                                         int T, int C, size_t base, const float* __restrict__ ck,
                                         size_t ck_lane, size_t ck_field, float& gw_out,
                                         float& gu_out) {
@@ -122,7 +126,13 @@ __device__ void wkv4_bwd_channel_serial(const typename E::raw* __restrict__ gy,
           const size_t idx = base + size_t(t) * C;
           const float kk = load_scalar<E>(k + idx) * kLog2e;
           const float vv = load_scalar<E>(v + idx);
-          const float g = load_scalar<E>(gy + idx);
+          float g = load_scalar<E>(gy + idx);
+          if (r != nullptr) {
+            const float sg = sigmoid_ref(load_scalar<E>(r + idx));
+            const float a = g * sg;
+            store_scalar<E>(gr + idx, a * round_to<E>(ys[i]) * (1.f - sg));
+            g = round_to<E>(a);
+          }
           const float zr = g * rs[i];
           const float ze = zr * fast_exp2(u2 + kk - nfs[i]);
           const float bk = fast_exp2(kk + orr);
@@ -148,7 +158,7 @@ __device__ void wkv4_bwd_channel_serial(const typename E::raw* __restrict__ gy,
   gu_out = gu;
 }
 
-template <typename E, int VEC, int L, int W>
+template <typename E, int VEC, int L, int W, bool GATE = false>
 struct Bwd {
   using raw = typename E::raw;
   using PackT = Pack<E, VEC>;
@@ -178,13 +188,15 @@ struct Bwd {
   // Loads the wave's chunk (L steps from t0) of segment seg through buffer
   // descriptors based at the chunk (row_base, ck_row wave-uniform; lane_boff,
   // ck_boff the lane's byte offsets); steps at or past T read as zero.
+  // GATE: also the receptance chunk rb (g is then the gradient of the gated
+  // output).
   __device__ static __forceinline__ void load(const raw* __restrict__ k, const raw* __restrict__ v,
-                                              const raw* __restrict__ g,
+                                              const raw* __restrict__ g, const raw* __restrict__ r,
                                               const float* __restrict__ ck, size_t ck_row,
                                               unsigned ck_boff, size_t ck_field, int seg,
                                               size_t row_base, size_t row_tail, unsigned lane_boff,
                                               int t0, int C, PackT (&kb)[L], PackT (&vb)[L],
-                                              PackT (&gb)[L], Recs& rc) {
+                                              PackT (&gb)[L], PackT (&rb)[L], Recs& rc) {
     const uint32_t bytes = span_bytes(row_tail, t0, C, int(sizeof(raw)));
     const size_t base = row_base + size_t(t0) * C;
     const rsrc_t rk = make_rsrc(k + base, bytes);
@@ -196,6 +208,11 @@ struct Bwd {
       load_buf(kb[i], rk, lane_boff, unsigned(i) * stride);
       load_buf(vb[i], rv, lane_boff, unsigned(i) * stride);
       load_buf(gb[i], rg, lane_boff, unsigned(i) * stride);
+    }
+    if constexpr (GATE) {
+      const rsrc_t rr = make_rsrc(r + base, bytes);
+#pragma unroll
+      for (int i = 0; i < L; ++i) load_buf(rb[i], rr, lane_boff, unsigned(i) * stride);
     }
     const float* rec = ck + ck_row + size_t(seg) * BPS * C;
     Pack<F32, VEC> a;
@@ -213,9 +230,9 @@ struct Bwd {
   __device__ static __forceinline__ void segment(
       Smem& sm, int seg, int nseg, int T, int C, int wave, int lane, bool active, size_t row_base,
       size_t row_tail, unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
-      const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC],
-      const Weights& Wt, raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC],
-      float (&gu)[VEC]) {
+      const PackT (&rb)[L], const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC],
+      const float (&U)[VEC], const Weights& Wt, raw* __restrict__ gk, raw* __restrict__ gv,
+      raw* __restrict__ gr, float (&gw)[VEC], float (&gu)[VEC]) {
     const int t0 = (seg * W + wave) * L;
     float P[VEC], Q[VEC];
 #pragma unroll
@@ -257,23 +274,46 @@ struct Bwd {
     // Forward recompute: keep z = gy/den, z y (zero past the end) and the
     // states (A_t, B_t) = (P, Q) before step t.
     float zz[L][VEC], zy[L][VEC], pa[L][VEC], qa[L][VEC];
+    OutPack<E, VEC> grp[GATE ? L : 1];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const bool valid = FULL || (t0 + i) < T;
+      float grv[VEC];
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
         const float vv = vb[i].get(c);
         const float e = ek[i][c];
         const float e1 = e * U[c];
         const float r = fast_rcp(Q[c] + e1);
-        const float z = gb[i].get(c) * r;
         const float y = fmaf(e1, vv, P[c]) * r;
+        float gyv = gb[i].get(c);
+        if constexpr (GATE) {
+          // The gate's backward with the separate kernels' roundings: its
+          // input gradient round(g s) feeds the recurrence, and
+          // grad_r = g s y (1 - s) with y rounded as the forward stored it.
+          const float sg = sigmoid_ref(rb[i].get(c));
+          const float a = gyv * sg;
+          grv[c] = a * round_to<E>(y) * (1.f - sg);
+          gyv = round_to<E>(a);
+        }
+        const float z = gyv * r;
         zz[i][c] = FULL || valid ? z : 0.f;
         zy[i][c] = FULL || valid ? z * y : 0.f;
         pa[i][c] = P[c];
         qa[i][c] = Q[c];
         P[c] = fmaf(e, vv, P[c] * D[c]);
         Q[c] = fmaf(Q[c], D[c], e);
+      }
+      if constexpr (GATE) grp[i].set(grv);
+    }
+    if constexpr (GATE) {
+      if (active) {
+        // Steps past T fall outside the descriptor and are dropped.
+        const rsrc_t rgr = make_rsrc(gr + row_base + size_t(t0) * C,
+                                     span_bytes(row_tail, t0, C, int(sizeof(raw))));
+        const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
+#pragma unroll
+        for (int i = 0; i < L; ++i) store_buf(grp[i], rgr, lane_boff, unsigned(i) * stride);
       }
     }
     // Reverse summary of this chunk from a zero state at its end, as dot
@@ -366,14 +406,17 @@ struct Bwd {
 };
 
 // decay: time_decay (decay_is_w == 0, w = -exp(decay)) or w itself.
-template <typename E, int VEC, int L, int W>
+// GATE: the forward was y = sigmoid(r) * wkv; gy is the gradient of that y,
+// and the kernel also writes grad_r (gr).
+template <typename E, int VEC, int L, int W, bool GATE>
 __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
     const typename E::raw* __restrict__ gy, const float* __restrict__ decay, int decay_is_w,
     const float* __restrict__ u_in, const typename E::raw* __restrict__ k,
-    const typename E::raw* __restrict__ v, const float* __restrict__ ck,
-    typename E::raw* __restrict__ gk, typename E::raw* __restrict__ gv,
+    const typename E::raw* __restrict__ v, const typename E::raw* __restrict__ r,
+    const float* __restrict__ ck, typename E::raw* __restrict__ gk,
+    typename E::raw* __restrict__ gv, typename E::raw* __restrict__ gr,
     float* __restrict__ gw_part, float* __restrict__ gu_part, int T, int C) {
-  using F = Bwd<E, VEC, L, W>;
+  using F = Bwd<E, VEC, L, W, GATE>;
   using PackT = typename F::PackT;
   __shared__ typename F::Smem sm;
 
@@ -431,34 +474,35 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
   for (int c = 0; c < VEC; ++c) { gw[c] = 0.f; gu[c] = 0.f; }
   if (!bad) {
     PackT kA[L], vA[L], gA[L], kB[L], vB[L], gB[L];
+    PackT xA[L], xB[L];  // receptance chunks (loaded and used only with GATE)
     typename F::Recs rA, rB;
     const int last = nseg - 1;
-    F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, last, row_base, row_tail, lane_boff,
-            last * F::SEG + wave * L, C, kA, vA, gA, rA);
+    F::load(k, v, gy, r, ck, ck_row, ck_boff, ck_field, last, row_base, row_tail, lane_boff,
+            last * F::SEG + wave * L, C, kA, vA, gA, xA, rA);
     // The next segment is prefetched on every path (segment 0 prefetches
     // itself again, a cache hit), so that the wait before a segment's
     // arithmetic only covers the loads it consumes.  Steps past T read as
     // zero (outside the buffer descriptors).
     for (int seg = last; seg >= 0; seg -= 2) {
       const int s1 = max(seg - 1, 0), s2 = max(seg - 2, 0);
-      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s1, row_base, row_tail, lane_boff,
-              s1 * F::SEG + wave * L, C, kB, vB, gB, rB);
+      F::load(k, v, gy, r, ck, ck_row, ck_boff, ck_field, s1, row_base, row_tail, lane_boff,
+              s1 * F::SEG + wave * L, C, kB, vB, gB, xB, rB);
       if (seg < nfull) {
         F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
-                                  kA, vA, gA, rA, D, DL, U, Wt, gk, gv, gw, gu);
+                                  kA, vA, gA, xA, rA, D, DL, U, Wt, gk, gv, gr, gw, gu);
       } else {
         F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
-                                   kA, vA, gA, rA, D, DL, U, Wt, gk, gv, gw, gu);
+                                   kA, vA, gA, xA, rA, D, DL, U, Wt, gk, gv, gr, gw, gu);
       }
       if (seg - 1 < 0) break;
-      F::load(k, v, gy, ck, ck_row, ck_boff, ck_field, s2, row_base, row_tail, lane_boff,
-              s2 * F::SEG + wave * L, C, kA, vA, gA, rA);
+      F::load(k, v, gy, r, ck, ck_row, ck_boff, ck_field, s2, row_base, row_tail, lane_boff,
+              s2 * F::SEG + wave * L, C, kA, vA, gA, xA, rA);
       if (seg - 1 < nfull) {
         F::template segment<true>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
-                                  row_tail, lane_boff, kB, vB, gB, rB, D, DL, U, Wt, gk, gv, gw, gu);
+                                  row_tail, lane_boff, kB, vB, gB, xB, rB, D, DL, U, Wt, gk, gv, gr, gw, gu);
       } else {
         F::template segment<false>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
-                                   row_tail, lane_boff, kB, vB, gB, rB, D, DL, U, Wt, gk, gv, gw, gu);
+                                   row_tail, lane_boff, kB, vB, gB, xB, rB, D, DL, U, Wt, gk, gv, gr, gw, gu);
       }
     }
   }
@@ -491,7 +535,8 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
       if (c >= C) continue;
       const float w2 = (decay_is_w ? decay[c] : -expf(decay[c])) * kLog2e;
       float sw, su;
-      wkv4_bwd_channel_serial<E, 8>(gy, k, v, gk, gv, w2, u_in[c] * kLog2e, T, C,
+      wkv4_bwd_channel_serial<E, 8>(gy, k, v, GATE ? r : nullptr, gk, gv, GATE ? gr : nullptr,
+                                    w2, u_in[c] * kLog2e, T, C,
                                     size_t(b) * T * C + c, ck, size_t(b) * nblk * C + c,
                                     ck_field, sw, su);
       gw_part[size_t(b) * C + c] = sw;
@@ -584,19 +629,31 @@ size_t wkv4_checkpoint_floats(int64_t B, int64_t T, int64_t C) {
 
 size_t wkv4_partials_floats(int64_t B, int64_t C) { return 2 * size_t(B) * size_t(C); }
 
+// r, gr (both null or both given): the gated backward (forward y = sigmoid(r)
+// * wkv, grad_r written to gr).
 template <typename E, int VEC, int L, int W>
 static int launch_bwd(const void* gy, const float* decay, int decay_is_w, const float* u,
-                      const void* k, const void* v, const float* ck, void* gk, void* gv,
-                      float* gtd, float* gtf, float* partials, int B, int T, int C,
-                      hipStream_t stream) {
+                      const void* k, const void* v, const void* r, const float* ck, void* gk,
+                      void* gv, void* gr, float* gtd, float* gtf, float* partials, int B, int T,
+                      int C, hipStream_t stream) {
   using raw = typename E::raw;
   float* gw_part = partials;
   float* gu_part = partials + size_t(B) * C;
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
-  launch(wkv::wkv4_bwd_kernel<E, VEC, L, W>, dim3(unsigned(B) * n_cg),
-                     dim3(W * 64), stream, false, static_cast<const raw*>(gy), decay, decay_is_w, u,
-                     static_cast<const raw*>(k), static_cast<const raw*>(v), ck,
-                     static_cast<raw*>(gk), static_cast<raw*>(gv), gw_part, gu_part, T, C);
+  const dim3 grid(unsigned(B) * n_cg), block(W * 64);
+  const raw* g_ = static_cast<const raw*>(gy);
+  const raw* k_ = static_cast<const raw*>(k);
+  const raw* v_ = static_cast<const raw*>(v);
+  const raw* r_ = static_cast<const raw*>(r);
+  if (r != nullptr) {
+    launch(wkv::wkv4_bwd_kernel<E, VEC, L, W, true>, grid, block, stream, false, g_, decay,
+           decay_is_w, u, k_, v_, r_, ck, static_cast<raw*>(gk), static_cast<raw*>(gv),
+           static_cast<raw*>(gr), gw_part, gu_part, T, C);
+  } else {
+    launch(wkv::wkv4_bwd_kernel<E, VEC, L, W, false>, grid, block, stream, false, g_, decay,
+           decay_is_w, u, k_, v_, r_, ck, static_cast<raw*>(gk), static_cast<raw*>(gv),
+           static_cast<raw*>(nullptr), gw_part, gu_part, T, C);
+  }
   int rc = check_launch("wkv4_bwd_kernel");
   if (rc) return rc;
   launch(wkv::wkv4_param_grad_kernel, dim3((C + 63) / 64), dim3(1024), stream, true,
@@ -606,13 +663,13 @@ static int launch_bwd(const void* gy, const float* decay, int decay_is_w, const 
 
 template <typename E>
 static int dispatch_bwd(const void* gy, const float* decay, int decay_is_w, const float* u,
-                        const void* k, const void* v, const float* ck, void* gk, void* gv,
-                        float* gtd, float* gtf, float* partials, int B, int T, int C,
-                        hipStream_t stream) {
+                        const void* k, const void* v, const void* r, const float* ck, void* gk,
+                        void* gv, void* gr, float* gtd, float* gtf, float* partials, int B,
+                        int T, int C, hipStream_t stream) {
   const TileCfg cfg = pick_bwd_cfg(B, C, int(sizeof(typename E::raw)));
-#define WKV_BWD_CASE(V, LL, WW)                                                             \
-  if (cfg.vec == V && cfg.L == LL && cfg.W == WW)                                           \
-    return launch_bwd<E, V, LL, WW>(gy, decay, decay_is_w, u, k, v, ck, gk, gv, gtd, gtf, \
+#define WKV_BWD_CASE(V, LL, WW)                                                                \
+  if (cfg.vec == V && cfg.L == LL && cfg.W == WW)                                              \
+    return launch_bwd<E, V, LL, WW>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf, \
                                     partials, B, T, C, stream);
   WKV_BWD_CASE(2, 8, 8)
   WKV_BWD_CASE(1, 8, 16)
@@ -625,24 +682,43 @@ static int dispatch_bwd(const void* gy, const float* decay, int decay_is_w, cons
   return fail(1, "wkv4_backward: no kernel for the selected tile configuration");
 }
 
+static int backward_any(const void* gy, const float* decay, int decay_is_w, const float* u,
+                        const void* k, const void* v, const void* r, const float* ck, void* gk,
+                        void* gv, void* gr, float* gtd, float* gtf, float* partials, int B,
+                        int T, int C, int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case 0:
+      return dispatch_bwd<wkv::F32>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf,
+                                    partials, B, T, C, stream);
+    case 1:
+      return dispatch_bwd<wkv::BF16>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf,
+                                     partials, B, T, C, stream);
+    case 2:
+      return dispatch_bwd<wkv::F16>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf,
+                                    partials, B, T, C, stream);
+    default:
+      return fail(1, "wkv4_backward: unknown dtype");
+  }
+}
+
 // Backward from checkpoint records ck (written by the forward kernel).
 int wkv4_backward_ck_impl(const void* gy, const float* decay, int decay_is_w, const float* u,
                           const void* k, const void* v, const float* ck, void* gk, void* gv,
                           float* gtd, float* gtf, float* partials, int B, int T, int C, int dtype,
                           hipStream_t stream) {
-  switch (dtype) {
-    case 0:
-      return dispatch_bwd<wkv::F32>(gy, decay, decay_is_w, u, k, v, ck, gk, gv, gtd, gtf,
-                                    partials, B, T, C, stream);
-    case 1:
-      return dispatch_bwd<wkv::BF16>(gy, decay, decay_is_w, u, k, v, ck, gk, gv, gtd, gtf,
-                                     partials, B, T, C, stream);
-    case 2:
-      return dispatch_bwd<wkv::F16>(gy, decay, decay_is_w, u, k, v, ck, gk, gv, gtd, gtf,
-                                    partials, B, T, C, stream);
-    default:
-      return fail(1, "wkv4_backward: unknown dtype");
-  }
+  return backward_any(gy, decay, decay_is_w, u, k, v, nullptr, ck, gk, gv, nullptr, gtd, gtf,
+                      partials, B, T, C, dtype, stream);
+}
+
+// The gated backward from checkpoint records: g is the gradient of
+// y = sigmoid(r) * wkv; writes grad_r besides grad_k, grad_v and the
+// parameter gradients.
+int wkv4_backward_gated_ck_impl(const void* g, const float* decay, const float* u, const void* k,
+                                const void* v, const void* r, const float* ck, void* gk,
+                                void* gv, void* gr, float* gtd, float* gtf, float* partials,
+                                int B, int T, int C, int dtype, hipStream_t stream) {
+  return backward_any(g, decay, 0, u, k, v, r, ck, gk, gv, gr, gtd, gtf, partials, B, T, C, dtype,
+                      stream);
 }
 
 // Backward from the inputs alone: the forward kernel writes the checkpoint

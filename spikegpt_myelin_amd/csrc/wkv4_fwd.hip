@@ -48,7 +48,7 @@
 
 namespace wkv {
 
-template <typename E, int VEC, int L, int W, bool WY>
+template <typename E, int VEC, int L, int W, bool WY, bool GATE = false>
 struct Fwd {
   using raw = typename E::raw;
   using PackT = Pack<E, VEC>;
@@ -71,10 +71,13 @@ struct Fwd {
   // Loads the chunk of L steps starting at t0 through buffer descriptors
   // based at the chunk (row_base is wave-uniform, lane_boff the lane's byte
   // offset).  Steps at or past T read as zero.
+  // GATE: the receptance chunk rb as well.
   __device__ static __forceinline__ void load_chunk(const raw* __restrict__ k,
-                                                    const raw* __restrict__ v, size_t row_base,
+                                                    const raw* __restrict__ v,
+                                                    const raw* __restrict__ r, size_t row_base,
                                                     size_t row_tail, unsigned lane_boff, int t0,
-                                                    int C, PackT (&kb)[L], PackT (&vb)[L]) {
+                                                    int C, PackT (&kb)[L], PackT (&vb)[L],
+                                                    PackT (&rb)[L]) {
     const uint32_t bytes = span_bytes(row_tail, t0, C, int(sizeof(raw)));
     const size_t base = row_base + size_t(t0) * C;
     const rsrc_t rk = make_rsrc(k + base, bytes);
@@ -85,6 +88,11 @@ struct Fwd {
       load_buf(kb[i], rk, lane_boff, unsigned(i) * stride);
       load_buf(vb[i], rv, lane_boff, unsigned(i) * stride);
     }
+    if constexpr (GATE) {
+      const rsrc_t rr = make_rsrc(r + base, bytes);
+#pragma unroll
+      for (int i = 0; i < L; ++i) load_buf(rb[i], rr, lane_boff, unsigned(i) * stride);
+    }
   }
 
   // One segment.  FULL: every step of the segment is inside the sequence.
@@ -94,7 +102,8 @@ struct Fwd {
       Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
       size_t row_tail, unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
       unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L],
-      const float (&D)[VEC], const float (&DL)[VEC], const float (&U)[VEC]) {
+      const PackT (&rb)[L], const float (&D)[VEC], const float (&DL)[VEC],
+      const float (&U)[VEC]) {
     const int t0 = seg * SEG + wave * L;
     const int par = seg & 1;
     // Phase 1: e = 2^{k log2e} and the chunk summary from a zero state.
@@ -172,6 +181,11 @@ struct Fwd {
           // products from being carried live into this phase.
           pin[c] = fmaf(e, vv, pin[c] * D[c]);
           qin[c] = fmaf(qin[c], D[c], e);
+          // GATE: sigmoid(r) * y with the separate kernels' roundings (y
+          // and sigmoid(r) each rounded to the element type, then the
+          // product), language.py:1035.
+          if constexpr (GATE)
+            yv[c] = round_to<E>(sigmoid_ref(rb[i].get(c))) * round_to<E>(yv[c]);
         }
         yp[i].set(yv);
       }
@@ -194,6 +208,7 @@ struct Fwd {
 template <typename E>
 __device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
                                         const typename E::raw* __restrict__ v,
+                                        const typename E::raw* __restrict__ r,
                                         typename E::raw* __restrict__ y, float w2, float u2, int T,
                                         int C, size_t base, float* __restrict__ ck,
                                         size_t ck_lane, size_t ck_field) {
@@ -213,7 +228,10 @@ __device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
       const float no = fmaxf(o, uk);
       const float a = fast_exp2(o - no);
       const float bb = fast_exp2(uk - no);
-      store_scalar<E>(y + idx, (a * p + bb * vv) / (a * q + bb));
+      float yv = (a * p + bb * vv) / (a * q + bb);
+      if (r != nullptr)
+        yv = round_to<E>(sigmoid_ref(load_scalar<E>(r + idx))) * round_to<E>(yv);
+      store_scalar<E>(y + idx, yv);
     }
     const float wo = w2 + o;
     const float no = fmaxf(wo, kk);
@@ -226,12 +244,15 @@ __device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
 }
 
 // decay: time_decay (decay_is_w == 0, w = -exp(decay)) or w itself.
-template <typename E, int VEC, int L, int W, bool WY>
+// GATE: y = sigmoid(r) * wkv (r [B,T,C] in the element type), the time
+// mix's receptance gate folded in.
+template <typename E, int VEC, int L, int W, bool WY, bool GATE>
 __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
     const typename E::raw* __restrict__ k, const typename E::raw* __restrict__ v,
     const float* __restrict__ decay, int decay_is_w, const float* __restrict__ time_first,
-    typename E::raw* __restrict__ y, float* __restrict__ ck, int T, int C) {
-  using F = Fwd<E, VEC, L, W, WY>;
+    const typename E::raw* __restrict__ r, typename E::raw* __restrict__ y,
+    float* __restrict__ ck, int T, int C) {
+  using F = Fwd<E, VEC, L, W, WY, GATE>;
   using PackT = typename F::PackT;
   __shared__ typename F::Smem sm;
 
@@ -272,28 +293,31 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const int nseg = (T + F::SEG - 1) / F::SEG;
   const int nfull = T / F::SEG;
   PackT kA[L], vA[L], kB[L], vB[L];
+  PackT rA[L], rB[L];  // receptance chunks (loaded and used only with GATE)
   // The next segment is prefetched on every path (past the end the
   // descriptor is empty and the loads return zeros without touching memory):
   // with the same loads issued on every path, the compiler's wait before a
   // segment's arithmetic only covers the loads it consumes, not the prefetch
   // issued just before it.
-  if (!bad) F::load_chunk(k, v, row_base, row_tail, lane_boff, wave * L, C, kA, vA);
+  if (!bad) F::load_chunk(k, v, r, row_base, row_tail, lane_boff, wave * L, C, kA, vA, rA);
   for (int seg = 0; seg < nseg && !bad; seg += 2) {
-    F::load_chunk(k, v, row_base, row_tail, lane_boff, (seg + 1) * F::SEG + wave * L, C, kB, vB);
+    F::load_chunk(k, v, r, row_base, row_tail, lane_boff, (seg + 1) * F::SEG + wave * L, C, kB, vB,
+                  rB);
     bad = seg < nfull
               ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, row_tail, lane_boff, y,
-                                          ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U)
+                                          ck, ck_row, ck_boff, ck_field, kA, vA, rA, D, DL, U)
               : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
-                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, D, DL, U);
+                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, rA, D, DL, U);
     if (bad || seg + 1 >= nseg) break;
-    F::load_chunk(k, v, row_base, row_tail, lane_boff, (seg + 2) * F::SEG + wave * L, C, kA, vA);
+    F::load_chunk(k, v, r, row_base, row_tail, lane_boff, (seg + 2) * F::SEG + wave * L, C, kA, vA,
+                  rA);
     bad = seg + 1 < nfull
               ? F::template segment<true>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                          row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
-                                          U)
+                                          row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, rB, D,
+                                          DL, U)
               : F::template segment<false>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                           row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, D, DL,
-                                           U);
+                                           row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, rB, D,
+                                           DL, U);
   }
   if (bad) {
     // Workgroup-uniform: recompute the row with the running-max recurrence.
@@ -303,7 +327,8 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
       if (c >= C) continue;
       const float w2 = (decay_is_w ? decay[c] : -expf(decay[c])) * kLog2e;
       const float u2 = time_first[c] * kLog2e;
-      wkv4_fwd_channel_serial<E>(k, v, WY ? y : nullptr, w2, u2, T, C, size_t(b) * T * C + c, ck,
+      wkv4_fwd_channel_serial<E>(k, v, GATE ? r : nullptr, WY ? y : nullptr, w2, u2, T, C,
+                                 size_t(b) * T * C + c, ck,
                                  size_t(b) * nblk * C + c, ck_field);
     }
   }
@@ -337,33 +362,41 @@ static TileCfg pick_fwd_cfg(int64_t B, int64_t C, int elem_bytes) {
   return TileCfg{1, 8, 16};
 }
 
+// r (GATE) requires y.
 template <typename E, int VEC, int L, int W>
 static int launch_fwd(const void* k, const void* v, const float* decay, int decay_is_w,
-                      const float* tf, void* y, float* ck, int B, int T, int C,
+                      const float* tf, const void* r, void* y, float* ck, int B, int T, int C,
                       hipStream_t stream) {
   using raw = typename E::raw;
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
   const dim3 grid(unsigned(B) * unsigned(n_cg)), block(W * 64);
-  if (y != nullptr) {
-    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, true>, grid, block, stream, true,
-                       static_cast<const raw*>(k), static_cast<const raw*>(v), decay, decay_is_w,
-                       tf, static_cast<raw*>(y), ck, T, C);
+  const raw* kk = static_cast<const raw*>(k);
+  const raw* vv = static_cast<const raw*>(v);
+  const raw* rr = static_cast<const raw*>(r);
+  if (r != nullptr) {
+    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, true, true>, grid, block, stream, true, kk, vv,
+           decay, decay_is_w, tf, rr, static_cast<raw*>(y), ck, T, C);
+  } else if (y != nullptr) {
+    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, true, false>, grid, block, stream, true, kk, vv,
+           decay, decay_is_w, tf, rr, static_cast<raw*>(y), ck, T, C);
   } else {
-    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, false>, grid, block, stream, true,
-                       static_cast<const raw*>(k), static_cast<const raw*>(v), decay, decay_is_w,
-                       tf, static_cast<raw*>(nullptr), ck, T, C);
+    launch(wkv::wkv4_fwd_kernel<E, VEC, L, W, false, false>, grid, block, stream, true, kk, vv,
+           decay, decay_is_w, tf, rr, static_cast<raw*>(nullptr), ck, T, C);
   }
   return check_launch("wkv4_fwd_kernel");
 }
 
 template <typename E>
 static int dispatch_fwd(const void* k, const void* v, const float* decay, int decay_is_w,
-                        const float* tf, void* y, float* ck, int B, int T, int C,
+                        const float* tf, const void* r, void* y, float* ck, int B, int T, int C,
                         hipStream_t stream) {
-  const TileCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
+  TileCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
+  // The gated kernel holds the receptance chunks as well: at 16 waves per
+  // workgroup (128 VGPRs) the two-channel tile spills, so it runs 8 waves.
+  if (r != nullptr && cfg.vec == 2 && cfg.W == 16) cfg = TileCfg{2, cfg.L, 8};
 #define WKV_FWD_CASE(V, LL, WW)                    \
   if (cfg.vec == V && cfg.L == LL && cfg.W == WW) \
-    return launch_fwd<E, V, LL, WW>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
+    return launch_fwd<E, V, LL, WW>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
   WKV_FWD_CASE(2, 8, 16)
   WKV_FWD_CASE(1, 8, 16)
   WKV_FWD_CASE(2, 8, 8)
@@ -375,15 +408,28 @@ static int dispatch_fwd(const void* k, const void* v, const float* decay, int de
   return fail(1, "wkv4_forward: no kernel for the selected tile configuration");
 }
 
+static int forward_any(const void* k, const void* v, const float* decay, int decay_is_w,
+                       const float* tf, const void* r, void* y, float* ck, int B, int T, int C,
+                       int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case 0: return dispatch_fwd<wkv::F32>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
+    case 1: return dispatch_fwd<wkv::BF16>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
+    case 2: return dispatch_fwd<wkv::F16>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
+    default: return fail(1, "wkv4_forward: unknown dtype");
+  }
+}
+
 int wkv4_forward_impl(const void* k, const void* v, const float* decay, int decay_is_w,
                       const float* tf, void* y, float* ck, int B, int T, int C, int dtype,
                       hipStream_t stream) {
-  switch (dtype) {
-    case 0: return dispatch_fwd<wkv::F32>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
-    case 1: return dispatch_fwd<wkv::BF16>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
-    case 2: return dispatch_fwd<wkv::F16>(k, v, decay, decay_is_w, tf, y, ck, B, T, C, stream);
-    default: return fail(1, "wkv4_forward: unknown dtype");
-  }
+  return forward_any(k, v, decay, decay_is_w, tf, nullptr, y, ck, B, T, C, dtype, stream);
+}
+
+// y = sigmoid(r) * wkv (the time mix's gate folded in); y must be given.
+int wkv4_forward_gated_impl(const void* k, const void* v, const float* decay, const float* tf,
+                            const void* r, void* y, float* ck, int B, int T, int C, int dtype,
+                            hipStream_t stream) {
+  return forward_any(k, v, decay, 0, tf, r, y, ck, B, T, C, dtype, stream);
 }
 
 }  // namespace wkv_host

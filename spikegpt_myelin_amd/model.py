@@ -33,10 +33,10 @@ from .gates import relu_square, sigmoid_gate
 from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguageModelState,
                          SpikeTimeMixState, SpikingSequenceLIFState, StepWorkspace, block_step,
                          initial_packed, pack_state, state_from_packed)
-from .language import weighted_key_value
 from .lif import lif_residual, lif_sequence
 from .splitk import split_k_sum
 from .timemix import layer_norm_shift_mix, layer_norm_shift_mix_fork, token_shift_mix
+from .wkv import weighted_key_value_gated
 
 
 @dataclass
@@ -223,8 +223,10 @@ class SpikeTimeMix(nn.Module):
         """Everything after the token-shift mixes (``language.py:1019-1036``)."""
         key = self.key(k_in)
         value = self.value(v_in)
-        wkv = weighted_key_value(key, value, self.time_decay, self.time_first)
-        return self.output(sigmoid_gate(self.receptance(r_in), wkv))
+        # sigmoid(r) * wkv with the gate folded into the WKV kernels.
+        gated = weighted_key_value_gated(key, value, self.time_decay, self.time_first,
+                                         self.receptance(r_in))
+        return self.output(gated)
 
 
 class SpikeChannelMix(nn.Module):

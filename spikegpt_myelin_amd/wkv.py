@@ -193,6 +193,107 @@ def _train_backward(ctx, grad_y, _grad_ck):
 _wkv4_forward_train.register_autograd(_train_backward, setup_context=_train_setup_context)
 
 
+# ------------------------------------------- gated training ops (time mix) --
+# y = sigmoid(receptance) * wkv(key, value), the time mix's gate
+# (language.py:1028-1035) folded into the WKV kernels; values equal
+# myelin::wkv_forward_bf16io followed by myelin::sigmoid_gate, bit for bit.
+@torch.library.custom_op("myelin::wkv4_gated_forward_train", mutates_args=())
+def _wkv4_gated_forward_train(
+    key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor, receptance: Tensor
+) -> tuple[Tensor, Tensor]:
+    _lib.require_gpu(key, value, time_decay, time_first, receptance)
+    if not (key.dtype == value.dtype == receptance.dtype and key.dtype in _NATIVE
+            and receptance.shape == key.shape):
+        raise ValueError("wkv4_gated_forward_train: key, value, receptance of one shape and dtype")
+    b, t, c = key.shape
+    k, v, r = _lib.aligned(key), _lib.aligned(value), _lib.aligned(receptance)
+    td = _lib.aligned(time_decay.float())
+    tf = _lib.aligned(time_first.float())
+    y = torch.empty_like(k)
+    ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=k.device)
+    lib = _lib.load()
+    rc = _lib.timed("wkv4_forward_gated", k.device, lambda: lib.wkv4_forward_gated_checkpointed(
+        k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), r.data_ptr(), y.data_ptr(),
+        ck.data_ptr(), b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
+    _lib.check(rc, "wkv4_forward_gated_checkpointed")
+    return y, ck
+
+
+@_wkv4_gated_forward_train.register_fake
+def _(key, value, time_decay, time_first, receptance):
+    b, t, c = key.shape
+    return (torch.empty_like(key),
+            torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=key.device))
+
+
+@torch.library.custom_op("myelin::wkv4_gated_backward_train", mutates_args=())
+def _wkv4_gated_backward_train(
+    grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
+    receptance: Tensor, checkpoint: Tensor,
+) -> list[Tensor]:
+    """[grad_key, grad_value, grad_receptance, grad_time_decay, grad_time_first]."""
+    _lib.require_gpu(grad_y, key, value, time_decay, time_first, receptance, checkpoint)
+    b, t, c = key.shape
+    k, v, r = _lib.aligned(key), _lib.aligned(value), _lib.aligned(receptance)
+    gy = _lib.aligned(grad_y.to(k.dtype))
+    td = _lib.aligned(time_decay.float())
+    tf = _lib.aligned(time_first.float())
+    ck = _lib.aligned(checkpoint)
+    gk, gv, gr = torch.empty_like(k), torch.empty_like(k), torch.empty_like(k)
+    gtd = torch.empty(c, dtype=torch.float32, device=k.device)
+    gtf = torch.empty(c, dtype=torch.float32, device=k.device)
+    ws = torch.empty(2 * b * c, dtype=torch.float32, device=k.device)  # [2, B, C] partials
+    lib = _lib.load()
+    rc = _lib.timed("wkv4_backward_gated", k.device, lambda: lib.wkv4_backward_gated_checkpointed(
+        gy.data_ptr(), td.data_ptr(), tf.data_ptr(), k.data_ptr(), v.data_ptr(), r.data_ptr(),
+        ck.data_ptr(), gk.data_ptr(), gv.data_ptr(), gr.data_ptr(), gtd.data_ptr(), gtf.data_ptr(),
+        ws.data_ptr(), ws.numel() * 4, b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
+    _lib.check(rc, "wkv4_backward_gated_checkpointed")
+    return [gk, gv, gr, gtd, gtf]
+
+
+@_wkv4_gated_backward_train.register_fake
+def _(grad_y, key, value, time_decay, time_first, receptance, checkpoint):
+    c = key.shape[-1]
+    f32 = {"dtype": torch.float32, "device": key.device}
+    return [torch.empty_like(key), torch.empty_like(key), torch.empty_like(key),
+            torch.empty(c, **f32), torch.empty(c, **f32)]
+
+
+def _gated_setup_context(ctx, inputs, output):
+    ctx.save_for_backward(*inputs, output[1])
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)
+
+
+def _gated_backward(ctx, grad_y, _grad_ck):
+    key, value, time_decay, time_first, receptance, ck = ctx.saved_tensors
+    gk, gv, gr, gtd, gtf = torch.ops.myelin.wkv4_gated_backward_train(
+        grad_y, key, value, time_decay, time_first, receptance, ck)
+    return gk, gv, gtd.to(time_decay.dtype), gtf.to(time_first.dtype), gr
+
+
+_wkv4_gated_forward_train.register_autograd(_gated_backward, setup_context=_gated_setup_context)
+
+
+def weighted_key_value_gated(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
+                             receptance: Tensor) -> Tensor:
+    """``sigmoid(receptance) * weighted_key_value(key, value, ...)`` (the time
+    mix's output before its projection, ``language.py:1028-1035``).  One
+    fused kernel pair when key, value and receptance share a shape and a
+    float32/bfloat16/float16 dtype on the GPU (values equal the two separate
+    ops bit for bit); otherwise the two ops."""
+    if (key.is_cuda and key.dtype == value.dtype == receptance.dtype and key.dtype in _NATIVE
+            and key.shape == value.shape == receptance.shape and key.ndim == 3):
+        y, _ = torch.ops.myelin.wkv4_gated_forward_train(key, value, time_decay, time_first,
+                                                         receptance)
+        return y
+    from .gates import sigmoid_gate
+    from .language import weighted_key_value
+
+    return sigmoid_gate(receptance, weighted_key_value(key, value, time_decay, time_first))
+
+
 # ------------------------------------------------------------ public ops ----
 _LIB = torch.library.Library("myelin", "FRAGMENT")
 _LIB.define("wkv_forward(Tensor key, Tensor value, Tensor time_decay, Tensor time_first) -> Tensor")

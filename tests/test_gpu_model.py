@@ -61,7 +61,8 @@ def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
 
     with monkeypatch.context() as mp:
         if oracle:
-            mp.setattr(M, "weighted_key_value", _oracle_wkv)
+            mp.setattr(M, "weighted_key_value_gated",
+                       lambda k, v, td, tf, r: torch.sigmoid(r) * _oracle_wkv(k, v, td, tf))
             mp.setattr(M, "lif_sequence", _oracle_lif)
             mp.setattr(M, "lif_residual", lambda residual, x, **kw: residual + _oracle_lif(x, **kw))
             mp.setattr(M, "token_shift_mix", _oracle_mix)

@@ -1,0 +1,94 @@
+"""The time mix's receptance gate folded into the WKV kernels
+(myelin::wkv4_gated_forward_train and its backward): equal, bit for bit, to
+the separate ops it replaces (myelin::wkv_forward{,_bf16io} followed by
+myelin::sigmoid_gate, and their backwards), and close to the float64
+oracle's sigmoid(r) * wkv."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import spikegpt_myelin_amd  # noqa: F401
+from oracle import wkv4 as O
+from spikegpt_myelin_amd import weighted_key_value_gated
+from spikegpt_myelin_amd.gates import sigmoid_gate
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _inputs(b, t, c, seed, dtype, key_scale=1.0):
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=seed, dtype=torch.float32)
+    g = torch.Generator().manual_seed(seed + 100)
+    r = torch.randn(b, t, c, generator=g) * 2
+    k = (k * key_scale)
+    return ([x.to(dtype) for x in (k, v)] + [td, tf] + [r.to(dtype), gy.to(dtype)])
+
+
+def _run(fn, k, v, td, tf, r, gy):
+    leaves = [x.to(DEV).requires_grad_(True) for x in (k, v, td, tf, r)]
+    y = fn(*leaves)
+    grads = torch.autograd.grad(y, leaves, gy.to(DEV))
+    return (y, *grads)
+
+
+def _unfused(k, v, td, tf, r):
+    op = torch.ops.myelin.wkv_forward if k.dtype == torch.float32 else \
+        torch.ops.myelin.wkv_forward_bf16io
+    return sigmoid_gate(r, op(k, v, td, tf))
+
+
+NAMES = ("y", "grad_k", "grad_v", "grad_time_decay", "grad_time_first", "grad_r")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("b,t,c", [(2, 70, 128), (3, 200, 256), (1, 1, 64), (2, 130, 512)])
+def test_equals_the_separate_ops(dtype, b, t, c):
+    print(f"gated wkv {dtype} B={b} T={t} C={c}", flush=True)
+    xs = _inputs(b, t, c, seed=t + c, dtype=dtype)
+    fused = _run(weighted_key_value_gated, *xs)
+    plain = _run(_unfused, *xs)
+    assert fused[0].dtype == dtype and fused[5].dtype == dtype
+    for name, a, e in zip(NAMES, fused, plain):
+        assert torch.equal(a, e), f"{name} differs from the separate ops"
+
+
+def test_headline_shape_equals_the_separate_ops():
+    xs = _inputs(64, 1024, 512, seed=5, dtype=torch.bfloat16)
+    fused = _run(weighted_key_value_gated, *xs)
+    plain = _run(_unfused, *xs)
+    for name, a, e in zip(NAMES, fused, plain):
+        assert torch.equal(a, e), f"{name} differs from the separate ops"
+
+
+def test_keys_outside_the_shared_frame():
+    # Keys scaled to several tens: such rows take the kernels' exact
+    # running-max path.  The recurrence's outputs stay equal; grad_r uses the
+    # backward's own recomputation of y there (within one bf16 step of the
+    # stored y).
+    xs = _inputs(2, 90, 128, seed=9, dtype=torch.bfloat16, key_scale=20.0)
+    fused = _run(weighted_key_value_gated, *xs)
+    plain = _run(_unfused, *xs)
+    for name, a, e in zip(NAMES[:5], fused[:5], plain[:5]):
+        assert torch.equal(a, e), f"{name} differs from the separate ops"
+    torch.testing.assert_close(fused[5].float(), plain[5].float(), rtol=2e-2, atol=1e-2)
+
+
+def test_matches_the_float64_oracle():
+    k, v, td, tf, r, gy = _inputs(2, 150, 192, seed=3, dtype=torch.bfloat16)
+    got = _run(weighted_key_value_gated, k, v, td, tf, r, gy)
+    leaves = [x.double().requires_grad_(True) for x in (k, v, td, tf, r)]
+    y = torch.sigmoid(leaves[4]) * O.wkv_loop(*leaves[:4])
+    ref = (y, *torch.autograd.grad(y, leaves, gy.double()))
+    for name, a, e in zip(NAMES, got, ref):
+        a = a.detach().double().cpu()
+        scale = max(float(e.abs().max()), 1e-30)
+        assert torch.allclose(a, e.detach(), rtol=2e-2, atol=1e-2 * scale), name
+
+
+def test_opcheck():
+    k, v, td, tf, r, gy = (x.to(DEV) for x in _inputs(2, 40, 128, seed=1, dtype=torch.bfloat16))
+    torch.library.opcheck(torch.ops.myelin.wkv4_gated_forward_train, (k, v, td, tf, r))
+    y, ck = torch.ops.myelin.wkv4_gated_forward_train(k, v, td, tf, r)
+    torch.library.opcheck(torch.ops.myelin.wkv4_gated_backward_train, (gy, k, v, td, tf, r, ck))
