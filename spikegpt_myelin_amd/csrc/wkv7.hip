@@ -508,6 +508,8 @@ struct BwdSmem {
   // + column], and dv.
   float red[kKS][4 * 5 * kN + kRedPad];
   float dvb[kKS][kN + kRedPad];
+  // Store target of the lanes that hold no dv value (one word per thread).
+  float dv_sink[kThreads];
 };
 
 // Recompute + reverse over one sub-chunk of cnt steps starting at staged
@@ -519,6 +521,13 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
                                              int sl, int cnt, const Lane& L, float (&G)[4][4]) {
   constexpr int KS = kKS;
   const int col = L.j0 + L.rg;  // column this lane holds after rows4_sum
+  // dv of row i0 + cg is stored by lane cg < 4 of each DPP row (every lane of
+  // the row holds the four rows' sums); the other lanes store to their own
+  // sink word, so the store needs no exec mask (a mask per step splits the
+  // sub-chunk into one basic block per step).
+  const bool dv_lane = L.cg < 4;
+  float* const dv_base = dv_lane ? &sm.dvb[0][L.i0 + L.cg] : &sm.dv_sink[threadIdx.x];
+  const int dv_stride = dv_lane ? kN + kRedPad : 0;
   float S[4][4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -611,8 +620,11 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
       rs[2 * kN + col] = rows4_sum(pw[0], pw[1], pw[2], pw[3]);
       rs[3 * kN + col] = rows4_sum(pa[0], pa[1], pa[2], pa[3]);
       rs[4 * kN + col] = rows4_sum(pb[0], pb[1], pb[2], pb[3]);
-      if (L.cg == 0)
-        *reinterpret_cast<float4*>(&sm.dvb[s][L.i0]) = make_float4(dvr[0], dvr[1], dvr[2], dvr[3]);
+      {
+        const float d01 = (L.cg & 1) ? dvr[1] : dvr[0];
+        const float d23 = (L.cg & 1) ? dvr[3] : dvr[2];
+        dv_base[s * dv_stride] = (L.cg & 2) ? d23 : d01;
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
