@@ -506,8 +506,11 @@ struct BwdSmem {
   // Per sub-chunk step: per-wave partial sums over the wave's 16 rows of the
   // five key-indexed gradients (dr, dk, dw, da, db) at [(wave * 5 + q) * kN
   // + column], and dv.
-  float red[kKS][4 * 5 * kN + kRedPad];
-  float dvb[kKS][kN + kRedPad];
+  // Double-buffered by sub-chunk parity: a sub-chunk writes one buffer while
+  // slower threads may still read the previous sub-chunk's sums from the
+  // other, so one barrier per sub-chunk suffices.
+  float red[2][kKS][4 * 5 * kN + kRedPad];
+  float dvb[2][kKS][kN + kRedPad];
   // Store target of the lanes that hold no dv value (one word per thread).
   float dv_sink[kThreads];
 };
@@ -517,7 +520,8 @@ struct BwdSmem {
 // per-step guards).  Leaves the per-step partial sums in sm.red / sm.dvb and
 // advances G to before the sub-chunk.
 template <bool FULL>
-__device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const float (&S0)[4][4],
+__device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float* sg,
+                                             const float (&S0)[4][4],
                                              int sl, int cnt, const Lane& L, float (&G)[4][4]) {
   constexpr int KS = kKS;
   const int col = L.j0 + L.rg;  // column this lane holds after rows4_sum
@@ -526,7 +530,7 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
   // sink word, so the store needs no exec mask (a mask per step splits the
   // sub-chunk into one basic block per step).
   const bool dv_lane = L.cg < 4;
-  float* const dv_base = dv_lane ? &sm.dvb[0][L.i0 + L.cg] : &sm.dv_sink[threadIdx.x];
+  float* const dv_base = dv_lane ? &sm.dvb[rbuf][0][L.i0 + L.cg] : &sm.dv_sink[threadIdx.x];
   const int dv_stride = dv_lane ? kN + kRedPad : 0;
   float S[4][4];
 #pragma unroll
@@ -614,7 +618,7 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, const float* sg, const
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) G[r][c] = fmaf(G[r][c], ww[c], cc[r] * aa[c]);
-      float* rs = &sm.red[s][L.wv * 5 * kN];
+      float* rs = &sm.red[rbuf][s][L.wv * 5 * kN];
       rs[0 * kN + col] = rows4_sum(pr[0], pr[1], pr[2], pr[3]);
       rs[1 * kN + col] = rows4_sum(pk[0], pk[1], pk[2], pk[3]);
       rs[2 * kN + col] = rows4_sum(pw[0], pw[1], pw[2], pw[3]);
@@ -651,7 +655,8 @@ struct GradStores {
     for (int k = 0; k < NS; ++k) dst[k] = nullptr;
   }
 
-  __device__ __forceinline__ void collect(const BwdSmem& sm, raw* dr, raw* dk, raw* dw, raw* da,
+  __device__ __forceinline__ void collect(const BwdSmem& sm, int rbuf, raw* dr, raw* dk, raw* dw,
+                                          raw* da,
                                           raw* db, raw* dv, int bi, int h, int t, int cnt, int T,
                                           int H) {
 #pragma unroll
@@ -668,15 +673,15 @@ struct GradStores {
         for (int e = 0; e < EPP; e += 4) {
           float4 x;
           if (q < 5) {
-            x = *reinterpret_cast<const float4*>(&sm.red[s][q * kN + pc * EPP + e]);
+            x = *reinterpret_cast<const float4*>(&sm.red[rbuf][s][q * kN + pc * EPP + e]);
 #pragma unroll
             for (int wv = 1; wv < 4; ++wv) {
               const float4 z = *reinterpret_cast<const float4*>(
-                  &sm.red[s][(wv * 5 + q) * kN + pc * EPP + e]);
+                  &sm.red[rbuf][s][(wv * 5 + q) * kN + pc * EPP + e]);
               x.x += z.x; x.y += z.y; x.z += z.z; x.w += z.w;
             }
           } else {
-            x = *reinterpret_cast<const float4*>(&sm.dvb[s][pc * EPP + e]);
+            x = *reinterpret_cast<const float4*>(&sm.dvb[rbuf][s][pc * EPP + e]);
           }
           f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
         }
@@ -767,13 +772,14 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
     if (blk > 0 && (m == kNSub - 1 || sc == nrec - 1)) st.load(in, bi, h, t0 - kKC, T, H);
     const float* sg = sm.stage[blk & 1];
     if (cnt == kKS) {
-      bwd_subchunk<true>(sm, sg, S0, sl, cnt, L, G);
+      bwd_subchunk<true>(sm, sc & 1, sg, S0, sl, cnt, L, G);
     } else {
-      bwd_subchunk<false>(sm, sg, S0, sl, cnt, L, G);
+      bwd_subchunk<false>(sm, sc & 1, sg, S0, sl, cnt, L, G);
     }
     __syncthreads();
-    out.collect(sm, dr, dk, dw, da, db, dv, bi, h, t0 + sl, cnt, T, H);
-    __syncthreads();
+    out.collect(sm, sc & 1, dr, dk, dw, da, db, dv, bi, h, t0 + sl, cnt, T, H);
+    // No barrier here: the next sub-chunk writes the other reduction buffer,
+    // and the barrier after it orders this collect before the one after.
     if (m == 0 && blk > 0) {
       st.store(sm.stage[(blk - 1) & 1]);
       __syncthreads();
