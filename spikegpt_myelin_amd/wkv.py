@@ -135,11 +135,10 @@ def _(key, value, time_decay, time_first):
     )
 
 
-@torch.library.custom_op("myelin::wkv4_backward_train", mutates_args=())
-def _wkv4_backward_train(
-    grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
-    checkpoint: Tensor,
-) -> list[Tensor]:
+def _launch_backward_train(grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor,
+                           time_first: Tensor, checkpoint: Tensor) -> list[Tensor]:
+    """[gk, gv (k's compute dtype), g_time_decay, g_time_first] from the
+    forward's checkpoint records."""
     _lib.require_gpu(grad_y, key, value, time_decay, time_first, checkpoint)
     b, t, c = key.shape
     k, v = _compute_inputs(key, value)
@@ -160,6 +159,14 @@ def _wkv4_backward_train(
     ))
     _lib.check(rc, "wkv4_backward_checkpointed")
     return [gk, gv, gtd, gtf]
+
+
+@torch.library.custom_op("myelin::wkv4_backward_train", mutates_args=())
+def _wkv4_backward_train(
+    grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
+    checkpoint: Tensor,
+) -> list[Tensor]:
+    return _launch_backward_train(grad_y, key, value, time_decay, time_first, checkpoint)
 
 
 @_wkv4_backward_train.register_fake
@@ -197,10 +204,9 @@ _wkv4_forward_train.register_autograd(_train_backward, setup_context=_train_setu
 # y = sigmoid(receptance) * wkv(key, value), the time mix's gate
 # (language.py:1028-1035) folded into the WKV kernels; values equal
 # myelin::wkv_forward_bf16io followed by myelin::sigmoid_gate, bit for bit.
-@torch.library.custom_op("myelin::wkv4_gated_forward_train", mutates_args=())
-def _wkv4_gated_forward_train(
-    key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor, receptance: Tensor
-) -> tuple[Tensor, Tensor]:
+def _launch_gated_forward(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
+                         receptance: Tensor) -> tuple[Tensor, Tensor]:
+    """y = sigmoid(receptance) * wkv and the checkpoint records."""
     _lib.require_gpu(key, value, time_decay, time_first, receptance)
     if not (key.dtype == value.dtype == receptance.dtype and key.dtype in _NATIVE
             and receptance.shape == key.shape):
@@ -219,6 +225,13 @@ def _wkv4_gated_forward_train(
     return y, ck
 
 
+@torch.library.custom_op("myelin::wkv4_gated_forward_train", mutates_args=())
+def _wkv4_gated_forward_train(
+    key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor, receptance: Tensor
+) -> tuple[Tensor, Tensor]:
+    return _launch_gated_forward(key, value, time_decay, time_first, receptance)
+
+
 @_wkv4_gated_forward_train.register_fake
 def _(key, value, time_decay, time_first, receptance):
     b, t, c = key.shape
@@ -226,11 +239,9 @@ def _(key, value, time_decay, time_first, receptance):
             torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=key.device))
 
 
-@torch.library.custom_op("myelin::wkv4_gated_backward_train", mutates_args=())
-def _wkv4_gated_backward_train(
-    grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
-    receptance: Tensor, checkpoint: Tensor,
-) -> list[Tensor]:
+def _launch_gated_backward(grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor,
+                          time_first: Tensor, receptance: Tensor,
+                          checkpoint: Tensor) -> list[Tensor]:
     """[grad_key, grad_value, grad_receptance, grad_time_decay, grad_time_first]."""
     _lib.require_gpu(grad_y, key, value, time_decay, time_first, receptance, checkpoint)
     b, t, c = key.shape
@@ -250,6 +261,15 @@ def _wkv4_gated_backward_train(
         ws.data_ptr(), ws.numel() * 4, b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
     _lib.check(rc, "wkv4_backward_gated_checkpointed")
     return [gk, gv, gr, gtd, gtf]
+
+
+@torch.library.custom_op("myelin::wkv4_gated_backward_train", mutates_args=())
+def _wkv4_gated_backward_train(
+    grad_y: Tensor, key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
+    receptance: Tensor, checkpoint: Tensor,
+) -> list[Tensor]:
+    return _launch_gated_backward(grad_y, key, value, time_decay, time_first, receptance,
+                                  checkpoint)
 
 
 @_wkv4_gated_backward_train.register_fake
@@ -276,6 +296,61 @@ def _gated_backward(ctx, grad_y, _grad_ck):
 _wkv4_gated_forward_train.register_autograd(_gated_backward, setup_context=_gated_setup_context)
 
 
+# ------------------------------------------------------ eager fast path -----
+# The private ops above carry torch.compile / fake-tensor / functorch support,
+# and their Python layers (autograd wrapper, default filling, redispatch)
+# cost more host time per call than the kernels take at training shapes.
+# Plain eager calls on real GPU tensors go through these two Functions
+# instead: the same launchers, the same saved tensors and results.
+def _eager(t: Tensor) -> bool:
+    """Real GPU tensor, outside tracing, transforms and dispatch modes."""
+    return (t.is_cuda and not torch.compiler.is_compiling()
+            and not torch._C._are_functorch_transforms_active()
+            and torch._C._len_torch_dispatch_stack() == 0
+            and not _subclass_or_fake(t))
+
+
+def _subclass_or_fake(t: Tensor) -> bool:
+    from torch._subclasses.fake_tensor import is_fake
+
+    # Tensor subclasses (functional, fake, wrapper tensors) keep the op path.
+    if type(t) is not Tensor and not isinstance(t, torch.nn.Parameter):
+        return True
+    return is_fake(t)
+
+
+class _Wkv4TrainFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, key, value, time_decay, time_first):
+        y, ck = _launch_forward(key, value, time_decay, time_first, with_checkpoint=True)
+        ctx.save_for_backward(key, value, time_decay, time_first, ck)
+        return y
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_y):
+        key, value, time_decay, time_first, ck = ctx.saved_tensors
+        gk, gv, gtd, gtf = _launch_backward_train(grad_y, key, value, time_decay, time_first, ck)
+        return (gk.to(key.dtype), gv.to(value.dtype), gtd.to(time_decay.dtype),
+                gtf.to(time_first.dtype))
+
+
+class _Wkv4GatedTrainFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, key, value, time_decay, time_first, receptance):
+        y, ck = _launch_gated_forward(key, value, time_decay, time_first, receptance)
+        ctx.save_for_backward(key, value, time_decay, time_first, receptance, ck)
+        return y
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_y):
+        key, value, time_decay, time_first, receptance, ck = ctx.saved_tensors
+        gk, gv, gr, gtd, gtf = _launch_gated_backward(grad_y, key, value, time_decay, time_first,
+                                                      receptance, ck)
+        return gk, gv, gtd.to(time_decay.dtype), gtf.to(time_first.dtype), gr
+
+
 def weighted_key_value_gated(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
                              receptance: Tensor) -> Tensor:
     """``sigmoid(receptance) * weighted_key_value(key, value, ...)`` (the time
@@ -285,6 +360,8 @@ def weighted_key_value_gated(key: Tensor, value: Tensor, time_decay: Tensor, tim
     ops bit for bit); otherwise the two ops."""
     if (key.is_cuda and key.dtype == value.dtype == receptance.dtype and key.dtype in _NATIVE
             and key.shape == value.shape == receptance.shape and key.ndim == 3):
+        if _eager(key):
+            return _Wkv4GatedTrainFn.apply(key, value, time_decay, time_first, receptance)
         y, _ = torch.ops.myelin.wkv4_gated_forward_train(key, value, time_decay, time_first,
                                                          receptance)
         return y
@@ -303,7 +380,10 @@ _LIB.define("wkv_forward_bf16io(Tensor key, Tensor value, Tensor time_decay, Ten
 def _forward_composite(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
     # fp32 recurrence on the exactly widened inputs; y in key.dtype
     # (wkv_triton.py:151-158; bf16io: wkv_bf16.py:147-154).
-    y, _ = torch.ops.myelin.wkv4_forward_train(key, value, time_decay, time_first)
+    if _eager(key):
+        y = _Wkv4TrainFn.apply(key, value, time_decay, time_first)
+    else:
+        y, _ = torch.ops.myelin.wkv4_forward_train(key, value, time_decay, time_first)
     return y if y.dtype == key.dtype else y.to(key.dtype)
 
 

@@ -366,3 +366,30 @@ def test_graph_capture_replays_match_eager():
         for got, ref, name in zip(outs, eager, ("y", "gk", "gv", "gtd", "gtf")):
             assert torch.equal(got, ref), f"replay {rep}: {name} differs from eager"
         del junk
+
+
+@pytest.mark.parametrize("kdt,vdt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.float32)])
+def test_eager_path_equals_op_path(kdt, vdt):
+    # Eager calls on GPU tensors run an autograd.Function over the launchers;
+    # traced calls run the private custom ops.  Same kernels, same values.
+    from spikegpt_myelin_amd import weighted_key_value_hip
+
+    k, v, td, tf, gy = O.make_inputs(2, 150, 192, seed=21, dtype=torch.float32)
+    kd, vd = k.to(kdt).to(DEV), v.to(vdt).to(DEV)
+    tdd, tfd, gyd = td.to(DEV), tf.to(DEV), gy.to(kdt).to(DEV)
+
+    def op_path(k_, v_, td_, tf_):
+        y, _ = torch.ops.myelin.wkv4_forward_train(k_, v_, td_, tf_)
+        return y.to(k_.dtype)
+
+    kk = kd.clone().requires_grad_(True)
+    y = weighted_key_value_hip(kk, vd, tdd, tfd)
+    fn = y.grad_fn
+    if type(fn).__name__ == "ToCopyBackward0":  # fp32 y cast to key.dtype
+        fn = fn.next_functions[0][0]
+    assert type(fn).__name__.startswith("_Wkv4TrainFn")
+    eager = _grads(weighted_key_value_hip, kd, vd, tdd, tfd, gyd)
+    traced = _grads(op_path, kd, vd, tdd, tfd, gyd)
+    for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), eager, traced):
+        assert a.dtype == b.dtype and torch.equal(a, b), name

@@ -92,3 +92,21 @@ def test_opcheck():
     torch.library.opcheck(torch.ops.myelin.wkv4_gated_forward_train, (k, v, td, tf, r))
     y, ck = torch.ops.myelin.wkv4_gated_forward_train(k, v, td, tf, r)
     torch.library.opcheck(torch.ops.myelin.wkv4_gated_backward_train, (gy, k, v, td, tf, r, ck))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_eager_path_equals_op_path(dtype):
+    # Eager calls run an autograd.Function over the launchers; traced calls
+    # run the private custom ops.  Same kernels, same values.
+    xs = _inputs(2, 150, 192, seed=22, dtype=dtype)
+
+    def op_path(k, v, td, tf, r):
+        y, _ = torch.ops.myelin.wkv4_gated_forward_train(k, v, td, tf, r)
+        return y
+
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs[:5]]
+    assert type(weighted_key_value_gated(*leaves).grad_fn).__name__.startswith("_Wkv4GatedTrainFn")
+    eager = _run(weighted_key_value_gated, *xs)
+    traced = _run(op_path, *xs)
+    for name, a, e in zip(NAMES, eager, traced):
+        assert a.dtype == e.dtype and torch.equal(a, e), name
