@@ -209,8 +209,9 @@ def arm_events(start: torch.cuda.Event, end: torch.cuda.Event) -> None:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    """The calling thread's current HIP stream on ``t``'s device."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The calling thread's current HIP stream on ``t``'s device (the raw
+    handle, without building a ``torch.cuda.Stream`` object per call)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def require_gpu(*tensors: torch.Tensor) -> None:
