@@ -12,10 +12,24 @@ was deleted, ``benchmarks/results/optimizer_wkv_experiments_5090.md:3``, and
 its arithmetic lived in the unpinned external ``fla`` package).  PARITY
 UNPINNED against the reference: there is no reference implementation, test or
 fixture to compare with.  What pins this restatement is mathematics only
-(``tests/test_oracle_wkv7.py``): with a = b = 0 it must equal causal
-(decayed) linear attention computed as a masked matrix product, autograd
-through it must agree with central finite differences, and the state carried
-across a split of the sequence must reproduce the unsplit run.
+(``tests/test_oracle_wkv7.py``):
+
+* with a = b = 0 it must equal causal (decayed) linear attention computed as
+  a masked matrix product;
+* the low-rank term on hand-computed one-hot states: S = e_i e_j^T,
+  a = e_j, b = e_m, w = 0, v = k = 0 gives S' = e_i e_m^T (the order
+  (S a) b^T, not (S b) a^T);
+* the delta-rule identity: w = 1, a = -kappa, b = kappa, r = kappa with unit
+  kappa gives y_t = v_t (k_t . kappa_t) from any state (output on the
+  post-update state);
+* :func:`wkv7_matrix_form` (numpy, explicit 64x64 transition matrices
+  diag(w) + a b^T and a matrix product per step) for a and b drawn
+  independently (:func:`make_general_inputs`);
+* autograd through it agrees with central finite differences and with the
+  explicit reverse recurrence, and the state carried across a split of the
+  sequence reproduces the unsplit run;
+* planted mistakes ((S b) a^T, output before the update, decay on the value
+  index) each fail one of the checks above.
 """
 
 from __future__ import annotations
@@ -81,6 +95,52 @@ def make_inputs(batch: int, steps: int, heads: int, n: int = 64, *, seed: int, d
     a = -kappa
     b = kappa * iclr
     return tuple(t.to(dtype) for t in (r, w, k, v, a, b))
+
+
+def make_general_inputs(batch: int, steps: int, heads: int, n: int = 64, *, seed: int,
+                        dtype=torch.float32):
+    """As :func:`make_inputs`, but with a and b along independent directions:
+    ``a = -kappa_a``, ``b = kappa_b * iclr`` with ``kappa_a``, ``kappa_b`` two
+    independent unit vectors per head.  ``a b^T`` is then not symmetric, so
+    ``(S a) b^T`` and ``(S b) a^T`` differ on these inputs (with ``a``
+    parallel to ``b`` they coincide).  ``|a| = 1`` and ``|b| <= 1`` keep the
+    state bounded over long sequences."""
+    g = torch.Generator().manual_seed(seed)
+    shape = (batch, steps, heads, n)
+    x = torch.randn(shape, generator=g) - 0.5
+    w = torch.exp(-torch.exp(x))
+    r = torch.randn(shape, generator=g)
+    k = torch.randn(shape, generator=g)
+    v = torch.randn(shape, generator=g)
+    ka = torch.randn(shape, generator=g)
+    ka = ka / ka.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    kb = torch.randn(shape, generator=g)
+    kb = kb / kb.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    iclr = torch.sigmoid(torch.randn(shape, generator=g))
+    return tuple(t.to(dtype) for t in (r, w, k, v, -ka, kb * iclr))
+
+
+def wkv7_matrix_form(r, w, k, v, a, b, state=None):
+    """The recurrence as explicit matrices, in numpy float64: per step the
+    transition ``M_t = diag(w_t) + outer(a_t, b_t)`` is built and
+    ``S_t = S_{t-1} @ M_t + outer(v_t, k_t)``, ``y_t = S_t @ r_t``.  A second
+    formulation, sharing no code with :func:`wkv7_loop`.  Inputs as
+    :func:`wkv7_loop` (torch or numpy); returns numpy ``(y, S_T)``."""
+    import numpy as np
+
+    r, w, k, v, a, b = (np.asarray(x, dtype=np.float64) for x in (r, w, k, v, a, b))
+    bsz, steps, heads, n = r.shape
+    y = np.zeros_like(r)
+    s_out = np.zeros((bsz, heads, n, n))
+    for bi in range(bsz):
+        for h in range(heads):
+            s = np.zeros((n, n)) if state is None else np.asarray(state, dtype=np.float64)[bi, h].copy()
+            for t in range(steps):
+                m = np.diag(w[bi, t, h]) + np.outer(a[bi, t, h], b[bi, t, h])
+                s = s @ m + np.outer(v[bi, t, h], k[bi, t, h])
+                y[bi, t, h] = s @ r[bi, t, h]
+            s_out[bi, h] = s
+    return y, s_out
 
 
 def wkv7_autograd_grads(r, w, k, v, a, b, state, gy, gs=None):

@@ -25,6 +25,7 @@ only (no autograd through the state).
 from __future__ import annotations
 
 import ctypes
+import weakref
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Iterator
 
@@ -145,6 +146,15 @@ def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _need(t: Tensor | None, shape: tuple, name: str, dtype: torch.dtype = torch.float32) -> None:
+    """Raise unless ``t`` (if given) is a contiguous ``dtype`` tensor of ``shape``."""
+    if t is None:
+        return
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype or not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous {dtype} tensor of shape "
+                         f"{tuple(shape)}; got {t.dtype} {tuple(t.shape)}")
+
+
 def _row(pre: int, *, residual: Tensor, stream: int, ln: torch.nn.LayerNorm | None = None,
          mix: tuple[Tensor, ...] = (), prev_in: Tensor | None = None,
          prev_out: Tensor | None = None, outs: tuple[Tensor, ...] = (), ids: Tensor | None = None,
@@ -154,6 +164,25 @@ def _row(pre: int, *, residual: Tensor, stream: int, ln: torch.nn.LayerNorm | No
          mem_out: Tensor | None = None, lif=None) -> None:
     a = _lib.StepRowArgs()
     B, C = residual.shape
+    # Every tensor is handed to the kernel as a raw pointer: check that each
+    # one has the [B, C] row shape (or [C] / [vocab, C]) the kernel indexes.
+    for name, t in (("prev_in", prev_in), ("prev_out", prev_out), ("add", add), ("gate", gate),
+                    ("mem_in", mem_in), ("mem_out", mem_out)):
+        _need(t, (B, C), name)
+    for j, o in enumerate(outs):
+        _need(o, (B, C), f"out[{j}]")
+    for mod, name in ((ln, "ln"), (ln0, "ln0")):
+        if mod is not None:
+            _need(mod.weight, (C,), f"{name}.weight")
+            _need(mod.bias, (C,), f"{name}.bias")
+    for j, m in enumerate(mix):
+        if m.numel() != C or m.dtype != torch.float32:
+            raise ValueError(f"mixing vector {j} has {m.numel()} elements; the row has {C}")
+    if ids is not None:
+        _need(ids, (B,), "ids", torch.int64)
+        if embedding is None or embedding.ndim != 2 or embedding.shape[1] != C:
+            raise ValueError(f"embedding must be [vocab, {C}]")
+        _need(embedding, tuple(embedding.shape), "embedding")
     a.batch, a.channels = B, C
     a.residual = residual.data_ptr()
     if ids is not None:
@@ -198,6 +227,7 @@ class StepWorkspace:
     """Activation buffers of one step for batch ``B`` (reused every step)."""
 
     def __init__(self, B: int, C: int, hidden: int, vocab: int, device: torch.device) -> None:
+        self.dims = (B, C, hidden, vocab)
         f = dict(device=device, dtype=torch.float32)
         self.residual = torch.empty(B, C, **f)
         self.mixed = torch.empty(3, B, C, **f)    # k, v, r inputs (channel mix: k, r)
@@ -289,6 +319,7 @@ def model_step(model: "SpikeLanguageModel", ids: Tensor, src: Tensor, dst: Tenso
     (may be the same tensor), returns ``ws.logits`` [B, vocab]."""
     stream = torch.cuda.current_stream(ids.device).cuda_stream
     cfg = model.config
+    _check_workspace(model, ws, ids.shape[0], src, dst)
     blocks = list(model.blocks)
     L = len(blocks)
     first = blocks[0]
@@ -319,6 +350,12 @@ def block_step(block: "SpikeGPTBlock", inputs: Tensor, src: Tensor, dst: Tensor,
     """One block's step on its input ``inputs`` [B, C]; state slot rows
     ``src``/``dst`` [7, B, C]; returns the new residual (``ws.residual``)."""
     stream = torch.cuda.current_stream(inputs.device).cuda_stream
+    B, C = inputs.shape
+    if ws.dims[:3] != (B, C, block.ffn.key.out_features):
+        raise ValueError(f"step workspace sized for (B, C, hidden) = {ws.dims[:3]}; the block "
+                         f"and batch need {(B, C, block.ffn.key.out_features)}")
+    _need(src, (len(SLOTS), B, C), "state src")
+    _need(dst, (len(SLOTS), B, C), "state dst")
     ws.residual.copy_(inputs)
     _row(PRE_NONE, residual=ws.residual, stream=stream, ln0=block.ln0, ln=block.ln1,
          mix=_mixes(block.att), prev_in=src[_TPREV], prev_out=dst[_TPREV],
@@ -330,18 +367,37 @@ def block_step(block: "SpikeGPTBlock", inputs: Tensor, src: Tensor, dst: Tensor,
     return ws.residual
 
 
-_WS_CACHE: dict = {}
+def _model_dims(model: "SpikeLanguageModel", batch: int) -> tuple[int, int, int, int]:
+    cfg = model.config
+    return (batch, cfg.n_embd, model.blocks[0].ffn.key.out_features, cfg.vocab_size)
+
+
+def _check_workspace(model: "SpikeLanguageModel", ws: StepWorkspace, batch: int,
+                     src: Tensor, dst: Tensor) -> None:
+    """The workspace and the state buffers must have the model's sizes: the
+    kernels index them by the model's B and C."""
+    dims = _model_dims(model, batch)
+    if ws.dims != dims:
+        raise ValueError(f"step workspace sized for (B, C, hidden, vocab) = {ws.dims}; "
+                         f"the model and batch need {dims}")
+    want = (model.config.n_layer, len(SLOTS), batch, model.config.n_embd)
+    for name, t in (("src", src), ("dst", dst)):
+        _need(t, want, f"state {name}")
+
+
+# Step workspaces per live model (weak keys: a workspace never outlives its
+# model, and a new model never finds an old model's buffers).
+_WS_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 
 
 def workspace_for(model: "SpikeLanguageModel", batch: int, device: torch.device) -> StepWorkspace:
-    key = (id(model), batch, device)
-    ws = _WS_CACHE.get(key)
+    dims = _model_dims(model, batch)
+    key = (dims, torch.device(device))
+    per_model = _WS_CACHE.get(model)
+    ws = None if per_model is None else per_model.get(key)
     if ws is None:
-        cfg = model.config
-        ws = StepWorkspace(batch, cfg.n_embd, model.blocks[0].ffn.key.out_features,
-                           cfg.vocab_size, device)
-        _WS_CACHE.clear()
-        _WS_CACHE[key] = ws
+        ws = StepWorkspace(*dims, device)
+        _WS_CACHE[model] = {key: ws}  # one workspace per model (the last batch size)
     return ws
 
 

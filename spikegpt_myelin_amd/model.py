@@ -26,6 +26,7 @@ from dataclasses import dataclass
 
 import torch
 import torch.nn.functional as F
+import torch.utils.checkpoint
 from torch import Tensor, nn
 
 from . import generation
@@ -322,6 +323,7 @@ class SpikeLanguageModel(nn.Module):
         self.blocks = nn.ModuleList(SpikeGPTBlock(config, i) for i in range(config.n_layer))
         self.ln_out = nn.LayerNorm(config.n_embd)
         self.head = SplitKLinear(config.n_embd, config.vocab_size, bias=False)
+        self.gradient_checkpointing = config.gradient_checkpointing
         self.apply(self._init_weights)
 
     @staticmethod
@@ -350,10 +352,22 @@ class SpikeLanguageModel(nn.Module):
             )
         hidden = self.embed_tokens(input_ids)
         for block in self.blocks:
-            hidden = block(hidden)
+            hidden = self._run_block(block, hidden)
         if targets is None:
             return self.head(self.ln_out(hidden))
         return self.loss_tail(hidden, targets)
+
+    def set_gradient_checkpointing(self, enabled: bool = True) -> None:
+        """``language.py:1396-1399``: block-level activation checkpointing."""
+        self.gradient_checkpointing = enabled
+
+    def _run_block(self, block: nn.Module, hidden: Tensor) -> Tensor:
+        """``language.py:1401-1404``: with checkpointing on (training, grad
+        enabled), a block keeps only its input and is recomputed in the
+        backward; the HIP ops' autograd Functions recompute like any other."""
+        if self.gradient_checkpointing and self.training and torch.is_grad_enabled():
+            return torch.utils.checkpoint.checkpoint(block, hidden, use_reentrant=False)
+        return block(hidden)
 
     def loss_tail(self, hidden: Tensor, targets: Tensor) -> tuple[Tensor, Tensor]:
         """``language.py:1469-1480``: ``ln_out -> head -> cross_entropy``."""

@@ -69,11 +69,15 @@ def test_wkv7_forward_matches_oracle(dtype):
     r, w, k, v, a, b = O7.make_inputs(2, 48, 3, 64, seed=3, dtype=dtype)
     y, s = ops.wkv7_forward(*(x.to(DEV) for x in (r, w, k, v, a, b)), None)
     y_ref, s_ref = O7.wkv7_loop(*(x.double() for x in (r, w, k, v, a, b)))
-    assert y.dtype == dtype
-    tol = dict(rtol=1e-4, atol=1e-4) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
-    scale = float(y_ref.abs().max())
-    assert torch.allclose(y.double().cpu(), y_ref, rtol=tol["rtol"], atol=tol["atol"] * scale)
-    assert torch.allclose(s.double().cpu(), s_ref, rtol=tol["rtol"], atol=tol["atol"] * float(s_ref.abs().max()))
+    assert y.dtype == dtype and s.dtype == torch.float32
+    # y: the 16-bit bar (2e-2 relative, 1e-2 absolute) or, for fp32, 1e-5
+    # relative with a floor of 1e-5 * max|ref|; the fp32 state: the latter.
+    y_ref_scale = float(y_ref.abs().max())
+    if dtype == torch.float32:
+        assert torch.allclose(y.double().cpu(), y_ref, rtol=1e-5, atol=1e-5 * y_ref_scale)
+    else:
+        assert torch.allclose(y.double().cpu(), y_ref, rtol=2e-2, atol=1e-2)
+    assert torch.allclose(s.double().cpu(), s_ref, rtol=1e-5, atol=1e-5 * float(s_ref.abs().max()))
 
 
 def test_wkv7_state_carry_and_golden_fixture():
@@ -84,7 +88,7 @@ def test_wkv7_state_carry_and_golden_fixture():
     g = {n.split("__")[1]: torch.from_numpy(data[n]) for n in data.files}
     xs = [g[n].float().to(DEV) for n in ("r", "w", "k", "v", "a", "b")]
     y, s = ops.wkv7_forward(*xs, None)
-    assert torch.allclose(y.double().cpu(), g["y"], rtol=1e-4, atol=1e-4 * float(g["y"].abs().max()))
+    assert torch.allclose(y.double().cpu(), g["y"], rtol=1e-5, atol=1e-5 * float(g["y"].abs().max()))
     # split the sequence: run the first half, carry the state into the second
     y1, s1 = ops.wkv7_forward(*(x[:, :5] for x in xs), None)
     y2, s2 = ops.wkv7_forward(*(x[:, 5:] for x in xs), s1)

@@ -97,6 +97,45 @@ def test_loss_matches_oracle_recurrences(autocast, monkeypatch):
     assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
 
 
+@pytest.mark.parametrize("autocast,scale", [(True, 1.0), (False, 1.0), (True, 4.0)])
+def test_loss_matches_oracle_recurrences_at_41m_depth(autocast, scale, monkeypatch):
+    # The 41M configuration itself: 12 layers, 512 channels, byte vocabulary,
+    # random init (scale 1) and with the projection weights scaled up so that
+    # the LIFs fire more often (scale 4); B=2, T=512 keeps the CPU oracle's
+    # twelve layers of loops within seconds.
+    model = _model(n_layer=12, n_embd=512, vocab=256, ctx=1024, seed=3).to(DEV)
+    if scale != 1.0:
+        with torch.no_grad():
+            for p in model.parameters():
+                if p.ndim == 2:
+                    p.mul_(scale)
+    ids, tgt = (x.to(DEV) for x in _batch(2, 512, seed=11))
+    print(f"41M depth: autocast={autocast} scale={scale}", flush=True)
+    with torch.no_grad():
+        hip = _loss(model, ids, tgt, autocast, False, monkeypatch)
+        ref = _loss(model, ids, tgt, autocast, True, monkeypatch)
+    rel = abs(float(hip) - float(ref)) / abs(float(ref))
+    print(f"41M depth loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})")
+    assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
+
+
+def test_gradient_checkpointing_gives_the_same_loss_and_gradients():
+    # language.py:1396-1404: with checkpointing on, each block is recomputed
+    # in the backward; the kernels are deterministic, so every value matches.
+    model = _model(n_layer=3, n_embd=128).to(DEV)
+    twin = copy.deepcopy(model)
+    twin.set_gradient_checkpointing(True)
+    ids, tgt = (x.to(DEV) for x in _batch(4, 64, seed=13))
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss_a, _ = model(ids, tgt)
+        loss_b, _ = twin(ids, tgt)
+    loss_a.backward()
+    loss_b.backward()
+    assert torch.equal(loss_a, loss_b)
+    for (name, p), q in zip(model.named_parameters(), twin.parameters()):
+        assert torch.equal(p.grad, q.grad), name
+
+
 def test_gradients_match_oracle_recurrences(monkeypatch):
     model = _model(n_layer=2, n_embd=64).to(DEV)
     with torch.no_grad():

@@ -4,8 +4,11 @@ Tolerances (written per test):
 * fp32 I/O: elementwise ``rtol=1e-5`` with ``atol=1e-5 * max|ref|`` and a
   normwise relative error below 1e-5, against the float64 oracle evaluated on
   the same fp32 inputs;
-* bf16/fp16 I/O: ``rtol=2e-2, atol=1e-2`` against the float64 oracle on the
-  same (already rounded) 16-bit inputs;
+* bf16/fp16 I/O: ``rtol=2e-2`` with an absolute ``atol=1e-2`` against the
+  float64 oracle on the same (already rounded) 16-bit inputs, plus a normwise
+  relative error below 5e-3 (one bf16 rounding is at most 2^-8 = 3.9e-3) on
+  the 16-bit outputs y, gk, gv, and below 1e-4 on the fp32 batch sums
+  gtd, gtf (fp32 accumulation over B*T terms);
 * the 16-bit-I/O op must equal the fp32 op's output rounded to the 16-bit
   type bit for bit whenever both use the same tile configuration (the
   widening is exact and both round once at the store).
@@ -32,19 +35,25 @@ def _lib_ops():
     return torch.ops.myelin
 
 
-def _close(got, ref, *, rtol, atol_scale, norm_tol=None, what=""):
-    """allclose with ``atol = atol_scale * max(max|ref|, 1)``: the inputs are
-    O(1), so a reference that is exactly zero (gk at T=1) is compared on the
-    problem's natural unit scale rather than on zero."""
+def _close(got, ref, *, rtol, atol=None, atol_scale=None, norm_tol=None, what=""):
+    """allclose with an absolute ``atol``, or with ``atol = atol_scale *
+    max(max|ref|, 1)`` (fp32: the inputs are O(1), so a reference that is
+    exactly zero, gk at T=1, is compared on the problem's natural unit scale
+    rather than on zero), plus an optional normwise relative bound.  The
+    errors are printed (pytest shows them with -s or on failure)."""
     got = got.double().cpu()
     ref = ref.double().cpu()
     scale = float(ref.abs().max()) if ref.numel() else 0.0
-    atol = atol_scale * max(scale, 1.0)
+    if atol is None:
+        atol = atol_scale * max(scale, 1.0)
     ok = torch.allclose(got, ref, rtol=rtol, atol=atol)
     err = (got - ref).abs().max().item() if ref.numel() else 0.0
-    assert ok, f"{what}: max abs err {err:.3e} (atol {atol:.3e}, rtol {rtol})"
-    if norm_tol is not None and ref.numel() and float(ref.norm()) > 0.0:
+    rel = 0.0
+    if ref.numel() and float(ref.norm()) > 0.0:
         rel = ((got - ref).norm() / ref.norm()).item()
+    print(f"{what}: max abs err {err:.3e} (max|ref| {scale:.3e}), normwise rel err {rel:.3e}")
+    assert ok, f"{what}: max abs err {err:.3e} (atol {atol:.3e}, rtol {rtol})"
+    if norm_tol is not None:
         assert rel < norm_tol, f"{what}: normwise rel err {rel:.3e} >= {norm_tol}"
 
 
@@ -79,7 +88,14 @@ def _oracle64_fast(k, v, td, tf, gy):
 
 
 FP32_TOL = dict(rtol=1e-5, atol_scale=1e-5, norm_tol=1e-5)
-BF16_TOL = dict(rtol=2e-2, atol_scale=1e-2)
+# The stated 16-bit bar, literally: 2e-2 relative, 1e-2 absolute.
+BF16_TOL = dict(rtol=2e-2, atol=1e-2, norm_tol=5e-3)
+BF16_PARAM_TOL = dict(rtol=2e-2, atol=1e-2, norm_tol=1e-4)
+
+
+def _bf16_tol(name):
+    """16-bit outputs (y, gk, gv) or fp32 batch-summed parameter gradients."""
+    return BF16_PARAM_TOL if name in ("gtd", "gtf") else BF16_TOL
 
 
 @pytest.mark.parametrize("steps", [1, 7, 64])
@@ -142,7 +158,7 @@ def test_16bit_io_op_matches_oracle(dtype, b, t, c, seed):
     assert got[0].dtype == dtype and got[1].dtype == dtype and got[3].dtype == torch.float32
     ref = _oracle64(k, v, td, tf, gy)
     for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
-        _close(g, r, what=f"{dtype} {(b, t, c)} {name}", **BF16_TOL)
+        _close(g, r, what=f"{dtype} {(b, t, c)} {name}", **_bf16_tol(name))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -188,15 +204,8 @@ def test_bf16_benchmark_shape_full_size():
     torch.cuda.synchronize()
     ref = _oracle64_fast(k, v, td, tf, gy)
     for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
-        _close(g, r, what=f"full {name}", **BF16_TOL)
-    # Per lane: sum_t gk = 0 and sum_t gv = sum_t gy exactly in real
-    # arithmetic; each bf16 output carries a relative rounding error <= 2^-8,
-    # which bounds the residual by 2^-8 * sum_t |g|.
-    gk64, gv64 = gk.double().cpu(), gv.double().cpu()
-    bound_k = gk64.abs().sum(1) * 2.0**-8 + 1e-6
-    bound_v = gv64.abs().sum(1) * 2.0**-8 + 1e-6
-    assert bool((gk64.sum(1).abs() <= bound_k).all())
-    assert bool(((gv64.sum(1) - gy.double().sum(1)).abs() <= bound_v).all())
+        _close(g, r, what=f"full {name}", **_bf16_tol(name))
+    _lane_invariants(gk, gv, gy, "headline")
 
 
 def test_long_context_shape_against_oracle():
@@ -208,7 +217,45 @@ def test_long_context_shape_against_oracle():
     gk, gv, gtd, gtf = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
     ref = _oracle64_fast(k, v, td, tf, gy)
     for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
-        _close(g, r, what=f"T=3072 {name}", **BF16_TOL)
+        _close(g, r, what=f"T=3072 {name}", **_bf16_tol(name))
+
+
+def _lane_invariants(gk, gv, gy, what):
+    """Per lane: sum_t gk = 0 and sum_t gv = sum_t gy exactly in real
+    arithmetic; each 16-bit output carries a relative rounding error <= 2^-8,
+    which bounds the residual by 2^-8 * sum_t |g|."""
+    gk64, gv64 = gk.double().cpu(), gv.double().cpu()
+    bound_k = gk64.abs().sum(1) * 2.0**-8 + 1e-6
+    bound_v = gv64.abs().sum(1) * 2.0**-8 + 1e-6
+    assert bool((gk64.sum(1).abs() <= bound_k).all()), f"{what}: sum_t gk != 0"
+    assert bool(((gv64.sum(1) - gy.double().cpu().sum(1)).abs() <= bound_v).all()), \
+        f"{what}: sum_t gv != sum_t gy"
+
+
+def test_216m_shape_full_size():
+    # B=16, T=1024, C=768 bf16 (one layer of the 216M-class model,
+    # language.py:292-298): the standalone ops and the training path
+    # (checkpointed forward, single-sweep backward) against the fp64 oracle
+    # on every lane, and the per-lane gradient invariants.  At this width a
+    # lane holds one channel (16 rows of 768 channels give 192 workgroups).
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    ops = _lib_ops()
+    b, t, c = 16, 1024, 768
+    print(f"216M shape B={b} T={t} C={c} bf16", flush=True)
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=3, dtype=torch.bfloat16)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
+    gk, gv, gtd, gtf = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
+    train = _grads(weighted_key_value_hip_bf16io, kd, vd, tdd, tfd, gyd)
+    torch.cuda.synchronize()
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip((y, gk, gv, gtd, gtf), ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"216m ops {name}", **_bf16_tol(name))
+    for g, r, name in zip(train, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"216m training path {name}", **_bf16_tol(name))
+    _lane_invariants(gk, gv, gy, "216m ops")
+    _lane_invariants(train[1], train[2], gy, "216m training path")
 
 
 @pytest.mark.parametrize("kind", ["wide_keys", "large_time_first", "one_bad_channel"])
@@ -301,13 +348,13 @@ def test_all_tile_configurations_agree(monkeypatch):
         y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
         g = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
         for got, r, name in zip((y, *g), ref, ("y", "gk", "gv", "gtd", "gtf")):
-            _close(got, r, what=f"cfg {fc}/{bc} {name}", **BF16_TOL)
+            _close(got, r, what=f"cfg {fc}/{bc} {name}", **_bf16_tol(name))
         # training path: forward records -> single-sweep backward
         from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
 
         got = _grads(weighted_key_value_hip_bf16io, kd, vd, tdd, tfd, gyd)
         for g2, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
-            _close(g2, r, what=f"autograd cfg {fc}/{bc} {name}", **BF16_TOL)
+            _close(g2, r, what=f"autograd cfg {fc}/{bc} {name}", **_bf16_tol(name))
 
 
 def test_compiles_without_graph_breaks():
@@ -332,10 +379,11 @@ def test_language_entry_point_dispatch_and_validation():
         weighted_key_value(kd, vd[..., :16], tdd, tfd)
 
 
-@pytest.mark.skip(reason="host segfault inside torch.cuda.graph capture_end when the op path is "
-                         "captured (library built by ROCm 7.2 hipcc, code object v6, loaded by "
-                         "torch's ROCm 7.0 runtime); cause not yet shown, so the case stays off "
-                         "the GPU until it is")
+@pytest.mark.skip(reason="host segfault (exit 139) inside torch.cuda.graph capture_end when the "
+                         "op path's forward and autograd backward are captured together; the "
+                         "whole-model step graph of the same library captures and replays "
+                         "correctly, so the code object is not the cause, and no cause in this "
+                         "repository's code has been shown, so the case stays off the GPU")
 def test_graph_capture_replays_match_eager():
     # The C ABI never allocates, synchronises or memsets, so the op path can
     # be captured in a HIP graph.  Replay several times with eager work and
@@ -368,14 +416,15 @@ def test_graph_capture_replays_match_eager():
         del junk
 
 
-@pytest.mark.parametrize("kdt,vdt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
-                                     (torch.bfloat16, torch.float32)])
-def test_eager_path_equals_op_path(kdt, vdt):
+@pytest.mark.parametrize("kdt,vdt,shape", [
+    (torch.bfloat16, torch.bfloat16, (2, 150, 192)), (torch.float32, torch.float32, (2, 150, 192)),
+    (torch.bfloat16, torch.float32, (2, 150, 192)), (torch.bfloat16, torch.bfloat16, (4, 300, 768))])
+def test_eager_path_equals_op_path(kdt, vdt, shape):
     # Eager calls on GPU tensors run an autograd.Function over the launchers;
     # traced calls run the private custom ops.  Same kernels, same values.
     from spikegpt_myelin_amd import weighted_key_value_hip
 
-    k, v, td, tf, gy = O.make_inputs(2, 150, 192, seed=21, dtype=torch.float32)
+    k, v, td, tf, gy = O.make_inputs(*shape, seed=21, dtype=torch.float32)
     kd, vd = k.to(kdt).to(DEV), v.to(vdt).to(DEV)
     tdd, tfd, gyd = td.to(DEV), tf.to(DEV), gy.to(kdt).to(DEV)
 

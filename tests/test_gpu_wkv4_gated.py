@@ -54,8 +54,11 @@ def test_equals_the_separate_ops(dtype, b, t, c):
         assert torch.equal(a, e), f"{name} differs from the separate ops"
 
 
-def test_headline_shape_equals_the_separate_ops():
-    xs = _inputs(64, 1024, 512, seed=5, dtype=torch.bfloat16)
+@pytest.mark.parametrize("b,t,c", [(64, 1024, 512), (16, 1024, 768)])
+def test_headline_shape_equals_the_separate_ops(b, t, c):
+    # The 41M and 216M layer shapes.
+    print(f"gated wkv bf16 B={b} T={t} C={c}", flush=True)
+    xs = _inputs(b, t, c, seed=5, dtype=torch.bfloat16)
     fused = _run(weighted_key_value_gated, *xs)
     plain = _run(_unfused, *xs)
     for name, a, e in zip(NAMES, fused, plain):
@@ -81,10 +84,18 @@ def test_matches_the_float64_oracle():
     leaves = [x.double().requires_grad_(True) for x in (k, v, td, tf, r)]
     y = torch.sigmoid(leaves[4]) * O.wkv_loop(*leaves[:4])
     ref = (y, *torch.autograd.grad(y, leaves, gy.double()))
+    # The stated 16-bit bar: 2e-2 relative, 1e-2 absolute; plus a normwise
+    # bound of 5e-3 (one bf16 rounding is at most 2^-8 = 3.9e-3).  This holds
+    # for the fp32 parameter gradients too: the recurrence's incoming gradient
+    # is round(g * sigmoid(r)) in bf16, as the separate gate op hands it to
+    # the WKV backward, so they carry one bf16 rounding (measured 1.7e-3).
     for name, a, e in zip(NAMES, got, ref):
-        a = a.detach().double().cpu()
-        scale = max(float(e.abs().max()), 1e-30)
-        assert torch.allclose(a, e.detach(), rtol=2e-2, atol=1e-2 * scale), name
+        a, e = a.detach().double().cpu(), e.detach()
+        err = float((a - e).abs().max())
+        rel = float((a - e).norm() / e.norm())
+        print(f"gated vs oracle {name}: max abs err {err:.3e}, normwise {rel:.3e}")
+        assert torch.allclose(a, e, rtol=2e-2, atol=1e-2), f"{name}: max abs err {err:.3e}"
+        assert rel < 5e-3, f"{name}: normwise rel err {rel:.3e}"
 
 
 def test_opcheck():

@@ -26,8 +26,12 @@ def _ops():
     return torch.ops.myelin
 
 
-def _case(b, t, h, seed, dtype, with_state):
-    xs = O7.make_inputs(b, t, h, 64, seed=seed, dtype=dtype)
+def _case(b, t, h, seed, dtype, with_state, general=False):
+    """Inputs of the benchmark distributions (a = -kappa, b = kappa * iclr,
+    parallel) or, with ``general``, a and b along independent directions, for
+    which (S a) b^T and (S b) a^T differ."""
+    make = O7.make_general_inputs if general else O7.make_inputs
+    xs = make(b, t, h, 64, seed=seed, dtype=dtype)
     g = torch.Generator().manual_seed(1000 + seed)
     s0 = 0.5 * torch.randn(b, h, 64, 64, generator=g) if with_state else None
     gy = torch.randn(b, t, h, 64, generator=g).to(dtype)
@@ -35,20 +39,35 @@ def _case(b, t, h, seed, dtype, with_state):
     return xs, s0, gy, gs
 
 
-def _tol(dtype):
-    # fp32 I/O: the kernel's fp32 state against fp64 over the sequence;
-    # 16-bit I/O: the documented 2e-2 relative / 1e-2 absolute bar, the
-    # absolute part scaled by the tensor's magnitude.
-    return (1e-4, 1e-4) if dtype == torch.float32 else (2e-2, 1e-2)
+# Tolerances.  16-bit outputs: the stated bar, 2e-2 relative with an
+# absolute 1e-2, and a normwise relative error below 5e-3 (one bf16 rounding
+# is at most 2^-8 = 3.9e-3).  fp32 outputs (every output of the fp32 op, and
+# the fp32 final state and its gradient of the 16-bit ops): FP32_RTOL relative
+# with a floor of FP32_RTOL * max|ref|, and a normwise bound of FP32_RTOL.
+# Measured on MI355X against the fp64 oracle (B=1, H=4, both input
+# families): max error / max|ref| and normwise error of every output stay at
+# 0.5-1.5e-7 for T = 16, 64, 256 and 1024 (no growth over T: the decays w < 1
+# and the low-rank term with |a| |b| <= 1 keep the state contractive), so the
+# stated 1e-5 holds with two orders of magnitude to spare.
+FP32_RTOL = 1e-5
 
 
 def _close(got, exp, dtype, name):
-    rtol, atol = _tol(dtype)
+    fp32_out = got.dtype == torch.float32
     got = got.detach().double().cpu()
+    exp = exp.detach().double().cpu()
     scale = max(float(exp.abs().max()), 1e-30)
-    ok = torch.allclose(got, exp, rtol=rtol, atol=atol * scale)
-    err = float((got - exp).abs().max()) / scale
-    assert ok, f"{name}: max abs err / max|ref| = {err:.3e}"
+    err = float((got - exp).abs().max())
+    rel = float((got - exp).norm() / exp.norm()) if float(exp.norm()) > 0 else err
+    print(f"{name} ({dtype}): max abs err {err:.3e}, max|ref| {scale:.3e}, normwise {rel:.3e}")
+    if fp32_out:
+        ok = torch.allclose(got, exp, rtol=FP32_RTOL, atol=FP32_RTOL * scale)
+        assert ok, f"{name}: max abs err / max|ref| = {err / scale:.3e}"
+        assert rel < FP32_RTOL, f"{name}: normwise rel err {rel:.3e}"
+    else:
+        ok = torch.allclose(got, exp, rtol=2e-2, atol=1e-2)
+        assert ok, f"{name}: max abs err {err:.3e} (max|ref| {scale:.3e})"
+        assert rel < 5e-3, f"{name}: normwise rel err {rel:.3e}"
 
 
 def _reference(xs, s0, gy, gs):
@@ -79,6 +98,30 @@ def test_autograd_matches_oracle(dtype, t):
         _close(g, e, dtype, name)
     if with_state:
         _close(got[6], ref[8], dtype, "ds0")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("t", [7, 17, 40])
+def test_independent_a_b_autograd_matches_oracle(dtype, t):
+    # a and b along independent directions: a b^T is not symmetric, so an
+    # (S b) a^T in place of (S a) b^T (or the matching transposes in the
+    # backward) would show in every output.
+    ops = _ops()
+    print(f"wkv7 general a,b {dtype} T={t}", flush=True)
+    xs, s0, gy, gs = _case(2, t, 3, seed=50 + t, dtype=dtype, with_state=True, general=True)
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    sd = s0.to(DEV).requires_grad_(True)
+    y, s = ops.wkv7_forward(*leaves, sd)
+    got = torch.autograd.grad([y, s], leaves + [sd], [gy.to(DEV), gs.to(DEV)])
+    ref = _reference(xs, s0, gy, gs)
+    _close(y, ref[0], dtype, "y")
+    _close(s, ref[1], dtype, "s")
+    for name, g, e in zip((*NAMES, "ds0"), got, ref[2:]):
+        _close(g, e, dtype, name)
+    # the standalone backward (records computed inside) gives the same
+    out = ops.wkv7_backward(*(x.to(DEV) for x in xs), s0.to(DEV), gy.to(DEV), gs.to(DEV))
+    for name, g, e in zip((*NAMES, "ds0"), out, ref[2:]):
+        _close(g, e, dtype, f"standalone {name}")
 
 
 @pytest.mark.parametrize("b,h", [(1, 1), (1, 3), (3, 5)])
@@ -168,13 +211,16 @@ def test_golden_fixture_gradients():
         _close(got, g[name], torch.float32, name)
 
 
-def test_benchmark_shape_full_size():
+@pytest.mark.parametrize("general", [False, True])
+def test_benchmark_shape_full_size(general):
     # B=16, T=1024, H=12 bf16 (the RWKV-7 benchmark configuration): every
     # (batch, head) is independent, so the first two batch rows are compared
-    # with the oracle run on those rows alone.
+    # with the oracle run on those rows alone.  Also with a, b independent.
     ops = _ops()
     b, t, h = 16, 1024, 12
-    xs = O7.make_inputs(b, t, h, 64, seed=4, dtype=torch.bfloat16)
+    make = O7.make_general_inputs if general else O7.make_inputs
+    print(f"wkv7 full size general={general}", flush=True)
+    xs = make(b, t, h, 64, seed=4, dtype=torch.bfloat16)
     gy = torch.randn(b, t, h, 64, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
     leaves = [x.to(DEV).requires_grad_(True) for x in xs]
     y, _ = ops.wkv7_forward(*leaves, None)
