@@ -84,6 +84,26 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
                   void* workspace, size_t workspace_bytes, int64_t B, int64_t T, int64_t C,
                   int dtype, void* stream);
 
+/* Fixed scratch behind wkv4_backward_noalloc, per GPU: 16 MiB. */
+#define WKV4_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* wkv4_backward without a workspace argument and without any allocation.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, kernels and results as wkv4_backward,
+ * with the workspace taken from a fixed device array of
+ * WKV4_NOALLOC_SCRATCH_BYTES per GPU (the library looks its address up once
+ * per device and never frees it).  Sizes whose wkv4_backward_workspace_bytes
+ * exceed that maximum are rejected with WKV_ERR_WORKSPACE_TOO_SMALL.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from different threads) race and must be serialised
+ * by the caller.  The stream must belong to the current device. */
+int wkv4_backward_noalloc(const void* grad_y, const float* w, const float* u, const void* k,
+                          const void* v, void* grad_k, void* grad_v, float* grad_time_decay,
+                          float* grad_time_first, int64_t B, int64_t T, int64_t C, int dtype,
+                          void* stream);
+
 /* Bytes of device workspace wkv4_backward_checkpointed needs (per-batch
  * parameter-gradient partials, 2*B*C fp32). */
 size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t C);

@@ -60,6 +60,10 @@ SIGNATURES = {
         _INT,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P],
     ),
+    "wkv4_backward_noalloc": (
+        _INT,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P],
+    ),
     "wkv4_checkpoint_bytes": (_SZ, [_I64, _I64, _I64]),
     "wkv4_forward_checkpointed": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_checkpointed_workspace_bytes": (_SZ, [_I64, _I64]),

@@ -6,8 +6,10 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <cmath>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "../../include/wkv_hip.h"
@@ -148,6 +150,42 @@ static bool dims_ok(int64_t B, int64_t T, int64_t C) {
   return B >= 0 && T >= 0 && C >= 0 && B < lim && T < lim && C < lim && B * T < lim * 64;
 }
 
+// Fixed scratch of wkv4_backward_noalloc (checkpoint records, then the
+// per-batch parameter-gradient partials).  Every GPU the library runs on holds
+// its own copy until the process ends.  On the host this name is only a
+// stand-in for the symbol: kernels get the device address that
+// hipGetSymbolAddress returns for the current device (scratch_address below).
+static __device__ __align__(256) unsigned char scratch[WKV4_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+static int scratch_address(void** out, const char* what) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(WKV_ERR_LAUNCH, std::string(what) + ": hipGetDevice: " + hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(WKV_ERR_INVALID_ARGUMENT, std::string(what) + ": device index out of range");
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || p == nullptr)
+        return fail(WKV_ERR_LAUNCH, std::string(what) + ": hipGetSymbolAddress(scratch): " +
+                                        hipGetErrorString(err));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return WKV_OK;
+}
+
 }  // namespace wkv_host
 
 using namespace wkv_host;
@@ -222,6 +260,42 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
                 "wkv4_backward: grad_y, k, v, grad_k, grad_v, workspace must be 16-byte aligned");
   return wkv4_backward_impl(grad_y, w, u, k, v, grad_k, grad_v, grad_time_decay, grad_time_first,
                             static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
+}
+
+int wkv4_backward_noalloc(const void* grad_y, const float* w, const float* u, const void* k,
+                          const void* v, void* grad_k, void* grad_v, float* grad_time_decay,
+                          float* grad_time_first, int64_t B, int64_t T, int64_t C, int dtype,
+                          void* stream) {
+  set_error("");
+  TimingScope timing;
+  if (!dtype_ok(dtype))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_noalloc: unknown dtype");
+  if (!dims_ok(B, T, C))
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_noalloc: bad sizes");
+  if (C == 0) return WKV_OK;
+  // Checked before any pointer is looked at.  Records and partials are
+  // written in full before they are read, so the scratch needs no clearing
+  // between calls.
+  const size_t need = wkv4_bwd_workspace_bytes_impl(B, T, C, dtype);
+  if (need > size_t(WKV4_NOALLOC_SCRATCH_BYTES))
+    return fail(WKV_ERR_WORKSPACE_TOO_SMALL,
+                "wkv4_backward_noalloc: these sizes need " + std::to_string(need) +
+                    " bytes of scratch, above the fixed maximum of " +
+                    std::to_string(size_t(WKV4_NOALLOC_SCRATCH_BYTES)) +
+                    " (use wkv4_backward with a workspace)");
+  if (!grad_time_decay || !grad_time_first)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_noalloc: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0 || T == 0) return wkv4_zero_param_grads(grad_time_decay, grad_time_first, int(C), s);
+  if (!grad_y || !w || !u || !k || !v || !grad_k || !grad_v)
+    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward_noalloc: null pointer");
+  if (!aligned16({grad_y, k, v, grad_k, grad_v}))
+    return fail(WKV_ERR_INVALID_ARGUMENT,
+                "wkv4_backward_noalloc: grad_y, k, v, grad_k, grad_v must be 16-byte aligned");
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws, "wkv4_backward_noalloc")) return rc;
+  return wkv4_backward_impl(grad_y, w, u, k, v, grad_k, grad_v, grad_time_decay, grad_time_first,
+                            static_cast<float*>(ws), int(B), int(T), int(C), dtype, s);
 }
 
 size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t C) {

@@ -125,3 +125,18 @@ def test_block_step_argument_errors(lib):
     assert lib.block_step_row(1, ctypes.byref(a), None) == 0  # empty batch: no-op
     assert lib.block_step_wkv(*([None] * 12), 2, 8, None) == 1
     assert lib.block_step_wkv(*([None] * 12), 0, 8, None) == 0
+
+
+def test_noalloc_backward_rejects_sizes_beyond_its_scratch(lib):
+    # Rejected on the host before any pointer is read: 3 fp32 records per
+    # channel per 64 steps at B=64, T=4096, C=512 are 25 MB > 16 MiB.
+    rc = lib.wkv4_backward_noalloc(None, None, None, None, None, None, None, None, None,
+                                   64, 4096, 512, 1, None)
+    assert rc == 3
+    msg = lib.wkv_last_error_string()
+    assert b"scratch" in msg and str(16 << 20).encode() in msg
+    # Within the maximum, the null pointers are what is rejected.
+    rc = lib.wkv4_backward_noalloc(None, None, None, None, None, None, None, None, None,
+                                   64, 1024, 512, 1, None)
+    assert rc == 1 and b"null" in lib.wkv_last_error_string()
+    assert lib.wkv4_backward_workspace_bytes(64, 1024, 512, 1) <= 16 << 20
