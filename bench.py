@@ -12,15 +12,15 @@ throughput; the same work through the torch.library op path (dispatch,
 allocation and autograd on every call) is reported as ``op_ms_per_step``.
 
 Reported beside the throughput:
-* ``roofline`` -- the dominant launch (the backward: the reverse-sweep kernel
-  plus the small batch-sum kernel), timed on every 10th step of the timed
-  region (``--event-every``) with HIP events bound to its first and last
-  kernel dispatch (``wkv_time_next_call``: the kernels' own start and end
-  timestamps on the launch stream, no marker packets); algorithmic bytes = 10 B per [B,T,C]
-  element (k, v, dy read, dk, dv written); peak 8 TB/s.  ``traffic`` comes
-  from the committed rocprofv3 PMC
-  summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters
-  on a copy of known size) when present, else null.
+* ``roofline`` -- the dominant kernel (the backward's reverse sweep,
+  ``wkv4_bwd_kernel``, or ``wkv4_bwd_split_kernel`` for few rows), timed
+  alone on every 10th step of the timed region (``--event-every``) with HIP
+  events bound to its own dispatch (``wkv_time_next_kernel``: the kernel's
+  start and end timestamps on the launch stream, no marker packets);
+  algorithmic bytes = 10 B per [B,T,C] element (k, v, dy read, dk, dv
+  written); peak 8 TB/s.  ``traffic`` comes from the committed rocprofv3 PMC
+  summary of that kernel (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the
+  same counters on a copy of known size) when present, else null.
 * ``cpu_baseline`` -- the reference's CPU WKV path restated in eager PyTorch
   (the sequential loop of src/spikegpt/language.py:399-449 in fp32, backward
   by autograd) on a bounded sample of the same workload, on this host's cores.
@@ -102,7 +102,7 @@ def cpu_baseline(B: int, T: int, C: int, sample_batch: int, fwd_only: bool = Fal
         once()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    return {
+    out = {
         "value": bs * T / med,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
@@ -111,6 +111,35 @@ def cpu_baseline(B: int, T: int, C: int, sample_batch: int, fwd_only: bool = Fal
                    f"{'forward' if fwd_only else 'forward+autograd backward'}, "
                    f"median of {len(times)} after 1 warmup; host {_cpu_model()}, "
                    f"os.cpu_count()={os.cpu_count()}"),
+    }
+    out["secondary"] = associative_scan_baseline(B, T, C)
+    return out
+
+
+def associative_scan_baseline(B: int, T: int, C: int, sample_batch: int = 64) -> dict:
+    """The reference's default CPU path, ``weighted_key_value``
+    (src/spikegpt/language.py:452-527: torch associative_scan over the
+    log-space monoid, generic combine mode), forward only, fp32."""
+    from oracle import wkv4 as O
+
+    bs = min(B, sample_batch)
+    k, v, td, tf, _ = O.make_inputs(bs, T, C, seed=0, dtype=torch.bfloat16)
+    k, v = k.float(), v.float()
+    with torch.no_grad():
+        O.wkv_associative_scan(k, v, td, tf)  # warmup
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.wkv_associative_scan(k, v, td, tf)
+            times.append(time.perf_counter() - t0)
+    return {
+        "value": bs * T / statistics.median(times),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"B={bs} of {B}, T={T}, C={C}, fp32, torch associative_scan (generic "
+                   "combine) forward only, median of 3 after 1 warmup; autograd unverified "
+                   "on torch < 2.13 (this image: torch " + torch.__version__.split("+")[0] + ")"),
     }
 
 
@@ -165,20 +194,27 @@ def bench_wkv4(args, cfg) -> dict:
     gk, gv = torch.empty_like(k), torch.empty_like(k)
     gtd = torch.empty(C, dtype=torch.float32, device=dev)
     gtf = torch.empty(C, dtype=torch.float32, device=dev)
-    ws = torch.empty(2 * B * C, dtype=torch.float32, device=dev)
+    # Workspaces: the split-over-time kernels' carries (few rows) and the
+    # backward's parameter-gradient partials.
+    fws_bytes = int(lib.wkv4_forward_workspace_bytes(B, T, C))
+    fws = torch.empty(max(fws_bytes, 16), dtype=torch.uint8, device=dev)
+    bws_bytes = int(lib.wkv4_backward_checkpointed_workspace_bytes(B, T, C))
+    ws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
+    split = fws_bytes > 0
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
 
     def fwd():
         _lib.check(lib.wkv4_forward_checkpointed(k.data_ptr(), v.data_ptr(), td.data_ptr(),
                                                  tf.data_ptr(), y.data_ptr(), ck.data_ptr(),
+                                                 fws.data_ptr() if split else None, fws_bytes,
                                                  B, T, C, code, sp), "forward")
 
     def bwd():
         _lib.check(lib.wkv4_backward_checkpointed(dy.data_ptr(), td.data_ptr(), tf.data_ptr(),
                                                   k.data_ptr(), v.data_ptr(), ck.data_ptr(),
                                                   gk.data_ptr(), gv.data_ptr(), gtd.data_ptr(),
-                                                  gtf.data_ptr(), ws.data_ptr(), ws.numel() * 4,
+                                                  gtf.data_ptr(), ws.data_ptr(), bws_bytes,
                                                   B, T, C, code, sp), "backward")
 
     # The same work through the drop-in op path (torch.library dispatch,
@@ -205,12 +241,17 @@ def bench_wkv4(args, cfg) -> dict:
     op_step_s = (time.perf_counter() - t0) / args.steps
 
     dom_name = "fwd" if fwd_only else "bwd"
+    # The dominant kernel: the reverse sweep of the backward (the forward for
+    # a forward-only workload), the launch's first dispatch, or its second
+    # after the fill of the split kernels' carry words.
+    dom_index = 1 if split else 0
     pool = EventPool(4 * args.steps * layers, stream)
 
-    def step(events=None, timed=(dom_name,)):
+    def step(events=None, timed=(dom_name,), kernel=None):
         # The launches named in `timed` carry HIP events on their first and
-        # last kernel dispatch (kernel start/end timestamps; the stream gets
-        # no marker packets, so the timed step is not perturbed).
+        # last kernel dispatch, or on their `kernel`-th dispatch alone (kernel
+        # start/end timestamps; the stream gets no marker packets, so the
+        # timed step is not perturbed).
         for _ in range(layers):
             for name, fn in (("fwd", fwd),) if fwd_only else (("fwd", fwd), ("bwd", bwd)):
                 if events is None or name not in timed:
@@ -218,7 +259,7 @@ def bench_wkv4(args, cfg) -> dict:
                     continue
                 s_ev = pool.take()
                 e_ev = pool.take()
-                _lib.arm_events(s_ev, e_ev)
+                _lib.arm_events(s_ev, e_ev, kernel)
                 fn()
                 events.append((name, s_ev, e_ev))
 
@@ -231,7 +272,7 @@ def bench_wkv4(args, cfg) -> dict:
     for i in range(args.steps):
         # A timed launch is fenced for its events; every `event_every`-th step
         # carries them so that the other steps run undisturbed.
-        step(events if i % args.event_every == 0 else None)
+        step(events if i % args.event_every == 0 else None, kernel=dom_index)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     step_s = elapsed / args.steps
@@ -281,21 +322,22 @@ def bench_wkv4(args, cfg) -> dict:
     }
     dom_t = statistics.mean(per[dom_name])
     if fwd_only:
-        dom, dom_bytes, launch_kernels = "wkv4_fwd_kernel", 3 * esize * B * T * C, ["wkv4_fwd_kernel"]
+        dom = "wkv4_fwd_split_kernel" if split else "wkv4_fwd_kernel"
+        dom_bytes = 3 * esize * B * T * C
+        entry = "wkv4_forward_checkpointed"
     else:
         out["bwd_launch_us"] = bwd_s * 1e6
-        dom, dom_bytes = "wkv4_bwd_kernel", 5 * esize * B * T * C
-        launch_kernels = ["wkv4_bwd_kernel", "wkv4_param_grad_kernel"]
+        dom = "wkv4_bwd_split_kernel" if split else "wkv4_bwd_kernel"
+        dom_bytes = 5 * esize * B * T * C
+        entry = "wkv4_backward_checkpointed"
     achieved = dom_bytes / dom_t / 1e9
     traffic_file = ROOT / "profiles" / f"{cfg['slug']}_pmc.md"
-    parts = [read_traffic(traffic_file, kname) for kname in launch_kernels]
-    traffic = sum(parts) if all(p is not None for p in parts) else None
+    traffic = read_traffic(traffic_file, dom)
     out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
                        "algorithmic_bytes_per_launch": dom_bytes,
                        "avg_launch_us": dom_t * 1e6,
-                       "launch": ("wkv4_backward_checkpointed: " if not fwd_only
-                                  else "wkv4_forward_checkpointed: ") + " + ".join(launch_kernels),
+                       "launch": f"{entry}, dispatch {dom_index} ({dom}) timed alone",
                        "traffic_source": (str(traffic_file.relative_to(ROOT))
                                           if traffic is not None else None)}
     if not args.no_cpu_baseline:

@@ -37,6 +37,14 @@ enum wkv_status {
   WKV_ERR_WORKSPACE_TOO_SMALL = 3
 };
 
+/* Bytes of device workspace the RWKV-4 forward entry points can use for
+ * these sizes: nonzero when fewer rows of 64 channels (B * ceil(C / 64))
+ * than the GPU has CUs would leave it idle, and the sequence is then split
+ * over workgroups that exchange their carries through the workspace; 0 when
+ * the one-row-per-workgroup kernel runs.  Any workspace passed is filled by
+ * the call itself (no clearing needed). */
+size_t wkv4_forward_workspace_bytes(int64_t B, int64_t T, int64_t C);
+
 /* RWKV-4 / SpikeGPT WKV forward.
  *
  * Replaces the kernel launch inside myelin::wkv_forward
@@ -45,9 +53,12 @@ enum wkv_status {
  * with fp32 recurrence state.  Unlike the Triton kernel (which takes the
  * transformed w = -exp(time_decay) computed by the host wrapper), this entry
  * point takes the raw fp32 time_decay [C] and time_first [C] and applies
- * w = -exp(time_decay) itself, saving the wrapper's extra launch. */
+ * w = -exp(time_decay) itself, saving the wrapper's extra launch.
+ * `workspace` (NULL allowed: then the one-row kernel runs) holds
+ * wkv4_forward_workspace_bytes() bytes. */
 int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
-                 void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream);
+                 void* y, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                 int64_t C, int dtype, void* stream);
 
 /* Bytes of the forward-state checkpoint records for these sizes: 3 fp32
  * per (batch, block of 64 steps, channel) -- the state (A, B) = 2^o (p, q)
@@ -61,12 +72,15 @@ size_t wkv4_checkpoint_bytes(int64_t B, int64_t T, int64_t C);
  * reads the sequence once; no counterpart in the reference, whose autograd
  * re-runs the forward inside the backward kernel (wkv_triton.py:85-115). */
 int wkv4_forward_checkpointed(const void* k, const void* v, const float* time_decay,
-                              const float* time_first, void* y, float* checkpoint, int64_t B,
-                              int64_t T, int64_t C, int dtype, void* stream);
+                              const float* time_first, void* y, float* checkpoint,
+                              void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                              int64_t C, int dtype, void* stream);
 
-/* Bytes of device workspace wkv4_backward needs for these sizes (the
- * checkpoint records it computes itself plus per-batch parameter-gradient
- * partials). */
+/* Bytes of device workspace wkv4_backward uses for these sizes: the
+ * checkpoint records it computes itself, then the per-batch parameter-
+ * gradient partials and, for few rows, the split kernels' carries.  The call
+ * accepts less (down to the records and the [2][B][C] partials) and then runs
+ * the one-row kernels. */
 size_t wkv4_backward_workspace_bytes(int64_t B, int64_t T, int64_t C, int dtype);
 
 /* RWKV-4 / SpikeGPT WKV backward.
@@ -94,19 +108,22 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
  * forbid hipMalloc).  Same arguments, kernels and results as wkv4_backward,
  * with the workspace taken from a fixed device array of
  * WKV4_NOALLOC_SCRATCH_BYTES per GPU (the library looks its address up once
- * per device and never frees it).  Sizes whose wkv4_backward_workspace_bytes
- * exceed that maximum are rejected with WKV_ERR_WORKSPACE_TOO_SMALL.  Every
+ * per device and never frees it).  Sizes whose minimum workspace (the
+ * records and the [2][B][C] partials wkv4_backward accepts at the least)
+ * exceeds that maximum are rejected with WKV_ERR_WORKSPACE_TOO_SMALL.  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (on
  * different streams, or from different threads) race and must be serialised
- * by the caller.  The stream must belong to the current device. */
+ * by the caller.  The stream must belong to the current device.  The split
+ * kernels run when their workspace fits in the array as well. */
 int wkv4_backward_noalloc(const void* grad_y, const float* w, const float* u, const void* k,
                           const void* v, void* grad_k, void* grad_v, float* grad_time_decay,
                           float* grad_time_first, int64_t B, int64_t T, int64_t C, int dtype,
                           void* stream);
 
-/* Bytes of device workspace wkv4_backward_checkpointed needs (per-batch
- * parameter-gradient partials, 2*B*C fp32). */
-size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t C);
+/* Bytes of device workspace wkv4_backward_checkpointed uses: the per-batch
+ * parameter-gradient partials (2*B*C fp32, the minimum it accepts), or for
+ * few rows the split kernel's per-segment partials and carries. */
+size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t T, int64_t C);
 
 /* wkv4_backward from the records of wkv4_forward_checkpointed on the same
  * k, v, time_decay, time_first.  Takes the raw time_decay (w = -exp(.) is
@@ -128,8 +145,8 @@ int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
  * checkpoint optional (NULL: none), as wkv4_forward_checkpointed. */
 int wkv4_forward_gated_checkpointed(const void* k, const void* v, const float* time_decay,
                                     const float* time_first, const void* r, void* y,
-                                    float* checkpoint, int64_t B, int64_t T, int64_t C, int dtype,
-                                    void* stream);
+                                    float* checkpoint, void* workspace, size_t workspace_bytes,
+                                    int64_t B, int64_t T, int64_t C, int dtype, void* stream);
 
 /* Backward of wkv4_forward_gated_checkpointed from its records: grad_y is
  * the gradient of the gated output; writes grad_k, grad_v, grad_r (dtype)
@@ -417,6 +434,13 @@ int block_step_wkv(const float* key, const float* value, const float* receptance
  * consumes the pair; an entry point that launches nothing leaves the events
  * unrecorded. */
 int wkv_time_next_call(void* start_event, void* stop_event);
+
+/* As wkv_time_next_call, but both events are bound to one kernel dispatch
+ * of the next entry point: the `kernel`-th (from 0) kernel it launches, so
+ * that one kernel's own duration is measured (e.g. the reverse sweep of a
+ * backward without the batch-sum kernel after it).  No reference
+ * counterpart; measurement only. */
+int wkv_time_next_kernel(void* start_event, void* stop_event, int kernel);
 
 /* Text of the last error raised on the calling thread ("" if none). */
 const char* wkv_last_error_string(void);

@@ -176,36 +176,25 @@ def monoid_combine(left, right):
     )
 
 
-def wkv_monoid_scan(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
-    """The reference's CPU path ``weighted_key_value`` (``language.py:452-527``).
-
-    Upcasts bf16/fp16 to float32 and keeps float32/float64 (``:483-485``).
-    The inclusive prefix of the monoid is taken as a left fold (the reference
-    hands the same combine to ``associative_scan``; associativity makes the
-    two equal up to rounding), then shifted to the exclusive prefix and merged
-    with the ``time_first`` bonus (``:514-526``).
-    """
-    validate_wkv_inputs(key, value, time_decay, time_first)
+def _monoid_operands(key, value, time_decay, time_first):
+    """Inputs of the monoid form of ``language.py:482-494``: the compute dtype
+    (bf16/fp16 upcast to float32, float32/float64 kept), ``decay = -exp(td)``,
+    ``first``, and the per-token elements ``(acc_decay, log_scale=k, num=v,
+    den=1)`` on ``[T, B, C]``."""
     orig = key.dtype
     dtype = torch.float32 if orig in (torch.float16, torch.bfloat16) else orig
     batch, steps, channels = key.shape
     decay = -torch.exp(time_decay.to(dtype))
     first = time_first.to(dtype)
-    keys = key.movedim(1, 0).to(dtype)
-    values = value.movedim(1, 0).to(dtype)
-    acc = None
-    scales, nums, dens = [], [], []
-    for t in range(steps):
-        elem = (decay.expand(batch, channels), keys[t], values[t], torch.ones_like(keys[t]))
-        acc = elem if acc is None else monoid_combine(acc, elem)
-        scales.append(acc[1])
-        nums.append(acc[2])
-        dens.append(acc[3])
-    if steps == 0:
-        return key.new_empty(key.shape)
-    scale_inc = torch.stack(scales)
-    num_inc = torch.stack(nums)
-    den_inc = torch.stack(dens)
+    keys = key.movedim(1, 0).contiguous().to(dtype)
+    values = value.movedim(1, 0).contiguous().to(dtype)
+    acc_decay = decay[None, None, :].expand(steps, batch, channels).contiguous()
+    return orig, dtype, first, (acc_decay, keys, values, torch.ones_like(keys))
+
+
+def _monoid_output(scale_inc, num_inc, den_inc, keys, values, first, dtype, orig):
+    """Exclusive prefix (shift by one token, ``language.py:514-519``) merged
+    with the ``time_first`` bonus of the current token (``:521-526``)."""
     neg = torch.full_like(scale_inc[:1], torch.finfo(dtype).min)
     zeros = torch.zeros_like(num_inc[:1])
     scale_ex = torch.cat([neg, scale_inc[:-1]])
@@ -217,6 +206,51 @@ def wkv_monoid_scan(key: Tensor, value: Tensor, time_decay: Tensor, time_first: 
     wb = torch.exp(bonus - merged)
     out = (wp * num_ex + wb * values) / (wp * den_ex + wb)
     return out.movedim(0, 1).to(orig)
+
+
+def wkv_monoid_scan(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
+    """The reference's CPU path ``weighted_key_value`` (``language.py:452-527``)
+    with its inclusive prefix taken as a sequential left fold of the monoid.
+
+    Upcasts bf16/fp16 to float32 and keeps float32/float64 (``:483-485``).
+    :func:`wkv_associative_scan` hands the same combine to
+    ``associative_scan`` as the reference does; associativity makes the two
+    equal up to rounding.
+    """
+    validate_wkv_inputs(key, value, time_decay, time_first)
+    if key.shape[1] == 0:
+        return key.new_empty(key.shape)
+    orig, dtype, first, elems = _monoid_operands(key, value, time_decay, time_first)
+    acc = None
+    scales, nums, dens = [], [], []
+    for t in range(key.shape[1]):
+        elem = tuple(x[t] for x in elems)
+        acc = elem if acc is None else monoid_combine(acc, elem)
+        scales.append(acc[1])
+        nums.append(acc[2])
+        dens.append(acc[3])
+    return _monoid_output(torch.stack(scales), torch.stack(nums), torch.stack(dens), elems[1],
+                          elems[2], first, dtype, orig)
+
+
+def wkv_associative_scan(key: Tensor, value: Tensor, time_decay: Tensor,
+                         time_first: Tensor) -> Tensor:
+    """``weighted_key_value`` (``language.py:452-527``) as the reference runs
+    it: the inclusive prefix of the monoid by
+    ``torch._higher_order_ops.associative_scan(combine, ..., dim=0,
+    combine_mode="generic")`` (``:496-512``), a tree of O(log T) combine
+    levels, so its rounding differs from the left fold's.  Forward only here:
+    the reference notes that its autograd needs torch >= 2.13 (this image has
+    torch 2.10)."""
+    from torch._higher_order_ops.associative_scan import associative_scan
+
+    validate_wkv_inputs(key, value, time_decay, time_first)
+    if key.shape[1] == 0:
+        return key.new_empty(key.shape)
+    orig, dtype, first, elems = _monoid_operands(key, value, time_decay, time_first)
+    _, scale_inc, num_inc, den_inc = associative_scan(monoid_combine, elems, dim=0,
+                                                      combine_mode="generic")
+    return _monoid_output(scale_inc, num_inc, den_inc, elems[1], elems[2], first, dtype, orig)
 
 
 def reference_forward(k: Tensor, v: Tensor, w: Tensor, u: Tensor) -> Tensor:

@@ -54,7 +54,8 @@ _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
 _F = ctypes.c_float
 SIGNATURES = {
-    "wkv4_forward": (_INT, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
+    "wkv4_forward_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "wkv4_forward": (_INT, [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64, _INT]),
     "wkv4_backward": (
         _INT,
@@ -65,10 +66,11 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P],
     ),
     "wkv4_checkpoint_bytes": (_SZ, [_I64, _I64, _I64]),
-    "wkv4_forward_checkpointed": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
-    "wkv4_backward_checkpointed_workspace_bytes": (_SZ, [_I64, _I64]),
-    "wkv4_forward_gated_checkpointed": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT,
-                                                _P]),
+    "wkv4_forward_checkpointed": (
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P]),
+    "wkv4_backward_checkpointed_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "wkv4_forward_gated_checkpointed": (
+        _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_gated_checkpointed": (
         _INT, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _INT, _P]),
     "wkv4_backward_checkpointed": (
@@ -127,6 +129,7 @@ SIGNATURES = {
     "block_step_row": (_INT, [_INT, ctypes.POINTER(StepRowArgs), _P]),
     "block_step_wkv": (_INT, [_P] * 12 + [_I64, _I64, _P]),
     "wkv_time_next_call": (_INT, [_P, _P]),
+    "wkv_time_next_kernel": (_INT, [_P, _P, _INT]),
     "wkv_last_error_string": (ctypes.c_char_p, []),
     "wkv_version": (ctypes.c_char_p, []),
 }
@@ -202,14 +205,19 @@ def timed(name: str, device: torch.device, call):
     return rc
 
 
-def arm_events(start: torch.cuda.Event, end: torch.cuda.Event) -> None:
+def arm_events(start: torch.cuda.Event, end: torch.cuda.Event, kernel: int | None = None) -> None:
     """Bind ``start``/``end`` to the first/last kernel dispatch of the next C ABI
-    call on this thread (kernel start and end timestamps, no marker packets)."""
+    call on this thread (kernel start and end timestamps, no marker packets),
+    or, with ``kernel``, both to that call's ``kernel``-th dispatch alone."""
     for ev in (start, end):
         if ev.cuda_event == 0:
             # torch creates the HIP event lazily at its first record.
             ev.record(torch.cuda.current_stream())
-    load().wkv_time_next_call(start.cuda_event, end.cuda_event)
+    if kernel is None:
+        load().wkv_time_next_call(start.cuda_event, end.cuda_event)
+    else:
+        check(load().wkv_time_next_kernel(start.cuda_event, end.cuda_event, kernel),
+              "wkv_time_next_kernel")
 
 
 def stream_of(t: torch.Tensor) -> int:

@@ -14,6 +14,7 @@
 
 #include "../../include/wkv_hip.h"
 #include "wkv_common.h"
+#include "wkv_impl.h"
 
 namespace wkv_host {
 
@@ -71,64 +72,6 @@ bool env_cfg(const char* name, int& vec, int& L, int& W) {
   if (!s) return false;
   return sscanf(s, "%d,%d,%d", &vec, &L, &W) == 3;
 }
-
-int wkv4_forward_impl(const void*, const void*, const float*, int, const float*, void*, float*,
-                      int, int, int, int, hipStream_t);
-int wkv4_backward_impl(const void*, const float*, const float*, const void*, const void*, void*,
-                       void*, float*, float*, float*, int, int, int, int, hipStream_t);
-int wkv4_backward_ck_impl(const void*, const float*, int, const float*, const void*, const void*,
-                          const float*, void*, void*, float*, float*, float*, int, int, int, int,
-                          hipStream_t);
-int wkv4_forward_gated_impl(const void*, const void*, const float*, const float*, const void*,
-                            void*, float*, int, int, int, int, hipStream_t);
-int wkv4_backward_gated_ck_impl(const void*, const float*, const float*, const void*, const void*,
-                                const void*, const float*, void*, void*, void*, float*, float*,
-                                float*, int, int, int, int, hipStream_t);
-size_t wkv4_bwd_workspace_bytes_impl(int64_t, int64_t, int64_t, int);
-size_t wkv4_checkpoint_floats(int64_t, int64_t, int64_t);
-size_t wkv4_partials_floats(int64_t, int64_t);
-int wkv4_zero_param_grads(float*, float*, int, hipStream_t);
-int wkv4_decode_impl(const void*, const void*, const float*, const float*, const float*,
-                     const float*, const float*, void*, float*, float*, float*, int, int, int,
-                     hipStream_t);
-int wkv7_forward_impl(const void*, const void*, const void*, const void*, const void*,
-                      const void*, const float*, void*, float*, float*, int, int, int, int,
-                      hipStream_t);
-int wkv7_backward_ck_impl(const void*, const void*, const void*, const void*, const void*,
-                          const void*, const void*, const float*, const float*, void*, void*,
-                          void*, void*, void*, void*, float*, int, int, int, int, hipStream_t);
-size_t wkv7_checkpoint_floats(int64_t, int64_t, int64_t);
-size_t lif_checkpoint_floats(int64_t, int64_t, int64_t);
-size_t shift_mix_partial_floats(int64_t, int64_t, int64_t, int64_t);
-int shift_mix_forward_impl(const void*, int, const float*, void* const*, int, int, int, int, int,
-                           hipStream_t);
-int shift_mix_backward_impl(const void*, int, const float*, const void* const*, int, void*, float*,
-                            float*, int, int, int, int, hipStream_t);
-int lif_forward_impl(const void*, void*, float*, int, int, int, float, float, float, float, int,
-                     hipStream_t);
-int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
-                      float, float, int, hipStream_t);
-int lif_residual_forward_impl(const void*, const float*, float*, float*, int, int, int, float,
-                              float, float, float, int, hipStream_t);
-int lif_residual_backward_impl(const void*, const float*, const float*, void*, int, int, int,
-                               float, float, float, float, int, hipStream_t);
-bool lif_residual_ok(int64_t, int64_t, int);
-int relu_square_forward_impl(const void*, void*, int64_t, int, hipStream_t);
-int relu_square_backward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
-int sigmoid_gate_forward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);
-int sigmoid_gate_backward_impl(const void*, const void*, const void*, void*, void*, int64_t, int,
-                               hipStream_t);
-int block_step_row_impl(int, const wkv_step_row_args&, hipStream_t);
-int ln_mix_forward_impl(const float*, const float*, const float*, const float*, int, void* const*,
-                        int, float*, float*, int, int, int, float, hipStream_t);
-int ln_mix_backward_impl(const float*, const float*, const float*, const float*, int,
-                         const float*, const float*, const void* const*, int, float*,
-                         const float*, float*, float*, int, int, int, hipStream_t);
-int64_t ln_mix_workgroups(int64_t, int64_t);
-int split_k_sum_impl(const float*, float*, int64_t, int64_t, hipStream_t);
-int block_step_wkv_impl(const float*, const float*, const float*, const float*, const float*,
-                        const float*, const float*, const float*, float*, float*, float*, float*,
-                        int64_t, int64_t, hipStream_t);
 
 static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }
 
@@ -192,19 +135,39 @@ using namespace wkv_host;
 
 extern "C" {
 
+size_t wkv4_forward_workspace_bytes(int64_t B, int64_t T, int64_t C) {
+  if (!dims_ok(B, T, C)) return 0;
+  return wkv4_fwd_workspace_bytes_impl(B, T, C);
+}
+
+// Shared checks of the forward entry points; 0 = proceed, -1 = nothing to
+// do, else the status.
+static int check_forward(const char* what, const void* k, const void* v, const float* td,
+                         const float* tf, const void* r, bool need_r, const void* y, bool need_y,
+                         const float* ck, bool need_ck, const void* ws, int64_t B, int64_t T,
+                         int64_t C, int dtype) {
+  const std::string w(what);
+  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, w + ": unknown dtype");
+  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, w + ": bad sizes");
+  if (B == 0 || T == 0 || C == 0) return -1;
+  if (!k || !v || !td || !tf || (need_r && !r) || (need_y && !y) || (need_ck && !ck))
+    return fail(WKV_ERR_INVALID_ARGUMENT, w + ": null pointer");
+  if (!aligned16({k, v, r, y, ck, ws}))
+    return fail(WKV_ERR_INVALID_ARGUMENT, w + ": tensors and workspace must be 16-byte aligned");
+  return 0;
+}
+
 int wkv4_forward(const void* k, const void* v, const float* time_decay, const float* time_first,
-                 void* y, int64_t B, int64_t T, int64_t C, int dtype, void* stream) {
+                 void* y, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                 int64_t C, int dtype, void* stream) {
   set_error("");
   TimingScope timing;
-  if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: unknown dtype");
-  if (!dims_ok(B, T, C)) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: bad sizes");
-  if (B == 0 || T == 0 || C == 0) return WKV_OK;
-  if (!k || !v || !time_decay || !time_first || !y)
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: null pointer");
-  if (!aligned16({k, v, y}))
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward: k, v, y must be 16-byte aligned");
-  return wkv4_forward_impl(k, v, time_decay, 0, time_first, y, nullptr, int(B), int(T), int(C),
-                           dtype, static_cast<hipStream_t>(stream));
+  const int rc = check_forward("wkv4_forward", k, v, time_decay, time_first, nullptr, false, y,
+                               true, nullptr, false, workspace, B, T, C, dtype);
+  if (rc) return rc < 0 ? WKV_OK : rc;
+  return wkv4_forward_impl(k, v, time_decay, 0, time_first, y, nullptr, workspace,
+                           workspace ? workspace_bytes : 0, int(B), int(T), int(C), dtype,
+                           static_cast<hipStream_t>(stream));
 }
 
 size_t wkv4_checkpoint_bytes(int64_t B, int64_t T, int64_t C) {
@@ -213,22 +176,17 @@ size_t wkv4_checkpoint_bytes(int64_t B, int64_t T, int64_t C) {
 }
 
 int wkv4_forward_checkpointed(const void* k, const void* v, const float* time_decay,
-                              const float* time_first, void* y, float* checkpoint, int64_t B,
-                              int64_t T, int64_t C, int dtype, void* stream) {
+                              const float* time_first, void* y, float* checkpoint,
+                              void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                              int64_t C, int dtype, void* stream) {
   set_error("");
   TimingScope timing;
-  if (!dtype_ok(dtype))
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: unknown dtype");
-  if (!dims_ok(B, T, C))
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: bad sizes");
-  if (B == 0 || T == 0 || C == 0) return WKV_OK;
-  if (!k || !v || !time_decay || !time_first || !checkpoint)
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_checkpointed: null pointer");
-  if (!aligned16({k, v, y, checkpoint}))
-    return fail(WKV_ERR_INVALID_ARGUMENT,
-                "wkv4_forward_checkpointed: tensors must be 16-byte aligned");
-  return wkv4_forward_impl(k, v, time_decay, 0, time_first, y, checkpoint, int(B), int(T), int(C),
-                           dtype, static_cast<hipStream_t>(stream));
+  const int rc = check_forward("wkv4_forward_checkpointed", k, v, time_decay, time_first, nullptr,
+                               false, y, false, checkpoint, true, workspace, B, T, C, dtype);
+  if (rc) return rc < 0 ? WKV_OK : rc;
+  return wkv4_forward_impl(k, v, time_decay, 0, time_first, y, checkpoint, workspace,
+                           workspace ? workspace_bytes : 0, int(B), int(T), int(C), dtype,
+                           static_cast<hipStream_t>(stream));
 }
 
 size_t wkv4_backward_workspace_bytes(int64_t B, int64_t T, int64_t C, int dtype) {
@@ -251,7 +209,7 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
   if (B == 0 || T == 0) return wkv4_zero_param_grads(grad_time_decay, grad_time_first, int(C), s);
   if (!grad_y || !w || !u || !k || !v || !grad_k || !grad_v || !workspace)
     return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_backward: null pointer");
-  const size_t need = wkv4_bwd_workspace_bytes_impl(B, T, C, dtype);
+  const size_t need = wkv4_bwd_min_workspace_bytes_impl(B, T, C);
   if (workspace_bytes < need)
     return fail(WKV_ERR_WORKSPACE_TOO_SMALL,
                 "wkv4_backward: workspace too small (need " + std::to_string(need) + " bytes)");
@@ -259,7 +217,7 @@ int wkv4_backward(const void* grad_y, const float* w, const float* u, const void
     return fail(WKV_ERR_INVALID_ARGUMENT,
                 "wkv4_backward: grad_y, k, v, grad_k, grad_v, workspace must be 16-byte aligned");
   return wkv4_backward_impl(grad_y, w, u, k, v, grad_k, grad_v, grad_time_decay, grad_time_first,
-                            static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
+                            workspace, workspace_bytes, int(B), int(T), int(C), dtype, s);
 }
 
 int wkv4_backward_noalloc(const void* grad_y, const float* w, const float* u, const void* k,
@@ -276,7 +234,7 @@ int wkv4_backward_noalloc(const void* grad_y, const float* w, const float* u, co
   // Checked before any pointer is looked at.  Records and partials are
   // written in full before they are read, so the scratch needs no clearing
   // between calls.
-  const size_t need = wkv4_bwd_workspace_bytes_impl(B, T, C, dtype);
+  const size_t need = wkv4_bwd_min_workspace_bytes_impl(B, T, C);
   if (need > size_t(WKV4_NOALLOC_SCRATCH_BYTES))
     return fail(WKV_ERR_WORKSPACE_TOO_SMALL,
                 "wkv4_backward_noalloc: these sizes need " + std::to_string(need) +
@@ -294,13 +252,15 @@ int wkv4_backward_noalloc(const void* grad_y, const float* w, const float* u, co
                 "wkv4_backward_noalloc: grad_y, k, v, grad_k, grad_v must be 16-byte aligned");
   void* ws = nullptr;
   if (int rc = scratch_address(&ws, "wkv4_backward_noalloc")) return rc;
+  // The split kernels run when their workspace fits in the scratch too.
   return wkv4_backward_impl(grad_y, w, u, k, v, grad_k, grad_v, grad_time_decay, grad_time_first,
-                            static_cast<float*>(ws), int(B), int(T), int(C), dtype, s);
+                            ws, size_t(WKV4_NOALLOC_SCRATCH_BYTES), int(B), int(T), int(C), dtype,
+                            s);
 }
 
-size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t C) {
-  if (!dims_ok(B, 1, C)) return 0;
-  return wkv4_partials_floats(B, C) * sizeof(float) + 256;
+size_t wkv4_backward_checkpointed_workspace_bytes(int64_t B, int64_t T, int64_t C) {
+  if (!dims_ok(B, T, C)) return 0;
+  return wkv4_bwd_ck_workspace_bytes_impl(B, T, C);
 }
 
 int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
@@ -329,28 +289,22 @@ int wkv4_backward_checkpointed(const void* grad_y, const float* time_decay,
     return fail(WKV_ERR_INVALID_ARGUMENT,
                 "wkv4_backward_checkpointed: tensors must be 16-byte aligned");
   return wkv4_backward_ck_impl(grad_y, time_decay, 0, time_first, k, v, checkpoint, grad_k,
-                               grad_v, grad_time_decay, grad_time_first,
-                               static_cast<float*>(workspace), int(B), int(T), int(C), dtype, s);
+                               grad_v, grad_time_decay, grad_time_first, workspace,
+                               workspace_bytes, int(B), int(T), int(C), dtype, s);
 }
 
 int wkv4_forward_gated_checkpointed(const void* k, const void* v, const float* time_decay,
                                     const float* time_first, const void* r, void* y,
-                                    float* checkpoint, int64_t B, int64_t T, int64_t C, int dtype,
-                                    void* stream) {
+                                    float* checkpoint, void* workspace, size_t workspace_bytes,
+                                    int64_t B, int64_t T, int64_t C, int dtype, void* stream) {
   set_error("");
   TimingScope timing;
-  if (!dtype_ok(dtype))
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_gated_checkpointed: unknown dtype");
-  if (!dims_ok(B, T, C))
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_gated_checkpointed: bad sizes");
-  if (B == 0 || T == 0 || C == 0) return WKV_OK;
-  if (!k || !v || !time_decay || !time_first || !r || !y)
-    return fail(WKV_ERR_INVALID_ARGUMENT, "wkv4_forward_gated_checkpointed: null pointer");
-  if (!aligned16({k, v, r, y, checkpoint}))
-    return fail(WKV_ERR_INVALID_ARGUMENT,
-                "wkv4_forward_gated_checkpointed: tensors must be 16-byte aligned");
-  return wkv4_forward_gated_impl(k, v, time_decay, time_first, r, y, checkpoint, int(B), int(T),
-                                 int(C), dtype, static_cast<hipStream_t>(stream));
+  const int rc = check_forward("wkv4_forward_gated_checkpointed", k, v, time_decay, time_first, r,
+                               true, y, true, checkpoint, false, workspace, B, T, C, dtype);
+  if (rc) return rc < 0 ? WKV_OK : rc;
+  return wkv4_forward_gated_impl(k, v, time_decay, time_first, r, y, checkpoint, workspace,
+                                 workspace ? workspace_bytes : 0, int(B), int(T), int(C), dtype,
+                                 static_cast<hipStream_t>(stream));
 }
 
 int wkv4_backward_gated_checkpointed(const void* grad_y, const float* time_decay,
@@ -381,9 +335,8 @@ int wkv4_backward_gated_checkpointed(const void* grad_y, const float* time_decay
     return fail(WKV_ERR_INVALID_ARGUMENT,
                 "wkv4_backward_gated_checkpointed: tensors must be 16-byte aligned");
   return wkv4_backward_gated_ck_impl(grad_y, time_decay, time_first, k, v, r, checkpoint, grad_k,
-                                     grad_v, grad_r, grad_time_decay, grad_time_first,
-                                     static_cast<float*>(workspace), int(B), int(T), int(C),
-                                     dtype, s);
+                                     grad_v, grad_r, grad_time_decay, grad_time_first, workspace,
+                                     workspace_bytes, int(B), int(T), int(C), dtype, s);
 }
 
 int wkv4_decode_step(const void* k, const void* v, const float* time_decay, const float* time_first,
@@ -901,8 +854,18 @@ int block_step_wkv(const float* key, const float* value, const float* receptance
 }
 
 int wkv_time_next_call(void* start_event, void* stop_event) {
+  g_pending_events = CallEvents{};
   g_pending_events.start = static_cast<hipEvent_t>(start_event);
   g_pending_events.stop = static_cast<hipEvent_t>(stop_event);
+  return WKV_OK;
+}
+
+int wkv_time_next_kernel(void* start_event, void* stop_event, int kernel) {
+  if (kernel < 0) return fail(WKV_ERR_INVALID_ARGUMENT, "wkv_time_next_kernel: negative index");
+  g_pending_events = CallEvents{};
+  g_pending_events.start = static_cast<hipEvent_t>(start_event);
+  g_pending_events.stop = static_cast<hipEvent_t>(stop_event);
+  g_pending_events.kernel = kernel;
   return WKV_OK;
 }
 

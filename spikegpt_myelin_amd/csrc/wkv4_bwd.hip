@@ -45,7 +45,10 @@
 // exact serial path (record o = -1e38 at block 0 instead of 0); such rows are
 // recomputed here one channel per thread with the reference's running-max
 // recurrences.
+#include <algorithm>
+
 #include "wkv_common.h"
+#include "wkv_impl.h"
 
 namespace wkv {
 
@@ -224,26 +227,13 @@ struct Bwd {
     for (int c = 0; c < VEC; ++c) rc.q[c] = a.x[c];
   }
 
-  // One segment (visited last to first).  FULL: every step is inside the
-  // sequence.
+  // e^{k} of the chunk's steps (zero past T) and the chunk's forward summary
+  // from a zero state.
   template <bool FULL>
-  __device__ static __forceinline__ void segment(
-      Smem& sm, int seg, int nseg, int T, int C, int wave, int lane, bool active, size_t row_base,
-      size_t row_tail, unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
-      const PackT (&rb)[L], const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC],
-      const float (&U)[VEC], const Weights& Wt, raw* __restrict__ gk, raw* __restrict__ gv,
-      raw* __restrict__ gr, float (&gw)[VEC], float (&gu)[VEC]) {
-    const int t0 = (seg * W + wave) * L;
-    float P[VEC], Q[VEC];
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      P[c] = rc.p[c];
-      Q[c] = rc.q[c];
-    }
-
-    // e^{k} and this chunk's forward summary from a zero state.
-    float ek[L][VEC];
-    float ps[VEC], qs[VEC];
+  __device__ static __forceinline__ void summarize(int t0, int T, const PackT (&kb)[L],
+                                                   const PackT (&vb)[L], const float (&D)[VEC],
+                                                   float (&ek)[L][VEC], float (&ps)[VEC],
+                                                   float (&qs)[VEC]) {
 #pragma unroll
     for (int c = 0; c < VEC; ++c) { ps[c] = 0.f; qs[c] = 0.f; }
 #pragma unroll
@@ -258,22 +248,20 @@ struct Bwd {
         qs[c] = fmaf(qs[c], D[c], e);
       }
     }
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      sm.p[c][wave][lane] = ps[c];
-      sm.q[c][wave][lane] = qs[c];
-    }
-    __syncthreads();
-    for (int w = 0; w < wave; ++w) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        P[c] = fmaf(P[c], DL[c], sm.p[c][w][lane]);
-        Q[c] = fmaf(Q[c], DL[c], sm.q[c][w][lane]);
-      }
-    }
-    // Forward recompute: keep z = gy/den, z y (zero past the end) and the
-    // states (A_t, B_t) = (P, Q) before step t.
-    float zz[L][VEC], zy[L][VEC], pa[L][VEC], qa[L][VEC];
+  }
+
+  // Forward recompute of the chunk from its forward carry (P, Q): keeps
+  // z = gy/den, z y (zero past the end) and the states (A_t, B_t) before
+  // step t; GATE: the gate's backward, grad_r stored.  Then the chunk's
+  // reverse summary (G, H) from a zero state at its end, as dot products
+  // with the weights e^{iw} of step i: G = sum_i e^{iw} z_i (H with z y).
+  template <bool FULL>
+  __device__ static __forceinline__ void recompute(
+      int t0, int T, int C, bool active, size_t row_base, size_t row_tail, unsigned lane_boff,
+      const PackT (&vb)[L], const PackT (&gb)[L], const PackT (&rb)[L], const float (&ek)[L][VEC],
+      const float (&D)[VEC], const float (&U)[VEC], const Weights& Wt, float (&P)[VEC],
+      float (&Q)[VEC], float (&zz)[L][VEC], float (&zy)[L][VEC], float (&pa)[L][VEC],
+      float (&qa)[L][VEC], raw* __restrict__ gr, float (&G)[VEC], float (&H)[VEC]) {
     OutPack<E, VEC> grp[GATE ? L : 1];
 #pragma unroll
     for (int i = 0; i < L; ++i) {
@@ -316,10 +304,6 @@ struct Bwd {
         for (int i = 0; i < L; ++i) store_buf(grp[i], rgr, lane_boff, unsigned(i) * stride);
       }
     }
-    // Reverse summary of this chunk from a zero state at its end, as dot
-    // products with the weights e^{iw} of step i: G = sum_i e^{iw} z_i
-    // (likewise H with z y).
-    float G[VEC], H[VEC];
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       G[c] = zz[0][c];
@@ -333,29 +317,17 @@ struct Bwd {
         H[c] = fmaf(zy[i][c], Wt.d0[i - 1][c], H[c]);
       }
     }
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      sm.G[c][wave][lane] = G[c];
-      sm.H[c][wave][lane] = H[c];
-    }
-    __syncthreads();
-    // Carry at this chunk's end: the later segment's carry, then the later
-    // chunks of this segment, nearest last.
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      const int sl = (seg + 1) & 1;
-      const bool later = seg + 1 < nseg;
-      G[c] = later ? sm.rcarry[sl][0][c][lane] : 0.f;
-      H[c] = later ? sm.rcarry[sl][1][c][lane] : 0.f;
-    }
-    for (int w = W - 1; w > wave; --w) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        G[c] = fmaf(DL[c], G[c], sm.G[c][w][lane]);
-        H[c] = fmaf(DL[c], H[c], sm.H[c][w][lane]);
-      }
-    }
-    // Reverse pass with outputs (stored together after the pass).
+  }
+
+  // Reverse pass of the chunk from the carry (G, H) at its end: gk, gv
+  // stored (together, after the pass), gw and gu accumulated; (G, H) leaves
+  // as the carry at the chunk's start.
+  __device__ static __forceinline__ void reverse(
+      int t0, int C, bool active, size_t row_base, size_t row_tail, unsigned lane_boff,
+      const PackT (&vb)[L], const float (&ek)[L][VEC], const float (&zz)[L][VEC],
+      const float (&zy)[L][VEC], const float (&pa)[L][VEC], const float (&qa)[L][VEC],
+      const float (&D)[VEC], const float (&U)[VEC], float (&G)[VEC], float (&H)[VEC],
+      raw* __restrict__ gk, raw* __restrict__ gv, float (&gw)[VEC], float (&gu)[VEC]) {
     OutPack<E, VEC> gko_p[L], gvo_p[L];
 #pragma unroll
     for (int i = L - 1; i >= 0; --i) {
@@ -394,6 +366,68 @@ struct Bwd {
         store_buf(gvo_p[i], rgv, lane_boff, unsigned(i) * stride);
       }
     }
+  }
+
+  // One segment (visited last to first).  FULL: every step is inside the
+  // sequence.
+  template <bool FULL>
+  __device__ static __forceinline__ void segment(
+      Smem& sm, int seg, int nseg, int T, int C, int wave, int lane, bool active, size_t row_base,
+      size_t row_tail, unsigned lane_boff, const PackT (&kb)[L], const PackT (&vb)[L], const PackT (&gb)[L],
+      const PackT (&rb)[L], const Recs& rc, const float (&D)[VEC], const float (&DL)[VEC],
+      const float (&U)[VEC], const Weights& Wt, raw* __restrict__ gk, raw* __restrict__ gv,
+      raw* __restrict__ gr, float (&gw)[VEC], float (&gu)[VEC]) {
+    const int t0 = (seg * W + wave) * L;
+    float P[VEC], Q[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      P[c] = rc.p[c];
+      Q[c] = rc.q[c];
+    }
+    float ek[L][VEC];
+    float ps[VEC], qs[VEC];
+    summarize<FULL>(t0, T, kb, vb, D, ek, ps, qs);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      sm.p[c][wave][lane] = ps[c];
+      sm.q[c][wave][lane] = qs[c];
+    }
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        P[c] = fmaf(P[c], DL[c], sm.p[c][w][lane]);
+        Q[c] = fmaf(Q[c], DL[c], sm.q[c][w][lane]);
+      }
+    }
+    float zz[L][VEC], zy[L][VEC], pa[L][VEC], qa[L][VEC];
+    float G[VEC], H[VEC];
+    recompute<FULL>(t0, T, C, active, row_base, row_tail, lane_boff, vb, gb, rb, ek, D, U, Wt, P,
+                    Q, zz, zy, pa, qa, gr, G, H);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      sm.G[c][wave][lane] = G[c];
+      sm.H[c][wave][lane] = H[c];
+    }
+    __syncthreads();
+    // Carry at this chunk's end: the later segment's carry, then the later
+    // chunks of this segment, nearest last.
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int sl = (seg + 1) & 1;
+      const bool later = seg + 1 < nseg;
+      G[c] = later ? sm.rcarry[sl][0][c][lane] : 0.f;
+      H[c] = later ? sm.rcarry[sl][1][c][lane] : 0.f;
+    }
+    for (int w = W - 1; w > wave; --w) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        G[c] = fmaf(DL[c], G[c], sm.G[c][w][lane]);
+        H[c] = fmaf(DL[c], H[c], sm.H[c][w][lane]);
+      }
+    }
+    reverse(t0, C, active, row_base, row_tail, lane_boff, vb, ek, zz, zy, pa, qa, D, U, G, H, gk,
+            gv, gw, gu);
     if (wave == 0) {
       const int sl = seg & 1;
 #pragma unroll
@@ -545,6 +579,256 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
   }
 }
 
+// ----------------------------------------------------- split over time ----
+// For few rows: one workgroup per (segment, row), blockIdx = (nseg - 1 -
+// segment) * rows + row, so that later segments are dispatched first.  The
+// forward state at the segment's start comes from the records; the reverse
+// carry at its end (G, H from all later steps) comes from the later
+// segments' words, mirroring the forward split kernel (lb_window_carry over
+// the K nearest later segments and one inclusive word):
+//   R_s = sum_{j>s} e^{(j-s-1) SEG w} agg_j,   incl_s = e^{SEG w} R_s + agg_s,
+// with agg_s the segment's reverse sums from a zero state at its end (the
+// fold of its chunks' sums) and incl_s the reverse state at its start.  gw
+// and gu are reduced per (batch, segment) into [B * nseg][C] partials, which
+// wkv4_bwd_fixup_kernel sums over the segments into [B][C] for
+// wkv4_param_grad_kernel.  Rows that the forward recomputed exactly, and rows
+// whose look-back gave up, are left to wkv4_bwd_fixup_kernel.
+//
+// Look-back words: lb[2][nseg][rows][64*VEC] (aggregates, then inclusive
+// states), each word the pair (G, H) of one channel; status[rows].
+template <typename E, int VEC, int L, int W, bool GATE>
+__global__ __launch_bounds__(W * 64) void wkv4_bwd_split_kernel(
+    const typename E::raw* __restrict__ gy, const float* __restrict__ decay, int decay_is_w,
+    const float* __restrict__ u_in, const typename E::raw* __restrict__ k,
+    const typename E::raw* __restrict__ v, const typename E::raw* __restrict__ r,
+    const float* __restrict__ ck, typename E::raw* __restrict__ gk,
+    typename E::raw* __restrict__ gv, typename E::raw* __restrict__ gr,
+    float* __restrict__ gw_part, float* __restrict__ gu_part, uint64_t* __restrict__ lb,
+    uint32_t* __restrict__ status, int rows, int T, int C) {
+  using F = Bwd<E, VEC, L, W, GATE>;
+  using PackT = typename F::PackT;
+  __shared__ typename F::Smem sm;
+
+  const int nseg = (T + F::SEG - 1) / F::SEG;
+  const int seg = nseg - 1 - __builtin_amdgcn_readfirstlane(int(blockIdx.x) / rows);
+  const int row = int(blockIdx.x) - (nseg - 1 - seg) * rows;
+  const int n_cg = (C + F::CPW - 1) / F::CPW;
+  const int b = row / n_cg;
+  const int cg = row - b * n_cg;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c0 = cg * F::CPW + lane * VEC;
+  const bool active = c0 < C;
+  const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * F::CPW;
+  const unsigned lane_boff = active ? unsigned(lane * VEC * sizeof(typename E::raw)) : 0u;
+  const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
+  const size_t ck_field = size_t(rows / n_cg) * nblk * C;
+  const size_t ck_row = size_t(b) * nblk * C + size_t(cg) * F::CPW;
+  const unsigned ck_boff = active ? unsigned(lane * VEC * sizeof(float)) : 0u;
+  const int t0 = (seg * W + wave) * L;
+
+  // Rows the forward kernels recomputed with their exact path carry o != 0
+  // in their block-0 records: the fix-up kernel handles them.
+  bool serial = false;
+  {
+    Pack<F32, VEC> o;
+    o.load(byte_offset(ck + ck_row, ck_boff));
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) serial |= active && o.x[c] != 0.f;
+  }
+  if (__syncthreads_or(serial) != 0) return;
+
+  PackT kb[L], vb[L], gb[L], xb[L];
+  typename F::Recs rc;
+  F::load(k, v, gy, r, ck, ck_row, ck_boff, ck_field, seg, row_base, row_tail, lane_boff, t0, C,
+          kb, vb, gb, xb, rc);
+
+  float D[VEC], DL[VEC], DS[VEC], U[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    const float dv = active ? decay[c0 + c] : 0.f;
+    const float uv = active ? u_in[c0 + c] : 0.f;
+    const float w2 = (decay_is_w ? dv : -expf(dv)) * kLog2e;
+    D[c] = fast_exp2(w2);
+    DL[c] = fast_exp2(w2 * float(L));
+    DS[c] = fast_exp2(w2 * float(F::SEG));
+    U[c] = fast_exp2(uv * kLog2e);
+  }
+  typename F::Weights Wt;
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    float pw = D[c];
+#pragma unroll
+    for (int i = 1; i < L; ++i) {
+      Wt.d0[i - 1][c] = pw;
+      pw *= D[c];
+    }
+  }
+
+  const bool full = (seg + 1) * F::SEG <= T;
+  float P[VEC], Q[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    P[c] = rc.p[c];
+    Q[c] = rc.q[c];
+  }
+  float ek[L][VEC];
+  float ps[VEC], qs[VEC];
+  if (full)
+    F::template summarize<true>(t0, T, kb, vb, D, ek, ps, qs);
+  else
+    F::template summarize<false>(t0, T, kb, vb, D, ek, ps, qs);
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    sm.p[c][wave][lane] = ps[c];
+    sm.q[c][wave][lane] = qs[c];
+  }
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      P[c] = fmaf(P[c], DL[c], sm.p[c][w][lane]);
+      Q[c] = fmaf(Q[c], DL[c], sm.q[c][w][lane]);
+    }
+  }
+  float zz[L][VEC], zy[L][VEC], pa[L][VEC], qa[L][VEC];
+  float G[VEC], H[VEC];
+  if (full)
+    F::template recompute<true>(t0, T, C, active, row_base, row_tail, lane_boff, vb, gb, xb, ek, D,
+                                U, Wt, P, Q, zz, zy, pa, qa, gr, G, H);
+  else
+    F::template recompute<false>(t0, T, C, active, row_base, row_tail, lane_boff, vb, gb, xb, ek,
+                                 D, U, Wt, P, Q, zz, zy, pa, qa, gr, G, H);
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    sm.G[c][wave][lane] = G[c];
+    sm.H[c][wave][lane] = H[c];
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    const size_t plane = size_t(nseg) * rows * F::CPW;  // words per kind
+    uint64_t* const mine = lb + (size_t(seg) * rows + row) * F::CPW + lane * VEC;
+    // This segment's reverse sums from a zero state at its end.
+    float ag[VEC], ah[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) { ag[c] = 0.f; ah[c] = 0.f; }
+    for (int w = W - 1; w >= 0; --w) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        ag[c] = fmaf(DL[c], ag[c], sm.G[c][w][lane]);
+        ah[c] = fmaf(DL[c], ah[c], sm.H[c][w][lane]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) lb_store(mine + c, lb_pack(ag[c], ah[c]));
+    float rg[VEC], rh[VEC];
+    const uint64_t* base = lb + size_t(row) * F::CPW + lane * VEC;
+    const bool gave_up = !lb_window_carry<VEC>(base, base + plane, size_t(rows) * F::CPW, seg,
+                                               nseg, -1, DS, rg, rh);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      lb_store(mine + plane + c, lb_pack(fmaf(DS[c], rg[c], ag[c]), fmaf(DS[c], rh[c], ah[c])));
+      sm.rcarry[0][0][c][lane] = rg[c];
+      sm.rcarry[0][1][c][lane] = rh[c];
+    }
+    if (__any(gave_up) && lane == 0) mark_row_redo(status, row);
+  }
+  __syncthreads();
+
+  // Carry at this chunk's end: the segment's carry, then the later chunks.
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    G[c] = sm.rcarry[0][0][c][lane];
+    H[c] = sm.rcarry[0][1][c][lane];
+  }
+  for (int w = W - 1; w > wave; --w) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      G[c] = fmaf(DL[c], G[c], sm.G[c][w][lane]);
+      H[c] = fmaf(DL[c], H[c], sm.H[c][w][lane]);
+    }
+  }
+  float gw[VEC], gu[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) { gw[c] = 0.f; gu[c] = 0.f; }
+  F::reverse(t0, C, active, row_base, row_tail, lane_boff, vb, ek, zz, zy, pa, qa, D, U, G, H, gk,
+             gv, gw, gu);
+
+  // gw, gu of this (batch, segment) reduced over the waves.
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    sm.G[c][wave][lane] = gw[c] * D[c];
+    sm.H[c][wave][lane] = gu[c] * U[c];
+  }
+  __syncthreads();
+  const size_t slot = (size_t(b) * nseg + seg) * C;
+  for (int ch = threadIdx.x; ch < F::CPW; ch += blockDim.x) {
+    const int c = cg * F::CPW + ch;
+    if (c >= C) continue;
+    const int l = ch / VEC, s = ch - l * VEC;
+    float sw = 0.f, su = 0.f;
+    for (int w = 0; w < W; ++w) {
+      sw += sm.G[s][w][l];
+      su += sm.H[s][w][l];
+    }
+    gw_part[slot + c] = sw;
+    gu_part[slot + c] = su;
+  }
+}
+
+// After the split backward: per row, its gw, gu summed over the segments in
+// a fixed order into the [B][C] partials (gw_b, gu_b) that
+// wkv4_param_grad_kernel sums over the batch.  Rows the split kernel left
+// (the forward's exact rows, and rows whose look-back gave up) are first
+// recomputed with the exact serial path, which writes gk, gv (and grad_r)
+// over the whole row and gives the row's sums directly.  One wave per row.
+template <typename E, bool GATE>
+__global__ __launch_bounds__(64) void wkv4_bwd_fixup_kernel(
+    const typename E::raw* __restrict__ gy, const float* __restrict__ decay, int decay_is_w,
+    const float* __restrict__ u_in, const typename E::raw* __restrict__ k,
+    const typename E::raw* __restrict__ v, const typename E::raw* __restrict__ r,
+    const float* __restrict__ ck, typename E::raw* __restrict__ gk,
+    typename E::raw* __restrict__ gv, typename E::raw* __restrict__ gr,
+    const float* __restrict__ gw_seg, const float* __restrict__ gu_seg,
+    float* __restrict__ gw_b, float* __restrict__ gu_b, const uint32_t* __restrict__ status,
+    int cpw, int n_cg, int nseg, int T, int C) {
+  const int row = blockIdx.x;
+  const int b = row / n_cg;
+  const int cg = row - b * n_cg;
+  const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
+  const size_t ck_field = size_t(gridDim.x / n_cg) * nblk * C;
+  bool redo = status[row] != kRowOk;
+  for (int ch = threadIdx.x; ch < cpw; ch += 64) {
+    const int c = cg * cpw + ch;
+    if (c < C) redo |= ck[size_t(b) * nblk * C + c] != 0.f;
+  }
+  redo = __any(redo);
+  for (int ch = threadIdx.x; ch < cpw; ch += 64) {
+    const int c = cg * cpw + ch;
+    if (c >= C) continue;
+    float sw = 0.f, su = 0.f;
+    if (redo) {
+      const float w2 = (decay_is_w ? decay[c] : -expf(decay[c])) * kLog2e;
+      wkv4_bwd_channel_serial<E, 8>(gy, k, v, GATE ? r : nullptr, gk, gv, GATE ? gr : nullptr,
+                                    w2, u_in[c] * kLog2e, T, C, size_t(b) * T * C + c, ck,
+                                    size_t(b) * nblk * C + c, ck_field, sw, su);
+    } else {
+      const float* pw = gw_seg + size_t(b) * nseg * C + c;
+      const float* pu = gu_seg + size_t(b) * nseg * C + c;
+#pragma unroll 8
+      for (int sg = 0; sg < nseg; ++sg) {
+        sw += pw[size_t(sg) * C];
+        su += pu[size_t(sg) * C];
+      }
+    }
+    gw_b[size_t(b) * C + c] = sw;
+    gu_b[size_t(b) * C + c] = su;
+  }
+}
+
 // grad_time_decay[c] = sum_b gw[b,c] * w[c] (chain rule through
 // w = -exp(time_decay), applied per batch element as the reference does,
 // wkv_triton.py:117,194); grad_time_first[c] = sum_b gu[b,c].  A block
@@ -596,8 +880,6 @@ __global__ void wkv4_zero2_kernel(float* a, float* b, int n) {
 // ------------------------------------------------------------ launcher ----
 namespace wkv_host {
 
-struct TileCfg { int vec, L, W; };
-
 // Tile configurations compiled into the library (selectable with
 // WKV_BWD_CFG="vec,L,W" for measurement).  SEG = W*L must be a multiple of
 // the 64-step checkpoint block.  Defaults: (2,8,8) for 16-bit tensors with
@@ -606,11 +888,9 @@ struct TileCfg { int vec, L, W; };
 // configurations are capped at 128 VGPRs and spill.
 static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}, {1, 8, 8},
                                         {1, 16, 4}, {2, 16, 4}};
-
-int pick_vec(int64_t B, int64_t C);
-bool env_cfg(const char* name, int& vec, int& L, int& W);
-int wkv4_forward_impl(const void*, const void*, const float*, int, const float*, void*, float*,
-                      int, int, int, int, hipStream_t);
+// Tile configurations of the split kernel (WKV_BWD_SPLIT_CFG).
+static constexpr TileCfg kBwdSplitCfgs[] = {{1, 8, 8}, {1, 16, 4}, {1, 8, 16}, {2, 8, 8},
+                                             {1, 4, 16}, {2, 4, 16}};
 
 static TileCfg pick_bwd_cfg(int64_t B, int64_t C, int elem_bytes) {
   int vec, L, W;
@@ -622,12 +902,51 @@ static TileCfg pick_bwd_cfg(int64_t B, int64_t C, int elem_bytes) {
   return TileCfg{1, 8, 8};
 }
 
+// The split kernel runs on the same condition as the forward's (few rows,
+// at least two segments); {0, 0, 0} when the one-row kernel runs.
+static TileCfg pick_bwd_split_cfg(int64_t B, int64_t T, int64_t C) {
+  TileCfg cfg{1, 16, 4};
+  int vec, L, W;
+  if (env_cfg("WKV_BWD_SPLIT_CFG", vec, L, W)) {
+    for (const TileCfg& c : kBwdSplitCfgs)
+      if (c.vec == vec && c.L == L && c.W == W && (vec == 1 || C % 2 == 0)) cfg = c;
+  }
+  const int64_t rows1 = B * ((C + 63) / 64);
+  const int64_t nseg = (T + cfg.L * cfg.W - 1) / (cfg.L * cfg.W);
+  const int mode = split_mode();
+  const bool want = mode == 1 || (mode != 0 && rows1 < kSplitRows && nseg >= kSplitMinSegs &&
+                                       B * T * C >= kSplitMinElems);
+  if (!want || nseg < 2 || B == 0 || C == 0) return TileCfg{0, 0, 0};
+  return cfg;
+}
+
 size_t wkv4_checkpoint_floats(int64_t B, int64_t T, int64_t C) {
   return size_t(wkv::kCkptFields) * size_t(B) * size_t((T + wkv::kCkptBlock - 1) / wkv::kCkptBlock) *
          size_t(C);
 }
 
 size_t wkv4_partials_floats(int64_t B, int64_t C) { return 2 * size_t(B) * size_t(C); }
+
+static size_t round16(size_t n) { return (n + 15) / 16 * 16; }
+
+// Workspace of the split backward: [2][B][C] and [2][B * nseg][C] fp32
+// partials, then the look-back words and the row status words.
+static size_t split_bwd_bytes(const TileCfg& cfg, int64_t B, int64_t T, int64_t C) {
+  const int64_t cpw = 64 * cfg.vec;
+  const int64_t rows = B * ((C + cpw - 1) / cpw);
+  const int64_t nseg = (T + cfg.L * cfg.W - 1) / (cfg.L * cfg.W);
+  const size_t words = size_t(2) * size_t(nseg) * size_t(rows) * size_t(cpw);
+  return round16(wkv4_partials_floats(B, C) * 4) + round16(wkv4_partials_floats(B * nseg, C) * 4) +
+         words * 8 + round16(size_t(rows) * 4);
+}
+
+// Workspace of a backward from records: the split kernel's when it runs,
+// else the [2][B][C] partials.
+size_t wkv4_bwd_ck_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
+  const TileCfg sc = pick_bwd_split_cfg(B, T, C);
+  const size_t plain = round16(wkv4_partials_floats(B, C) * 4);
+  return sc.vec == 0 ? plain : std::max(plain, split_bwd_bytes(sc, B, T, C));
+}
 
 // r, gr (both null or both given): the gated backward (forward y = sigmoid(r)
 // * wkv, grad_r written to gr).
@@ -661,11 +980,80 @@ static int launch_bwd(const void* gy, const float* decay, int decay_is_w, const 
   return check_launch("wkv4_param_grad_kernel");
 }
 
+template <typename E, int VEC, int L, int W>
+static int launch_bwd_split(const void* gy, const float* decay, int decay_is_w, const float* u,
+                            const void* k, const void* v, const void* r, const float* ck,
+                            void* gk, void* gv, void* gr, float* gtd, float* gtf, void* ws, int B,
+                            int T, int C, hipStream_t stream) {
+  using raw = typename E::raw;
+  constexpr int CPW = 64 * VEC;
+  const int n_cg = (C + CPW - 1) / CPW;
+  const int rows = B * n_cg;
+  const int nseg = (T + L * W - 1) / (L * W);
+  const size_t b_bytes = round16(wkv4_partials_floats(B, C) * 4);
+  const size_t seg_bytes = round16(wkv4_partials_floats(int64_t(B) * nseg, C) * 4);
+  float* gw_b = static_cast<float*>(ws);
+  float* gu_b = gw_b + size_t(B) * C;
+  float* gw_part = reinterpret_cast<float*>(static_cast<char*>(ws) + b_bytes);
+  float* gu_part = gw_part + size_t(B) * nseg * C;
+  uint64_t* lb = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + b_bytes + seg_bytes);
+  const size_t words = size_t(2) * nseg * rows * CPW;
+  uint32_t* status = reinterpret_cast<uint32_t*>(lb + words);
+  if (int rc = lb_fill(lb, words * 8 + round16(size_t(rows) * 4), stream)) return rc;
+  const raw* g_ = static_cast<const raw*>(gy);
+  const raw* k_ = static_cast<const raw*>(k);
+  const raw* v_ = static_cast<const raw*>(v);
+  const raw* r_ = static_cast<const raw*>(r);
+  raw* gk_ = static_cast<raw*>(gk);
+  raw* gv_ = static_cast<raw*>(gv);
+  raw* gr_ = static_cast<raw*>(gr);
+  const dim3 grid(unsigned(nseg) * unsigned(rows)), block(W * 64);
+  if (r != nullptr) {
+    launch(wkv::wkv4_bwd_split_kernel<E, VEC, L, W, true>, grid, block, stream, false, g_, decay,
+           decay_is_w, u, k_, v_, r_, ck, gk_, gv_, gr_, gw_part, gu_part, lb, status, rows, T, C);
+  } else {
+    launch(wkv::wkv4_bwd_split_kernel<E, VEC, L, W, false>, grid, block, stream, false, g_, decay,
+           decay_is_w, u, k_, v_, r_, ck, gk_, gv_, static_cast<raw*>(nullptr), gw_part, gu_part,
+           lb, status, rows, T, C);
+  }
+  if (int rc = check_launch("wkv4_bwd_split_kernel")) return rc;
+  if (r != nullptr) {
+    launch(wkv::wkv4_bwd_fixup_kernel<E, true>, dim3(rows), dim3(64), stream, false, g_, decay,
+           decay_is_w, u, k_, v_, r_, ck, gk_, gv_, gr_, gw_part, gu_part, gw_b, gu_b, status,
+           CPW, n_cg, nseg, T, C);
+  } else {
+    launch(wkv::wkv4_bwd_fixup_kernel<E, false>, dim3(rows), dim3(64), stream, false, g_, decay,
+           decay_is_w, u, k_, v_, r_, ck, gk_, gv_, static_cast<raw*>(nullptr), gw_part, gu_part,
+           gw_b, gu_b, status, CPW, n_cg, nseg, T, C);
+  }
+  if (int rc = check_launch("wkv4_bwd_fixup_kernel")) return rc;
+  launch(wkv::wkv4_param_grad_kernel, dim3((C + 63) / 64), dim3(1024), stream, true, gw_b, gu_b,
+         decay, decay_is_w, gtd, gtf, B, C);
+  return check_launch("wkv4_param_grad_kernel");
+}
+
+// ws: the workspace (at least the [2][B][C] partials); the split kernel runs
+// when it is eligible and ws holds its workspace.
 template <typename E>
 static int dispatch_bwd(const void* gy, const float* decay, int decay_is_w, const float* u,
                         const void* k, const void* v, const void* r, const float* ck, void* gk,
-                        void* gv, void* gr, float* gtd, float* gtf, float* partials, int B,
-                        int T, int C, hipStream_t stream) {
+                        void* gv, void* gr, float* gtd, float* gtf, void* ws, size_t ws_bytes,
+                        int B, int T, int C, hipStream_t stream) {
+  const TileCfg sc = pick_bwd_split_cfg(B, T, C);
+  if (sc.vec != 0 && ws_bytes >= split_bwd_bytes(sc, B, T, C)) {
+#define WKV_BWD_SPLIT_CASE(V, LL, WW)                                                        \
+  if (sc.vec == V && sc.L == LL && sc.W == WW)                                              \
+    return launch_bwd_split<E, V, LL, WW>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, \
+                                          gtd, gtf, ws, B, T, C, stream);
+    WKV_BWD_SPLIT_CASE(1, 8, 8)
+    WKV_BWD_SPLIT_CASE(1, 16, 4)
+    WKV_BWD_SPLIT_CASE(1, 8, 16)
+    WKV_BWD_SPLIT_CASE(2, 8, 8)
+    WKV_BWD_SPLIT_CASE(1, 4, 16)
+    WKV_BWD_SPLIT_CASE(2, 4, 16)
+#undef WKV_BWD_SPLIT_CASE
+  }
+  float* partials = static_cast<float*>(ws);
   const TileCfg cfg = pick_bwd_cfg(B, C, int(sizeof(typename E::raw)));
 #define WKV_BWD_CASE(V, LL, WW)                                                                \
   if (cfg.vec == V && cfg.L == LL && cfg.W == WW)                                              \
@@ -684,18 +1072,18 @@ static int dispatch_bwd(const void* gy, const float* decay, int decay_is_w, cons
 
 static int backward_any(const void* gy, const float* decay, int decay_is_w, const float* u,
                         const void* k, const void* v, const void* r, const float* ck, void* gk,
-                        void* gv, void* gr, float* gtd, float* gtf, float* partials, int B,
-                        int T, int C, int dtype, hipStream_t stream) {
+                        void* gv, void* gr, float* gtd, float* gtf, void* ws, size_t ws_bytes,
+                        int B, int T, int C, int dtype, hipStream_t stream) {
   switch (dtype) {
     case 0:
       return dispatch_bwd<wkv::F32>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf,
-                                    partials, B, T, C, stream);
+                                    ws, ws_bytes, B, T, C, stream);
     case 1:
       return dispatch_bwd<wkv::BF16>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf,
-                                     partials, B, T, C, stream);
+                                     ws, ws_bytes, B, T, C, stream);
     case 2:
       return dispatch_bwd<wkv::F16>(gy, decay, decay_is_w, u, k, v, r, ck, gk, gv, gr, gtd, gtf,
-                                    partials, B, T, C, stream);
+                                    ws, ws_bytes, B, T, C, stream);
     default:
       return fail(1, "wkv4_backward: unknown dtype");
   }
@@ -704,10 +1092,10 @@ static int backward_any(const void* gy, const float* decay, int decay_is_w, cons
 // Backward from checkpoint records ck (written by the forward kernel).
 int wkv4_backward_ck_impl(const void* gy, const float* decay, int decay_is_w, const float* u,
                           const void* k, const void* v, const float* ck, void* gk, void* gv,
-                          float* gtd, float* gtf, float* partials, int B, int T, int C, int dtype,
-                          hipStream_t stream) {
-  return backward_any(gy, decay, decay_is_w, u, k, v, nullptr, ck, gk, gv, nullptr, gtd, gtf,
-                      partials, B, T, C, dtype, stream);
+                          float* gtd, float* gtf, void* ws, size_t ws_bytes, int B, int T, int C,
+                          int dtype, hipStream_t stream) {
+  return backward_any(gy, decay, decay_is_w, u, k, v, nullptr, ck, gk, gv, nullptr, gtd, gtf, ws,
+                      ws_bytes, B, T, C, dtype, stream);
 }
 
 // The gated backward from checkpoint records: g is the gradient of
@@ -715,33 +1103,45 @@ int wkv4_backward_ck_impl(const void* gy, const float* decay, int decay_is_w, co
 // parameter gradients.
 int wkv4_backward_gated_ck_impl(const void* g, const float* decay, const float* u, const void* k,
                                 const void* v, const void* r, const float* ck, void* gk,
-                                void* gv, void* gr, float* gtd, float* gtf, float* partials,
-                                int B, int T, int C, int dtype, hipStream_t stream) {
-  return backward_any(g, decay, 0, u, k, v, r, ck, gk, gv, gr, gtd, gtf, partials, B, T, C, dtype,
-                      stream);
+                                void* gv, void* gr, float* gtd, float* gtf, void* ws,
+                                size_t ws_bytes, int B, int T, int C, int dtype,
+                                hipStream_t stream) {
+  return backward_any(g, decay, 0, u, k, v, r, ck, gk, gv, gr, gtd, gtf, ws, ws_bytes, B, T, C,
+                      dtype, stream);
+}
+
+// Workspace of wkv4_backward_impl: the checkpoint records, then what the
+// forward (split) and the backward from the records need (used one after the
+// other, so they share the space).  The minimum: records and the one-row
+// kernels' partials.
+size_t wkv4_bwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C, int dtype) {
+  (void)dtype;
+  return round16(wkv4_checkpoint_floats(B, T, C) * 4) +
+         std::max(wkv4_fwd_workspace_bytes_impl(B, T, C), wkv4_bwd_ck_workspace_bytes_impl(B, T, C));
+}
+
+size_t wkv4_bwd_min_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
+  return round16(wkv4_checkpoint_floats(B, T, C) * 4) + round16(wkv4_partials_floats(B, C) * 4);
 }
 
 // Backward from the inputs alone: the forward kernel writes the checkpoint
 // records (no y) into the workspace, then the reverse sweep runs.
 int wkv4_backward_impl(const void* gy, const float* w, const float* u, const void* k,
-                       const void* v, void* gk, void* gv, float* gtd, float* gtf, float* ws,
-                       int B, int T, int C, int dtype, hipStream_t stream) {
-  float* ck = ws;
-  float* partials = ws + wkv4_checkpoint_floats(B, T, C);
+                       const void* v, void* gk, void* gv, float* gtd, float* gtf, void* ws,
+                       size_t ws_bytes, int B, int T, int C, int dtype, hipStream_t stream) {
+  const size_t ck_bytes = round16(wkv4_checkpoint_floats(B, T, C) * 4);
+  float* ck = static_cast<float*>(ws);
+  void* rest = static_cast<char*>(ws) + ck_bytes;
+  const size_t rest_bytes = ws_bytes - ck_bytes;
   // The forward stage does not end the call: it carries no stop event.
   CallEvents& ev = active_events();
   hipEvent_t stop = ev.stop;
-  ev.stop = nullptr;
-  int rc = wkv4_forward_impl(k, v, w, 1, u, nullptr, ck, B, T, C, dtype, stream);
+  if (ev.kernel < 0) ev.stop = nullptr;
+  int rc = wkv4_forward_impl(k, v, w, 1, u, nullptr, ck, rest, rest_bytes, B, T, C, dtype, stream);
   ev.stop = stop;
   if (rc) return rc;
-  return wkv4_backward_ck_impl(gy, w, 1, u, k, v, ck, gk, gv, gtd, gtf, partials, B, T, C, dtype,
-                               stream);
-}
-
-size_t wkv4_bwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C, int dtype) {
-  (void)dtype;
-  return (wkv4_checkpoint_floats(B, T, C) + wkv4_partials_floats(B, C)) * sizeof(float) + 256;
+  return wkv4_backward_ck_impl(gy, w, 1, u, k, v, ck, gk, gv, gtd, gtf, rest, rest_bytes, B, T, C,
+                               dtype, stream);
 }
 
 int wkv4_zero_param_grads(float* gtd, float* gtf, int C, hipStream_t stream) {

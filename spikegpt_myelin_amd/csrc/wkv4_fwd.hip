@@ -44,7 +44,10 @@
 // recomputed by the reference's running-max recurrence, one channel per
 // thread.  Inputs whose keys stay inside +-30 (the benchmark's clamp) never
 // take that path.
+#include <algorithm>
+
 #include "wkv_common.h"
+#include "wkv_impl.h"
 
 namespace wkv {
 
@@ -95,20 +98,15 @@ struct Fwd {
     }
   }
 
-  // One segment.  FULL: every step of the segment is inside the sequence.
-  // Returns true when the range guard rejects the row (workgroup-uniform).
+  // Phase 1 of a chunk (L steps from t0): e = 2^{k log2e} of every step
+  // (zero past T) and the chunk's summary (ps, qs) from a zero state.
+  // Returns whether a key of the chunk is outside the fixed frame's range.
   template <bool FULL>
-  __device__ static __forceinline__ bool segment(
-      Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
-      size_t row_tail, unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
-      unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L],
-      const PackT (&rb)[L], const float (&D)[VEC], const float (&DL)[VEC],
-      const float (&U)[VEC]) {
-    const int t0 = seg * SEG + wave * L;
-    const int par = seg & 1;
-    // Phase 1: e = 2^{k log2e} and the chunk summary from a zero state.
-    float s[L][VEC];
-    float ps[VEC], qs[VEC], mk[VEC];
+  __device__ static __forceinline__ bool summarize(int t0, int T, const PackT (&kb)[L],
+                                                   const PackT (&vb)[L], const float (&D)[VEC],
+                                                   float (&s)[L][VEC], float (&ps)[VEC],
+                                                   float (&qs)[VEC]) {
+    float mk[VEC];
 #pragma unroll
     for (int c = 0; c < VEC; ++c) { ps[c] = 0.f; qs[c] = 0.f; mk[c] = 0.f; }
 #pragma unroll
@@ -127,29 +125,18 @@ struct Fwd {
     }
     bool bad = false;
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      bad |= mk[c] * kLog2e > kMaxK;
-      sm.p[par][c][wave][lane] = ps[c];
-      sm.q[par][c][wave][lane] = qs[c];
-    }
-    if (__any(active && bad) && lane == 0) sm.bad = 1;
-    __syncthreads();
-    if (sm.bad) return true;
+    for (int c = 0; c < VEC; ++c) bad |= mk[c] * kLog2e > kMaxK;
+    return bad;
+  }
 
-    // Carry-in of this chunk: segment carry, then the earlier chunks.
-    float pin[VEC], qin[VEC];
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      pin[c] = seg > 0 ? sm.carry[par ^ 1][0][c][lane] : 0.f;
-      qin[c] = seg > 0 ? sm.carry[par ^ 1][1][c][lane] : 0.f;
-    }
-    for (int w = 0; w < wave; ++w) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        pin[c] = fmaf(pin[c], DL[c], sm.p[par][c][w][lane]);
-        qin[c] = fmaf(qin[c], DL[c], sm.q[par][c][w][lane]);
-      }
-    }
+  // Phase 2 of a chunk from its carry-in (pin, qin): the checkpoint record
+  // when the chunk starts a 64-step block, then the outputs.
+  __device__ static __forceinline__ void emit(
+      int t0, int T, int C, int wave, bool active, size_t row_base, size_t row_tail,
+      unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
+      unsigned ck_boff, size_t ck_field, const float (&s)[L][VEC], const PackT (&vb)[L],
+      const PackT (&rb)[L], const float (&D)[VEC], const float (&U)[VEC], float (&pin)[VEC],
+      float (&qin)[VEC]) {
     if (ck != nullptr && wave % CPB == 0 && active && t0 < T) {
       const float zero[VEC] = {};
       float* rec = ck + ck_row + size_t(t0 / kCkptBlock) * C;
@@ -157,15 +144,6 @@ struct Fwd {
       store_vec<F32, VEC>(byte_offset(rec + 1 * ck_field, ck_boff), pin);
       store_vec<F32, VEC>(byte_offset(rec + 2 * ck_field, ck_boff), qin);
     }
-    if (wave == W - 1) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        sm.carry[par][0][c][lane] = fmaf(pin[c], DL[c], ps[c]);
-        sm.carry[par][1][c][lane] = fmaf(qin[c], DL[c], qs[c]);
-      }
-    }
-
-    // Phase 2: outputs.
     if constexpr (WY) {
       OutPack<E, VEC> yp[L];
 #pragma unroll
@@ -198,6 +176,54 @@ struct Fwd {
         for (int i = 0; i < L; ++i) store_buf(yp[i], ry, lane_boff, unsigned(i) * stride);
       }
     }
+  }
+
+  // One segment.  FULL: every step of the segment is inside the sequence.
+  // Returns true when the range guard rejects the row (workgroup-uniform).
+  template <bool FULL>
+  __device__ static __forceinline__ bool segment(
+      Smem& sm, int seg, int T, int C, int wave, int lane, bool active, size_t row_base,
+      size_t row_tail, unsigned lane_boff, raw* __restrict__ y, float* __restrict__ ck, size_t ck_row,
+      unsigned ck_boff, size_t ck_field, const PackT (&kb)[L], const PackT (&vb)[L],
+      const PackT (&rb)[L], const float (&D)[VEC], const float (&DL)[VEC],
+      const float (&U)[VEC]) {
+    const int t0 = seg * SEG + wave * L;
+    const int par = seg & 1;
+    float s[L][VEC];
+    float ps[VEC], qs[VEC];
+    const bool bad = summarize<FULL>(t0, T, kb, vb, D, s, ps, qs);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      sm.p[par][c][wave][lane] = ps[c];
+      sm.q[par][c][wave][lane] = qs[c];
+    }
+    if (__any(active && bad) && lane == 0) sm.bad = 1;
+    __syncthreads();
+    if (sm.bad) return true;
+
+    // Carry-in of this chunk: segment carry, then the earlier chunks.
+    float pin[VEC], qin[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      pin[c] = seg > 0 ? sm.carry[par ^ 1][0][c][lane] : 0.f;
+      qin[c] = seg > 0 ? sm.carry[par ^ 1][1][c][lane] : 0.f;
+    }
+    for (int w = 0; w < wave; ++w) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        pin[c] = fmaf(pin[c], DL[c], sm.p[par][c][w][lane]);
+        qin[c] = fmaf(qin[c], DL[c], sm.q[par][c][w][lane]);
+      }
+    }
+    if (wave == W - 1) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        sm.carry[par][0][c][lane] = fmaf(pin[c], DL[c], ps[c]);
+        sm.carry[par][1][c][lane] = fmaf(qin[c], DL[c], qs[c]);
+      }
+    }
+    emit(t0, T, C, wave, active, row_base, row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field,
+         s, vb, rb, D, U, pin, qin);
     return false;
   }
 };
@@ -334,21 +360,190 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   }
 }
 
+// ----------------------------------------------------- split over time ----
+// For few rows (B * ceil(C / 64) below the CU count) the one-row kernel
+// leaves CUs idle.  Here a workgroup owns one segment (W chunks of L steps)
+// of one row: blockIdx = segment * rows + row, so every row's segment s is
+// dispatched before segment s+1.  The workgroup reduces its segment to its
+// aggregate -- the state change over the segment from a zero state, the
+// Horner fold of its chunk summaries -- and publishes it.  Its carry-in is
+// the state at the segment's start,
+//   carry_s = sum_{j<s} e^{(s-1-j) SEG w} agg_j = e^{K SEG w} incl_{s-K-1}
+//             + sum_{j=s-K}^{s-1} e^{(s-1-j) SEG w} agg_j,
+// taken from the K = kLbWindow previous segments' aggregates and the
+// inclusive state incl_{s-K-1} (the state at the end of that segment), the
+// same words on every run (lb_window_carry), so the result is deterministic.
+// It then publishes incl_s = e^{SEG w} carry_s + agg_s and runs its segment
+// from registers as the one-row kernel does.  k, v are read once, y written
+// once; the carries are 16 bytes per channel and segment.  Waits only go to
+// lower block indices, and every wait is bounded (kLbMaxPolls): a workgroup
+// that gives up marks its row, and the fix-up kernel that follows recomputes
+// marked rows exactly, as it does rows whose keys leave the fixed frame's
+// range.
+//
+// Look-back words: lb[2][nseg][rows][64*VEC] (aggregates, then inclusive
+// states), each word the pair (p, q) of one channel; status[rows] (kRowOk, or
+// kRowRedo for a row the fix-up kernel recomputes).
+template <typename E, int VEC, int L, int W, bool WY, bool GATE>
+__global__ __launch_bounds__(W * 64) void wkv4_fwd_split_kernel(
+    const typename E::raw* __restrict__ k, const typename E::raw* __restrict__ v,
+    const float* __restrict__ decay, int decay_is_w, const float* __restrict__ time_first,
+    const typename E::raw* __restrict__ r, typename E::raw* __restrict__ y,
+    float* __restrict__ ck, uint64_t* __restrict__ lb, uint32_t* __restrict__ status, int rows,
+    int T, int C) {
+  using F = Fwd<E, VEC, L, W, WY, GATE>;
+  using PackT = typename F::PackT;
+  __shared__ typename F::Smem sm;
+
+  const int nseg = (T + F::SEG - 1) / F::SEG;
+  const int seg = __builtin_amdgcn_readfirstlane(int(blockIdx.x) / rows);
+  const int row = int(blockIdx.x) - seg * rows;
+  const int n_cg = (C + F::CPW - 1) / F::CPW;
+  const int b = row / n_cg;
+  const int cg = row - b * n_cg;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c0 = cg * F::CPW + lane * VEC;
+  const bool active = c0 < C;
+  const size_t row_base = size_t(b) * T * C + size_t(cg) * F::CPW;
+  const size_t row_tail = size_t(T) * C - size_t(cg) * F::CPW;
+  const unsigned lane_boff = active ? unsigned(lane * VEC * sizeof(typename E::raw)) : 0u;
+  const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
+  const size_t ck_field = size_t(rows / n_cg) * nblk * C;  // B * nblk * C
+  const size_t ck_row = size_t(b) * nblk * C + size_t(cg) * F::CPW;
+  const unsigned ck_boff = active ? unsigned(lane * VEC * sizeof(float)) : 0u;
+  const int t0 = seg * F::SEG + wave * L;
+
+  PackT kb[L], vb[L], rb[L];
+  F::load_chunk(k, v, r, row_base, row_tail, lane_boff, t0, C, kb, vb, rb);
+
+  float D[VEC], DL[VEC], DS[VEC], U[VEC];
+  bool u_ok = true;
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    const float dv = active ? decay[c0 + c] : 0.f;
+    const float tf = active ? time_first[c0 + c] : 0.f;
+    const float w2 = (decay_is_w ? dv : -expf(dv)) * kLog2e;
+    const float u2 = tf * kLog2e;
+    D[c] = fast_exp2(w2);
+    DL[c] = fast_exp2(w2 * float(L));
+    DS[c] = fast_exp2(w2 * float(F::SEG));
+    U[c] = fast_exp2(u2);
+    u_ok &= fabsf(u2) <= kMaxU;
+  }
+  if (threadIdx.x == 0) sm.bad = 0;
+  const bool u_bad = __syncthreads_or(!u_ok) != 0;
+
+  float s[L][VEC];
+  float ps[VEC], qs[VEC];
+  const bool full = (seg + 1) * F::SEG <= T;
+  const bool kbad = full ? F::template summarize<true>(t0, T, kb, vb, D, s, ps, qs)
+                         : F::template summarize<false>(t0, T, kb, vb, D, s, ps, qs);
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    sm.p[0][c][wave][lane] = ps[c];
+    sm.q[0][c][wave][lane] = qs[c];
+  }
+  if (__any(active && kbad) && lane == 0) sm.bad = 1;
+  __syncthreads();
+  const bool bad = u_bad || sm.bad != 0;
+
+  const size_t plane = size_t(nseg) * rows * F::CPW;  // words per kind
+  uint64_t* const mine = lb + (size_t(seg) * rows + row) * F::CPW + lane * VEC;
+  if (wave == 0) {
+    if (bad) {
+      // Out of the fixed frame's range: publish placeholders (successors
+      // must not wait) and leave the row to the fix-up kernel.
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        lb_store(mine + c, kLbNaN);
+        lb_store(mine + plane + c, kLbNaN);
+      }
+      if (lane == 0) mark_row_redo(status, row);
+    } else {
+      float ap[VEC], aq[VEC];
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) { ap[c] = 0.f; aq[c] = 0.f; }
+      for (int w = 0; w < W; ++w) {
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+          ap[c] = fmaf(ap[c], DL[c], sm.p[0][c][w][lane]);
+          aq[c] = fmaf(aq[c], DL[c], sm.q[0][c][w][lane]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) lb_store(mine + c, lb_pack(ap[c], aq[c]));
+      float cp[VEC], cq[VEC];
+      const uint64_t* base = lb + size_t(row) * F::CPW + lane * VEC;
+      const bool gave_up = !lb_window_carry<VEC>(base, base + plane, size_t(rows) * F::CPW, seg,
+                                                 nseg, +1, DS, cp, cq);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        lb_store(mine + plane + c, lb_pack(fmaf(cp[c], DS[c], ap[c]), fmaf(cq[c], DS[c], aq[c])));
+        sm.carry[0][0][c][lane] = cp[c];
+        sm.carry[0][1][c][lane] = cq[c];
+      }
+      if (__any(gave_up) && lane == 0) mark_row_redo(status, row);
+    }
+  }
+  __syncthreads();
+  if (bad) return;
+
+  // Carry-in of this chunk: the segment's carry, then the earlier chunks.
+  float pin[VEC], qin[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    pin[c] = sm.carry[0][0][c][lane];
+    qin[c] = sm.carry[0][1][c][lane];
+  }
+  for (int w = 0; w < wave; ++w) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      pin[c] = fmaf(pin[c], DL[c], sm.p[0][c][w][lane]);
+      qin[c] = fmaf(qin[c], DL[c], sm.q[0][c][w][lane]);
+    }
+  }
+  F::emit(t0, T, C, wave, active, row_base, row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field,
+          s, vb, rb, D, U, pin, qin);
+}
+
+// Rows a split forward marked (keys outside the fixed frame's range, or a
+// look-back that gave up): recomputed with the running-max recurrence, one
+// channel per thread, overwriting y and the records.  One wave per row; an
+// unmarked row returns at once.
+template <typename E, bool WY, bool GATE>
+__global__ __launch_bounds__(64) void wkv4_fwd_fixup_kernel(
+    const typename E::raw* __restrict__ k, const typename E::raw* __restrict__ v,
+    const float* __restrict__ decay, int decay_is_w, const float* __restrict__ time_first,
+    const typename E::raw* __restrict__ r, typename E::raw* __restrict__ y,
+    float* __restrict__ ck, const uint32_t* __restrict__ status, int cpw, int n_cg, int T,
+    int C) {
+  const int row = blockIdx.x;
+  if (status[row] == kRowOk) return;
+  const int b = row / n_cg;
+  const int cg = row - b * n_cg;
+  const int nblk = (T + kCkptBlock - 1) / kCkptBlock;
+  const size_t ck_field = size_t(gridDim.x / n_cg) * nblk * C;
+  for (int ch = threadIdx.x; ch < cpw; ch += 64) {
+    const int c = cg * cpw + ch;
+    if (c >= C) continue;
+    const float w2 = (decay_is_w ? decay[c] : -expf(decay[c])) * kLog2e;
+    const float u2 = time_first[c] * kLog2e;
+    wkv4_fwd_channel_serial<E>(k, v, GATE ? r : nullptr, WY ? y : nullptr, w2, u2, T, C,
+                               size_t(b) * T * C + c, ck, size_t(b) * nblk * C + c, ck_field);
+  }
+}
+
 }  // namespace wkv
 
 // ------------------------------------------------------------ launcher ----
 namespace wkv_host {
-
-struct TileCfg { int vec, L, W; };
 
 // Tile configurations compiled into the library (no VGPR spills at 64*W
 // threads per workgroup).  SEG = W*L must be a multiple of the 64-step
 // checkpoint block.
 static constexpr TileCfg kFwdCfgs[] = {{2, 8, 16}, {1, 8, 16}, {2, 8, 8}, {1, 16, 8}, {1, 8, 8},
                                         {1, 16, 4}, {2, 16, 4}};
-
-int pick_vec(int64_t B, int64_t C);
-bool env_cfg(const char* name, int& vec, int& L, int& W);
 
 // fp32 tensors already give 4-byte lane loads at one channel per lane; the
 // 16-bit types use two channels per lane when the batch fills the GPU.
@@ -360,6 +555,102 @@ static TileCfg pick_fwd_cfg(int64_t B, int64_t C, int elem_bytes) {
   }
   if (elem_bytes == 2 && pick_vec(B, C) == 2) return TileCfg{2, 8, 16};
   return TileCfg{1, 8, 16};
+}
+
+// ------------------------------------------------ split over time (host) --
+// Tile configurations of the split kernel (SEG = W*L steps per workgroup,
+// a multiple of the 64-step record block).
+static constexpr TileCfg kFwdSplitCfgs[] = {{1, 8, 8}, {1, 8, 16}, {1, 16, 4}, {2, 8, 8},
+                                             {1, 4, 16}, {2, 4, 16}};
+
+// The split kernel runs when the one-row kernel would leave CUs idle: fewer
+// than kSplitRows rows of 64 channels and at least two segments.
+// WKV_SPLIT=0 / 1 forces it off / on (measurement); WKV_FWD_SPLIT_CFG picks
+// the tile.  Returns {0, 0, 0} when the one-row kernel runs.
+int split_mode() {
+  const char* s = getenv("WKV_SPLIT");
+  return s ? atoi(s) : -1;
+}
+
+static TileCfg pick_fwd_split_cfg(int64_t B, int64_t T, int64_t C) {
+  TileCfg cfg{1, 16, 4};
+  int vec, L, W;
+  if (env_cfg("WKV_FWD_SPLIT_CFG", vec, L, W)) {
+    for (const TileCfg& c : kFwdSplitCfgs)
+      if (c.vec == vec && c.L == L && c.W == W && (vec == 1 || C % 2 == 0)) cfg = c;
+  }
+  const int64_t rows1 = B * ((C + 63) / 64);
+  const int64_t nseg = (T + cfg.L * cfg.W - 1) / (cfg.L * cfg.W);
+  const int mode = split_mode();
+  const bool want = mode == 1 || (mode != 0 && rows1 < kSplitRows && nseg >= kSplitMinSegs &&
+                                       B * T * C >= kSplitMinElems);
+  if (!want || nseg < 2 || B == 0 || C == 0) return TileCfg{0, 0, 0};
+  return cfg;
+}
+
+// Workspace of the split forward: look-back words, then the row status words.
+static size_t split_fwd_bytes(const TileCfg& cfg, int64_t B, int64_t T, int64_t C) {
+  const int64_t cpw = 64 * cfg.vec;
+  const int64_t rows = B * ((C + cpw - 1) / cpw);
+  const int64_t nseg = (T + cfg.L * cfg.W - 1) / (cfg.L * cfg.W);
+  const size_t words = size_t(2) * size_t(nseg) * size_t(rows) * size_t(cpw);
+  return words * 8 + ((size_t(rows) * 4 + 15) / 16) * 16;
+}
+
+size_t wkv4_fwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
+  const TileCfg cfg = pick_fwd_split_cfg(B, T, C);
+  return cfg.vec == 0 ? 0 : split_fwd_bytes(cfg, B, T, C);
+}
+
+// Fills `bytes` (a multiple of 16) of look-back workspace with all ones.
+int lb_fill(void* ws, size_t bytes, hipStream_t stream) {
+  const size_t n16 = bytes / 16;
+  const unsigned blocks = unsigned(std::min<size_t>((n16 + 255) / 256, 4096));
+  launch(wkv::lb_fill_kernel<0>, dim3(blocks), dim3(256), stream, false,
+         static_cast<wkv::u32x4*>(ws), n16);
+  return check_launch("lb_fill_kernel");
+}
+
+template <typename E, int VEC, int L, int W>
+static int launch_fwd_split(const void* k, const void* v, const float* decay, int decay_is_w,
+                            const float* tf, const void* r, void* y, float* ck, void* ws,
+                            size_t ws_bytes, int B, int T, int C, hipStream_t stream) {
+  using raw = typename E::raw;
+  constexpr int CPW = 64 * VEC;
+  const int n_cg = (C + CPW - 1) / CPW;
+  const int rows = B * n_cg;
+  const int nseg = (T + L * W - 1) / (L * W);
+  const size_t words = size_t(2) * nseg * rows * CPW;
+  uint64_t* lb = static_cast<uint64_t*>(ws);
+  uint32_t* status = reinterpret_cast<uint32_t*>(lb + words);
+  if (int rc = lb_fill(ws, ws_bytes, stream)) return rc;
+  const raw* kk = static_cast<const raw*>(k);
+  const raw* vv = static_cast<const raw*>(v);
+  const raw* rr = static_cast<const raw*>(r);
+  raw* yy = static_cast<raw*>(y);
+  const dim3 grid(unsigned(nseg) * unsigned(rows)), block(W * 64);
+  if (r != nullptr) {
+    launch(wkv::wkv4_fwd_split_kernel<E, VEC, L, W, true, true>, grid, block, stream, false, kk,
+           vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C);
+  } else if (y != nullptr) {
+    launch(wkv::wkv4_fwd_split_kernel<E, VEC, L, W, true, false>, grid, block, stream, false, kk,
+           vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C);
+  } else {
+    launch(wkv::wkv4_fwd_split_kernel<E, VEC, L, W, false, false>, grid, block, stream, false,
+           kk, vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C);
+  }
+  if (int rc = check_launch("wkv4_fwd_split_kernel")) return rc;
+  if (r != nullptr) {
+    launch(wkv::wkv4_fwd_fixup_kernel<E, true, true>, dim3(rows), dim3(64), stream, true, kk, vv,
+           decay, decay_is_w, tf, rr, yy, ck, status, CPW, n_cg, T, C);
+  } else if (y != nullptr) {
+    launch(wkv::wkv4_fwd_fixup_kernel<E, true, false>, dim3(rows), dim3(64), stream, true, kk, vv,
+           decay, decay_is_w, tf, rr, yy, ck, status, CPW, n_cg, T, C);
+  } else {
+    launch(wkv::wkv4_fwd_fixup_kernel<E, false, false>, dim3(rows), dim3(64), stream, true, kk,
+           vv, decay, decay_is_w, tf, rr, yy, ck, status, CPW, n_cg, T, C);
+  }
+  return check_launch("wkv4_fwd_fixup_kernel");
 }
 
 // r (GATE) requires y.
@@ -388,8 +679,23 @@ static int launch_fwd(const void* k, const void* v, const float* decay, int deca
 
 template <typename E>
 static int dispatch_fwd(const void* k, const void* v, const float* decay, int decay_is_w,
-                        const float* tf, const void* r, void* y, float* ck, int B, int T, int C,
-                        hipStream_t stream) {
+                        const float* tf, const void* r, void* y, float* ck, void* ws,
+                        size_t ws_bytes, int B, int T, int C, hipStream_t stream) {
+  const TileCfg sc = pick_fwd_split_cfg(B, T, C);
+  if (sc.vec != 0 && ws != nullptr && ws_bytes >= split_fwd_bytes(sc, B, T, C)) {
+    const size_t need = split_fwd_bytes(sc, B, T, C);
+#define WKV_FWD_SPLIT_CASE(V, LL, WW)                                                        \
+  if (sc.vec == V && sc.L == LL && sc.W == WW)                                              \
+    return launch_fwd_split<E, V, LL, WW>(k, v, decay, decay_is_w, tf, r, y, ck, ws, need, B, \
+                                          T, C, stream);
+    WKV_FWD_SPLIT_CASE(1, 8, 8)
+    WKV_FWD_SPLIT_CASE(1, 8, 16)
+    WKV_FWD_SPLIT_CASE(1, 16, 4)
+    WKV_FWD_SPLIT_CASE(2, 8, 8)
+    WKV_FWD_SPLIT_CASE(1, 4, 16)
+    WKV_FWD_SPLIT_CASE(2, 4, 16)
+#undef WKV_FWD_SPLIT_CASE
+  }
   TileCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
   // The gated kernel holds the receptance chunks as well: at 16 waves per
   // workgroup (128 VGPRs) the two-channel tile spills, so it runs 8 waves.
@@ -409,27 +715,35 @@ static int dispatch_fwd(const void* k, const void* v, const float* decay, int de
 }
 
 static int forward_any(const void* k, const void* v, const float* decay, int decay_is_w,
-                       const float* tf, const void* r, void* y, float* ck, int B, int T, int C,
-                       int dtype, hipStream_t stream) {
+                       const float* tf, const void* r, void* y, float* ck, void* ws,
+                       size_t ws_bytes, int B, int T, int C, int dtype, hipStream_t stream) {
   switch (dtype) {
-    case 0: return dispatch_fwd<wkv::F32>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
-    case 1: return dispatch_fwd<wkv::BF16>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
-    case 2: return dispatch_fwd<wkv::F16>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);
+    case 0:
+      return dispatch_fwd<wkv::F32>(k, v, decay, decay_is_w, tf, r, y, ck, ws, ws_bytes, B, T, C,
+                                    stream);
+    case 1:
+      return dispatch_fwd<wkv::BF16>(k, v, decay, decay_is_w, tf, r, y, ck, ws, ws_bytes, B, T, C,
+                                     stream);
+    case 2:
+      return dispatch_fwd<wkv::F16>(k, v, decay, decay_is_w, tf, r, y, ck, ws, ws_bytes, B, T, C,
+                                    stream);
     default: return fail(1, "wkv4_forward: unknown dtype");
   }
 }
 
+// ws (may be null): workspace for the split kernel, wkv4_fwd_workspace_bytes_impl bytes.
 int wkv4_forward_impl(const void* k, const void* v, const float* decay, int decay_is_w,
-                      const float* tf, void* y, float* ck, int B, int T, int C, int dtype,
-                      hipStream_t stream) {
-  return forward_any(k, v, decay, decay_is_w, tf, nullptr, y, ck, B, T, C, dtype, stream);
+                      const float* tf, void* y, float* ck, void* ws, size_t ws_bytes, int B,
+                      int T, int C, int dtype, hipStream_t stream) {
+  return forward_any(k, v, decay, decay_is_w, tf, nullptr, y, ck, ws, ws_bytes, B, T, C, dtype,
+                     stream);
 }
 
 // y = sigmoid(r) * wkv (the time mix's gate folded in); y must be given.
 int wkv4_forward_gated_impl(const void* k, const void* v, const float* decay, const float* tf,
-                            const void* r, void* y, float* ck, int B, int T, int C, int dtype,
-                            hipStream_t stream) {
-  return forward_any(k, v, decay, 0, tf, r, y, ck, B, T, C, dtype, stream);
+                            const void* r, void* y, float* ck, void* ws, size_t ws_bytes, int B,
+                            int T, int C, int dtype, hipStream_t stream) {
+  return forward_any(k, v, decay, 0, tf, r, y, ck, ws, ws_bytes, B, T, C, dtype, stream);
 }
 
 }  // namespace wkv_host

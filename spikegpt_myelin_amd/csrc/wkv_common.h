@@ -294,13 +294,16 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 
-// Timing events of the entry point running on this thread (armed by
-// wkv_time_next_call): the first kernel dispatch of the call carries `start`
-// and the dispatch that ends the call carries `stop`.  Both stay null outside
-// a timed call.
+// Timing events of the entry point running on this thread.  Armed by
+// wkv_time_next_call (kernel < 0): the first kernel dispatch of the call
+// carries `start` and the dispatch that ends the call carries `stop`; or by
+// wkv_time_next_kernel: dispatch number `kernel` of the call carries both.
+// `count` numbers the call's dispatches.  All null outside a timed call.
 struct CallEvents {
   hipEvent_t start = nullptr;
   hipEvent_t stop = nullptr;
+  int kernel = -1;
+  int count = 0;
 };
 CallEvents& active_events();
 
@@ -312,11 +315,19 @@ template <typename... KArgs, typename... Args>
 void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream, bool ends_call,
             Args... args) {
   CallEvents& ev = active_events();
-  hipEvent_t stop = ends_call ? ev.stop : nullptr;
-  if (ev.start != nullptr || stop != nullptr) {
-    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, ev.start, stop, 0,
-                          static_cast<KArgs>(args)...);
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (ev.kernel < 0) {
+    start = ev.start;
+    stop = ends_call ? ev.stop : nullptr;
     ev.start = nullptr;
+  } else if (ev.count == ev.kernel) {
+    start = ev.start;
+    stop = ev.stop;
+  }
+  ++ev.count;
+  if (start != nullptr || stop != nullptr) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0,
+                          static_cast<KArgs>(args)...);
   } else {
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, static_cast<KArgs>(args)...);
   }
@@ -418,6 +429,120 @@ __global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restric
     __syncthreads();
   }
   if (grp == 0 && c < C) out[size_t(r) * C + c] = sh[0][lane];
+}
+
+// ------------------------------------------------- look-back words ----
+// Carries exchanged between workgroups of one kernel (the RWKV-4 kernels
+// split over time): a pair of fp32 values (a, b) packed in one 64-bit word
+// that is written and read with relaxed agent-scope atomics.  Such accesses
+// are coherent across the chip's XCDs (their L2s are not) without any fence,
+// and a 64-bit word is written in one piece, so the word is its own "ready"
+// flag: the workspace is filled with kLbEmpty before the kernel, and a word
+// that differs from it holds a published pair.  kLbEmpty is two NaNs with an
+// all-ones payload, which arithmetic never produces (the hardware's NaN
+// results are the canonical 0x7fc00000); a pair that still matches it (NaN
+// inputs carrying that payload) is published as canonical NaNs instead.
+constexpr uint64_t kLbEmpty = ~uint64_t(0);
+constexpr uint64_t kLbNaN = (uint64_t(0x7fc00000u) << 32) | 0x7fc00000u;
+// Polls of one word before a workgroup gives up waiting (the row is then
+// recomputed by the exact path).  A published word arrives within
+// microseconds; the bound only guarantees that every wave ends.
+constexpr int kLbMaxPolls = 1 << 16;
+// Marker values of the per-row status words (filled with all ones).
+constexpr uint32_t kRowOk = ~uint32_t(0);
+constexpr uint32_t kRowRedo = 0u;
+
+__device__ __forceinline__ uint64_t lb_pack(float a, float b) {
+  const uint64_t w = (uint64_t(__float_as_uint(b)) << 32) | __float_as_uint(a);
+  return w == kLbEmpty ? kLbNaN : w;
+}
+__device__ __forceinline__ float lb_lo(uint64_t w) { return __uint_as_float(uint32_t(w)); }
+__device__ __forceinline__ float lb_hi(uint64_t w) { return __uint_as_float(uint32_t(w >> 32)); }
+__device__ __forceinline__ void lb_store(uint64_t* p, uint64_t w) {
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Aggregates a split kernel folds before the inclusive word it waits for.
+#ifndef WKV_LB_WINDOW
+#define WKV_LB_WINDOW 4
+#endif
+constexpr int kLbWindow = WKV_LB_WINDOW;
+
+// Carry of segment s of a row split over time, from look-back words.  dir =
+// +1: the carry comes from the segments before s (forward), -1: from those
+// after it (backward).  The K = kLbWindow nearest such segments contribute
+// their aggregates and the next one out its inclusive word, folded by Horner
+// from the farthest:  carry = (...(incl * DS + agg_far) * DS ...) * DS +
+// agg_near, where DS is the decay over one segment.  The words read never
+// depend on when they were published, so the carry (and the kernel's result)
+// is the same on every run.  agg, incl: this lane's words of segment 0;
+// segment j's are seg_stride words further.  Returns false when a word did
+// not arrive within kLbMaxPolls polls.
+template <int VEC>
+__device__ __forceinline__ bool lb_window_carry(const uint64_t* agg, const uint64_t* incl,
+                                                size_t seg_stride, int s, int nseg, int dir,
+                                                const float (&DS)[VEC], float (&ca)[VEC],
+                                                float (&cb)[VEC]) {
+  constexpr int K = kLbWindow;
+  uint64_t wa[K][VEC], wi[VEC];
+  const int jo = s - dir * (K + 1);  // the inclusive word's segment
+  const bool has_incl = jo >= 0 && jo < nseg;
+  for (int polls = 0;; ++polls) {
+    bool ready = true;
+#pragma unroll
+    for (int d = 1; d <= K; ++d) {
+      const int j = s - dir * d;
+      if (j < 0 || j >= nseg) continue;
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        wa[d - 1][c] = lb_load(agg + size_t(j) * seg_stride + c);
+        ready &= wa[d - 1][c] != kLbEmpty;
+      }
+    }
+    if (has_incl) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        wi[c] = lb_load(incl + size_t(jo) * seg_stride + c);
+        ready &= wi[c] != kLbEmpty;
+      }
+    }
+    if (ready) break;
+    if (polls >= kLbMaxPolls) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    ca[c] = has_incl ? lb_lo(wi[c]) : 0.f;
+    cb[c] = has_incl ? lb_hi(wi[c]) : 0.f;
+  }
+#pragma unroll
+  for (int d = K; d >= 1; --d) {
+    const int j = s - dir * d;
+    if (j < 0 || j >= nseg) continue;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      ca[c] = fmaf(ca[c], DS[c], lb_lo(wa[d - 1][c]));
+      cb[c] = fmaf(cb[c], DS[c], lb_hi(wa[d - 1][c]));
+    }
+  }
+  return true;
+}
+
+// Marks a row for recomputation by the exact path (read by a later kernel).
+__device__ __forceinline__ void mark_row_redo(uint32_t* status, int row) {
+  __hip_atomic_store(status + row, kRowRedo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Fills n16 pieces of 16 bytes with all ones (the look-back words and row
+// status words of a split kernel, before it runs).  A template so that each
+// translation unit that launches it holds its own copy.
+template <int Unused = 0>
+__global__ __launch_bounds__(256) void lb_fill_kernel(u32x4* __restrict__ p, size_t n16) {
+  const u32x4 ones = {~0u, ~0u, ~0u, ~0u};
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n16; i += size_t(gridDim.x) * 256)
+    p[i] = ones;
 }
 
 }  // namespace wkv

@@ -57,6 +57,22 @@ def checkpoint_shape(b: int, t: int, c: int) -> tuple[int, int, int, int]:
     return (CKPT_FIELDS, b, (t + CKPT_BLOCK - 1) // CKPT_BLOCK, c)
 
 
+def _forward_workspace(lib, b: int, t: int, c: int, device) -> tuple[Tensor | None, int]:
+    """Workspace of the split-over-time forward (few rows), or (None, 0)
+    when the one-row kernel runs; the library fills it itself."""
+    nbytes = int(lib.wkv4_forward_workspace_bytes(b, t, c))
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
+def _backward_workspace(lib, b: int, t: int, c: int, device) -> Tensor:
+    """Workspace of a backward from records: [2, B, C] partials, or the split
+    kernel's per-segment partials and carries for few rows."""
+    nbytes = int(lib.wkv4_backward_checkpointed_workspace_bytes(b, t, c))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
 def _launch_forward(key, value, time_decay, time_first, *, with_checkpoint: bool):
     """y (compute dtype) and, optionally, the checkpoint records."""
     _lib.require_gpu(key, value, time_decay, time_first)
@@ -67,17 +83,18 @@ def _launch_forward(key, value, time_decay, time_first, *, with_checkpoint: bool
     y = torch.empty_like(k)
     lib = _lib.load()
     code = _lib.dtype_code(k.dtype)
+    ws, nbytes = _forward_workspace(lib, b, t, c, k.device)
     if with_checkpoint:
         ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=k.device)
         rc = _lib.timed("wkv4_forward", k.device, lambda: lib.wkv4_forward_checkpointed(
             k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), y.data_ptr(), ck.data_ptr(),
-            b, t, c, code, _lib.stream_of(k),
+            _lib.ptr(ws), nbytes, b, t, c, code, _lib.stream_of(k),
         ))
         _lib.check(rc, "wkv4_forward_checkpointed")
         return y, ck
     rc = _lib.timed("wkv4_forward", k.device, lambda: lib.wkv4_forward(
         k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), y.data_ptr(),
-        b, t, c, code, _lib.stream_of(k),
+        _lib.ptr(ws), nbytes, b, t, c, code, _lib.stream_of(k),
     ))
     _lib.check(rc, "wkv4_forward")
     return y, None
@@ -150,12 +167,12 @@ def _launch_backward_train(grad_y: Tensor, key: Tensor, value: Tensor, time_deca
     gv = torch.empty_like(k)
     gtd = torch.empty(c, dtype=torch.float32, device=k.device)
     gtf = torch.empty(c, dtype=torch.float32, device=k.device)
-    ws = torch.empty(2 * b * c, dtype=torch.float32, device=k.device)  # [2, B, C] partials
     lib = _lib.load()
+    ws = _backward_workspace(lib, b, t, c, k.device)
     rc = _lib.timed("wkv4_backward", k.device, lambda: lib.wkv4_backward_checkpointed(
         gy.data_ptr(), td.data_ptr(), tf.data_ptr(), k.data_ptr(), v.data_ptr(), ck.data_ptr(),
         gk.data_ptr(), gv.data_ptr(), gtd.data_ptr(), gtf.data_ptr(), ws.data_ptr(),
-        ws.numel() * 4, b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k),
+        ws.numel(), b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k),
     ))
     _lib.check(rc, "wkv4_backward_checkpointed")
     return [gk, gv, gtd, gtf]
@@ -218,9 +235,10 @@ def _launch_gated_forward(key: Tensor, value: Tensor, time_decay: Tensor, time_f
     y = torch.empty_like(k)
     ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=k.device)
     lib = _lib.load()
+    ws, nbytes = _forward_workspace(lib, b, t, c, k.device)
     rc = _lib.timed("wkv4_forward_gated", k.device, lambda: lib.wkv4_forward_gated_checkpointed(
         k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), r.data_ptr(), y.data_ptr(),
-        ck.data_ptr(), b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
+        ck.data_ptr(), _lib.ptr(ws), nbytes, b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
     _lib.check(rc, "wkv4_forward_gated_checkpointed")
     return y, ck
 
@@ -253,12 +271,12 @@ def _launch_gated_backward(grad_y: Tensor, key: Tensor, value: Tensor, time_deca
     gk, gv, gr = torch.empty_like(k), torch.empty_like(k), torch.empty_like(k)
     gtd = torch.empty(c, dtype=torch.float32, device=k.device)
     gtf = torch.empty(c, dtype=torch.float32, device=k.device)
-    ws = torch.empty(2 * b * c, dtype=torch.float32, device=k.device)  # [2, B, C] partials
     lib = _lib.load()
+    ws = _backward_workspace(lib, b, t, c, k.device)
     rc = _lib.timed("wkv4_backward_gated", k.device, lambda: lib.wkv4_backward_gated_checkpointed(
         gy.data_ptr(), td.data_ptr(), tf.data_ptr(), k.data_ptr(), v.data_ptr(), r.data_ptr(),
         ck.data_ptr(), gk.data_ptr(), gv.data_ptr(), gr.data_ptr(), gtd.data_ptr(), gtf.data_ptr(),
-        ws.data_ptr(), ws.numel() * 4, b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
+        ws.data_ptr(), ws.numel(), b, t, c, _lib.dtype_code(k.dtype), _lib.stream_of(k)))
     _lib.check(rc, "wkv4_backward_gated_checkpointed")
     return [gk, gv, gr, gtd, gtf]
 

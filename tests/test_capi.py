@@ -48,16 +48,16 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_host_side_argument_errors(lib):
     # Rejected before any launch: unknown dtype, negative size, null pointers.
-    rc = lib.wkv4_forward(None, None, None, None, None, 1, 1, 1, 7, None)
+    rc = lib.wkv4_forward(None, None, None, None, None, None, 0, 1, 1, 1, 7, None)
     assert rc == 1 and b"dtype" in lib.wkv_last_error_string()
-    rc = lib.wkv4_forward(None, None, None, None, None, -1, 1, 1, 0, None)
+    rc = lib.wkv4_forward(None, None, None, None, None, None, 0, -1, 1, 1, 0, None)
     assert rc == 1 and b"sizes" in lib.wkv_last_error_string()
-    rc = lib.wkv4_forward(None, None, None, None, None, 1, 1, 1, 1, None)
+    rc = lib.wkv4_forward(None, None, None, None, None, None, 0, 1, 1, 1, 1, None)
     assert rc == 1 and b"null" in lib.wkv_last_error_string()
     rc = lib.wkv7_forward(None, None, None, None, None, None, None, None, None, 1, 1, 1, 32, 0, None)
     assert rc == 1 and b"64" in lib.wkv_last_error_string()
     # Empty problems are a no-op success.
-    assert lib.wkv4_forward(None, None, None, None, None, 0, 5, 8, 0, None) == 0
+    assert lib.wkv4_forward(None, None, None, None, None, None, 0, 0, 5, 8, 0, None) == 0
 
 
 def test_checkpoint_size_matches_python_layout(lib):

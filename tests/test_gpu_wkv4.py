@@ -161,10 +161,12 @@ def test_16bit_io_op_matches_oracle(dtype, b, t, c, seed):
         _close(g, r, what=f"{dtype} {(b, t, c)} {name}", **_bf16_tol(name))
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_16bit_io_equals_fp32_op_rounded(dtype, monkeypatch):
+def test_16bit_io_equals_fp32_op_rounded(dtype, split, monkeypatch):
     # wkv_bf16.py:11-14: same arithmetic on exactly widened inputs, one
     # rounding at the store -- given one tile configuration for both.
+    monkeypatch.setenv("WKV_SPLIT", split)
     monkeypatch.setenv("WKV_FWD_CFG", "1,8,16")
     monkeypatch.setenv("WKV_BWD_CFG", "1,8,16")
     ops = _lib_ops()
@@ -258,11 +260,14 @@ def test_216m_shape_full_size():
     _lane_invariants(train[1], train[2], gy, "216m training path")
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
 @pytest.mark.parametrize("kind", ["wide_keys", "large_time_first", "one_bad_channel"])
-def test_out_of_range_inputs_take_the_exact_path(kind):
+def test_out_of_range_inputs_take_the_exact_path(kind, split, monkeypatch):
     # Keys spanning > 96 base-2 exponents inside one segment, or |u| > 16,
     # are outside the shared-frame range; such rows are recomputed with the
-    # running-max recurrence and must still match the oracle.
+    # running-max recurrence and must still match the oracle.  split=1: the
+    # split-over-time kernels, whose fix-up kernels recompute such rows.
+    monkeypatch.setenv("WKV_SPLIT", split)
     ops = _lib_ops()
     b, t, c = 2, 200, 64
     k, v, td, tf, gy = O.make_inputs(b, t, c, seed=10)
@@ -285,12 +290,14 @@ def test_out_of_range_inputs_take_the_exact_path(kind):
         _close(g, r, rtol=1e-4, atol_scale=1e-4, what=f"{kind} {name}")
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
 @pytest.mark.parametrize("kind", ["wide_keys", "large_time_first", "one_bad_channel"])
-def test_out_of_range_inputs_training_path(kind):
+def test_out_of_range_inputs_training_path(kind, split, monkeypatch):
     # Same inputs through autograd: the forward's records come from the exact
     # path and the backward recomputes from them.
     from spikegpt_myelin_amd import weighted_key_value_hip
 
+    monkeypatch.setenv("WKV_SPLIT", split)
     b, t, c = 2, 200, 64
     k, v, td, tf, gy = O.make_inputs(b, t, c, seed=10)
     if kind == "wide_keys":
@@ -319,7 +326,11 @@ def test_empty_sequence_and_batch():
         assert torch.equal(gtf.cpu(), torch.zeros(8))
 
 
-def test_deterministic():
+@pytest.mark.parametrize("split", ["0", "1"])
+def test_deterministic(split, monkeypatch):
+    # split=1: the split kernels' carries come from the same look-back words
+    # on every run, so their results do not depend on timing either.
+    monkeypatch.setenv("WKV_SPLIT", split)
     ops = _lib_ops()
     k, v, td, tf, gy = O.make_inputs(8, 512, 256, seed=11, dtype=torch.bfloat16)
     kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
@@ -334,6 +345,7 @@ def test_deterministic():
 def test_all_tile_configurations_agree(monkeypatch):
     # Every compiled tile configuration computes the same function.  The
     # library reads WKV_FWD_CFG / WKV_BWD_CFG ("vec,L,W") at each call.
+    monkeypatch.setenv("WKV_SPLIT", "0")
     ops = _lib_ops()
     inputs = O.make_inputs(3, 700, 256, seed=12, dtype=torch.bfloat16)
     kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in inputs)
@@ -355,6 +367,86 @@ def test_all_tile_configurations_agree(monkeypatch):
         got = _grads(weighted_key_value_hip_bf16io, kd, vd, tdd, tfd, gyd)
         for g2, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
             _close(g2, r, what=f"autograd cfg {fc}/{bc} {name}", **_bf16_tol(name))
+
+
+SPLIT_CASES = [(3, 200, 96, 30), (2, 1000, 130, 31), (4, 257, 512, 32), (1, 323, 64, 33),
+               (2, 3000, 70, 34), (5, 128, 33, 35)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("b,t,c,seed", SPLIT_CASES)
+def test_split_over_time_matches_oracle(dtype, b, t, c, seed, monkeypatch):
+    # The split-over-time kernels (few rows: one workgroup per segment and
+    # row, carries exchanged through look-back words) against the fp64
+    # oracle: the standalone ops (records computed inside the backward) and
+    # the training path.  T not a multiple of the segment, C not a multiple
+    # of 64, a single row.
+    from spikegpt_myelin_amd import weighted_key_value_hip, weighted_key_value_hip_bf16io
+
+    monkeypatch.setenv("WKV_SPLIT", "1")
+    print(f"split B={b} T={t} C={c} {dtype}", flush=True)
+    ops = _lib_ops()
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=seed, dtype=dtype)
+    kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    names = ("y", "gk", "gv", "gtd", "gtf")
+    if dtype == torch.float32:
+        y = ops.wkv_forward(kd, vd, tdd, tfd)
+        g = ops.wkv_backward(gyd, -torch.exp(tdd), tfd, kd, vd)
+        train = _grads(weighted_key_value_hip, kd, vd, tdd, tfd, gyd)
+        tol = lambda name: FP32_TOL  # noqa: E731
+    else:
+        y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
+        g = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
+        train = _grads(weighted_key_value_hip_bf16io, kd, vd, tdd, tfd, gyd)
+        tol = _bf16_tol
+    for got, r, name in zip((y, *g), ref, names):
+        _close(got, r, what=f"split ops {name}", **tol(name))
+    for got, r, name in zip(train, ref, names):
+        _close(got, r, what=f"split training path {name}", **tol(name))
+
+
+@pytest.mark.parametrize("fcfg,bcfg", [("1,8,8", "1,8,8"), ("1,8,16", "1,16,4"),
+                                       ("1,16,4", "1,8,16"), ("2,8,8", "2,8,8"),
+                                       ("1,4,16", "2,4,16"), ("2,4,16", "1,4,16")])
+def test_split_tile_configurations(fcfg, bcfg, monkeypatch):
+    # Every compiled split tile configuration (WKV_FWD_SPLIT_CFG /
+    # WKV_BWD_SPLIT_CFG = "vec,L,W") against the oracle, with the
+    # out-of-range fix-up exercised on one row.
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    monkeypatch.setenv("WKV_SPLIT", "1")
+    monkeypatch.setenv("WKV_FWD_SPLIT_CFG", fcfg)
+    monkeypatch.setenv("WKV_BWD_SPLIT_CFG", bcfg)
+    print(f"split tiles fwd={fcfg} bwd={bcfg}", flush=True)
+    k, v, td, tf, gy = O.make_inputs(3, 700, 256, seed=36, dtype=torch.bfloat16)
+    got = _grads(weighted_key_value_hip_bf16io, *(x.to(DEV) for x in (k, v, td, tf, gy)))
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"split {fcfg}/{bcfg} {name}", **_bf16_tol(name))
+    k2 = k.clone()
+    k2[1, 400, 7] = 100.0  # one row (b=1, channels 0..63) leaves the fixed frame
+    got = _grads(weighted_key_value_hip_bf16io, *(x.to(DEV) for x in (k2, v, td, tf, gy)))
+    ref = _oracle64_fast(k2, v, td, tf, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, rtol=2e-2, atol=1e-2, what=f"split {fcfg}/{bcfg} fix-up {name}")
+
+
+def test_split_and_one_row_kernels_agree(monkeypatch):
+    # The two decompositions of the long-context shape (4 of its 24 rows)
+    # compute the same function: equal to fp32 rounding before the bf16
+    # store, so within one bf16 step.
+    ops = _lib_ops()
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(4, 3072, 512, seed=37, dtype=torch.bfloat16))
+    outs = {}
+    for split in ("0", "1"):
+        monkeypatch.setenv("WKV_SPLIT", split)
+        y = ops.wkv_forward_bf16io(k, v, td, tf)
+        g = ops.wkv_backward_bf16io(gy, -torch.exp(td), tf, k, v)
+        outs[split] = (y, *g)
+    for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), outs["0"], outs["1"]):
+        a, b = a.float(), b.float()
+        assert torch.allclose(a, b, rtol=2 ** -7, atol=1e-6 * float(a.abs().max())), name
 
 
 def test_compiles_without_graph_breaks():

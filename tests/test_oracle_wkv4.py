@@ -249,3 +249,32 @@ def test_golden_fixtures_reproduce():
         assert torch.allclose(y, g["y"], atol=1e-12, rtol=1e-10), case
         for got, name in ((gk, "gk"), (gv, "gv"), (gtd, "gtd"), (gtf, "gtf")):
             assert torch.allclose(got, g[name], atol=1e-10, rtol=1e-9), (case, name)
+
+
+def test_associative_scan_matches_the_loop_in_float64():
+    # language.py:452-527 as the reference runs it (associative_scan, generic
+    # combine mode): equal to the independently pinned loop in fp64, at T
+    # values that are and are not powers of two (the scan's tree shape).
+    for steps in (1, 2, 7, 16, 33):
+        k, v, td, tf = _inputs(2, steps, 6, seed=40 + steps)
+        y = O.wkv_associative_scan(k, v, td, tf)
+        assert torch.allclose(y, O.wkv_loop(k, v, td, tf), atol=1e-12, rtol=1e-10), steps
+    # T = 1 gives y = v (tests/test_language.py:42 of the reference)
+    k, v, td, tf = _inputs(3, 1, 5, seed=47)
+    assert torch.allclose(O.wkv_associative_scan(k, v, td, tf), v, atol=1e-14)
+
+
+def test_associative_scan_float32_and_bf16_upcast():
+    # Config-0 distributions in fp32 (C0: B=2, T=128, C=512): the tree-ordered
+    # scan, the left fold and the fp64 loop agree to fp32 rounding; bf16
+    # inputs are upcast to fp32 and the result cast back (language.py:483-485).
+    k, v, td, tf, _ = O.make_inputs(2, 128, 512, seed=0)
+    y = O.wkv_associative_scan(k, v, td, tf)
+    assert y.dtype == torch.float32
+    ref = O.wkv_loop(k.double(), v.double(), td.double(), tf.double())
+    assert torch.allclose(y.double(), ref, rtol=1e-5, atol=1e-5 * float(ref.abs().max()))
+    assert torch.allclose(y, O.wkv_monoid_scan(k, v, td, tf), rtol=1e-5, atol=1e-5)
+    kb, vb = k.bfloat16(), v.bfloat16()
+    yb = O.wkv_associative_scan(kb, vb, td, tf)
+    assert yb.dtype == torch.bfloat16
+    assert torch.equal(yb, O.wkv_associative_scan(kb.float(), vb.float(), td, tf).bfloat16())
