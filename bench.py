@@ -33,7 +33,8 @@ decode, B=256, fused block step in one HIP graph), ``lif`` (sequence LIF forward
 ``timemix`` (fused token-shift mix, three vectors, same shape),
 ``e2e41m`` (the whole 41M SpikeGPT
 training step, 12 layers x 512, vocab 256, B=64, T=1024; the default run
-also reports it as ``e2e_train_step``).
+also reports it as ``e2e_train_step``), ``e2e216m`` (the 216M-class training
+step, 18 layers x 768, vocab 50277, B=16, T=1024).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -743,15 +744,22 @@ def bench_timemix(args) -> dict:
     return out
 
 
-def bench_e2e(steps: int, warmup: int) -> dict:
-    """The 41M SpikeGPT training step: 12 layers, 512 embedding, byte vocab
-    (256), B=64, T=1024, random init, synthetic tokens, bf16 autocast, fused
-    AdamW with gradient clipping -- the recipe of the reference's trainer
-    (examples/train_tiny_spikegpt.py:646-655, 797, 866-880).  WKV and LIF run
-    in the HIP kernels; GEMMs, norms and the loss are PyTorch-ROCm."""
+# Training-step models: (B, T, layers, embedding, vocabulary).  "41m": the
+# 41M SpikeGPT (12 x 512, byte vocabulary); "216m": the reference's gpt2-216m
+# preset (src/spikegpt/language.py:297-298: 18 layers x 768, context 1024)
+# with the GPT-2 BPE vocabulary size 50277, B=16.
+E2E_MODELS = {"41m": (64, 1024, 12, 512, 256), "216m": (16, 1024, 18, 768, 50277)}
+
+
+def bench_e2e(steps: int, warmup: int, model_name: str = "41m") -> dict:
+    """A SpikeGPT training step: random init, synthetic tokens, bf16 autocast,
+    fused AdamW with gradient clipping -- the recipe of the reference's
+    trainer (examples/train_tiny_spikegpt.py:646-655, 797, 866-880).  WKV,
+    LIF, token shift, layer norm + mix and the gates run in the HIP kernels;
+    GEMMs and the loss are PyTorch-ROCm (hipBLASLt)."""
     from spikegpt_myelin_amd.model import SpikeGPTConfig, SpikeLanguageModel
 
-    B, T, layers, embd, vocab = 64, 1024, 12, 512, 256
+    B, T, layers, embd, vocab = E2E_MODELS[model_name]
     dev = torch.device("cuda", 0)
     torch.manual_seed(0)
     cfg = SpikeGPTConfig(vocab_size=vocab, context_length=T, n_layer=layers, n_embd=embd,
@@ -782,7 +790,7 @@ def bench_e2e(steps: int, warmup: int) -> dict:
     dt = (time.perf_counter() - t0) / steps
     return {"tokens_per_s": B * T / dt, "ms_per_step": dt * 1e3, "steps": steps,
             "warmup": warmup, "loss_last": float(loss), "params": n_params,
-            "config": {"model": "spikegpt-41m", "n_layer": layers, "n_embd": embd,
+            "config": {"model": f"spikegpt-{model_name}", "n_layer": layers, "n_embd": embd,
                        "vocab": vocab, "B": B, "T": T, "dtype": "bf16 autocast",
                        "optimizer": "AdamW fused, clip 1.0", "data": "synthetic tokens"}}
 
@@ -795,7 +803,7 @@ def main() -> int:
     ap.add_argument("--event-every", type=int, default=10,
                     help="time the dominant launch with HIP events on every N-th timed step")
     ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "block_decode", "wkv7", "lif",
-                             "timemix", "e2e41m"])
+                             "timemix", "e2e41m", "e2e216m"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=20,
@@ -831,8 +839,8 @@ def main() -> int:
         out = bench_lif(args)
     elif args.workload == "timemix":
         out = bench_timemix(args)
-    elif args.workload == "e2e41m":
-        out = bench_e2e(args.steps, args.warmup)
+    elif args.workload in ("e2e41m", "e2e216m"):
+        out = bench_e2e(args.steps, args.warmup, args.workload[3:])
     else:
         out = bench_wkv4(args, WORKLOADS[args.workload])
         if args.workload == "wkv4" and args.e2e_steps > 0:

@@ -97,12 +97,15 @@ def test_loss_matches_oracle_recurrences(autocast, monkeypatch):
     assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
 
 
-@pytest.mark.parametrize("autocast,scale", [(True, 1.0), (False, 1.0), (True, 4.0)])
+@pytest.mark.parametrize("autocast,scale", [(True, 1.0), (False, 1.0), (True, 4.0), (True, 8.0),
+                                            (False, 8.0)])
 def test_loss_matches_oracle_recurrences_at_41m_depth(autocast, scale, monkeypatch):
     # The 41M configuration itself: 12 layers, 512 channels, byte vocabulary,
-    # random init (scale 1) and with the projection weights scaled up so that
-    # the LIFs fire more often (scale 4); B=2, T=512 keeps the CPU oracle's
-    # twelve layers of loops within seconds.
+    # random init (scale 1), and with the projection weights scaled up so
+    # that the LIFs fire and the recurrences shape the output (scales 4, 8);
+    # B=2, T=512 keeps the CPU oracle's twelve layers of loops within seconds.
+    import spikegpt_myelin_amd.model as M
+
     model = _model(n_layer=12, n_embd=512, vocab=256, ctx=1024, seed=3).to(DEV)
     if scale != 1.0:
         with torch.no_grad():
@@ -114,8 +117,34 @@ def test_loss_matches_oracle_recurrences_at_41m_depth(autocast, scale, monkeypat
     with torch.no_grad():
         hip = _loss(model, ids, tgt, autocast, False, monkeypatch)
         ref = _loss(model, ids, tgt, autocast, True, monkeypatch)
+        with monkeypatch.context() as mp:
+            # Power of the check: the same model with the time mix's
+            # recurrence output zeroed.
+            mp.setattr(M, "weighted_key_value_gated", lambda k, v, td, tf, r: torch.zeros_like(k))
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+                no_wkv, _ = model(ids, tgt)
     rel = abs(float(hip) - float(ref)) / abs(float(ref))
-    print(f"41M depth loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})")
+    moved = abs(float(no_wkv) - float(ref)) / abs(float(ref))
+    print(f"41M depth loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e}); "
+          f"without the recurrence {float(no_wkv):.6f} (rel {moved:.2e})")
+    assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
+    if scale >= 8.0:
+        # here the recurrence moves the loss by far more than the bar
+        assert moved > 10 * 2e-3, f"the recurrence hardly moves the loss ({moved:.2e})"
+
+
+def test_loss_matches_oracle_recurrences_at_216m_shape(monkeypatch):
+    # The 216M-class architecture (language.py:297-298: 18 layers x 768,
+    # GPT-2 BPE vocabulary 50277), random init, bf16 autocast; B=1, T=256.
+    # At 768 channels the block takes the two-kernel layer norm + token shift
+    # path (the fused kernel holds at most 512 channels per row).
+    model = _model(n_layer=18, n_embd=768, vocab=50277, ctx=1024, seed=4).to(DEV)
+    ids, tgt = (x.to(DEV) for x in _batch(1, 256, vocab=50277, seed=12))
+    with torch.no_grad():
+        hip = _loss(model, ids, tgt, True, False, monkeypatch)
+        ref = _loss(model, ids, tgt, True, True, monkeypatch)
+    rel = abs(float(hip) - float(ref)) / abs(float(ref))
+    print(f"216M shape loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})")
     assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
 
 

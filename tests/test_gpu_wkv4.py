@@ -461,6 +461,23 @@ def test_compiles_without_graph_breaks():
     assert torch.equal(cf(kd, vd, tdd, tfd), f(kd, vd, tdd, tfd))
 
 
+@pytest.mark.parametrize("fwd,bwd,dtype", [("wkv_forward", "wkv_backward", torch.float32),
+                                           ("wkv_forward_bf16io", "wkv_backward_bf16io",
+                                            torch.bfloat16)])
+def test_opcheck_public_ops(fwd, bwd, dtype):
+    # torch.library's own checks on the four public ops: schema and mutation,
+    # autograd registration, fake-tensor shapes, AOT dispatch (static and
+    # dynamic shapes).  The forwards are CompositeImplicitAutograd bodies
+    # over myelin::wkv4_forward_train (so that autograd saves the checkpoint
+    # records); the backwards are opaque custom ops, as in the reference.
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(2, 40, 64, seed=16, dtype=dtype))
+    fop, bop = getattr(torch.ops.myelin, fwd).default, getattr(torch.ops.myelin, bwd).default
+    torch.library.opcheck(fop, (k, v, td, tf))
+    leaves = tuple(x.clone().requires_grad_(True) for x in (k, v, td, tf))
+    torch.library.opcheck(fop, leaves)
+    torch.library.opcheck(bop, (gy, -torch.exp(td), tf, k, v))
+
+
 def test_language_entry_point_dispatch_and_validation():
     from spikegpt_myelin_amd import weighted_key_value
 
