@@ -3,9 +3,12 @@ kernels against the same model (identical weights and batch) with all three
 replaced by the CPU oracle's formulations.
 
 Bars: loss within 0.2 % relative (the end-model bar), under bf16 autocast
-and in fp32; parameter gradients in fp32 with cosine similarity > 0.999 (the
-spike threshold makes gradients discontinuous, so an elementwise bound would
-test rounding luck, not the kernels).
+and in fp32, where the loss is not chaotic (the measured noise floor is given
+at the 41M-depth test); in the firing regime of the 41M depth, each layer's
+halves teacher-forced against the oracle (bars at TEACHER_FORCED_TOL);
+parameter gradients in fp32 with cosine similarity > 0.999 (the spike
+threshold makes gradients discontinuous, so an elementwise bound would test
+rounding luck, not the kernels).
 """
 
 from __future__ import annotations
@@ -56,26 +59,33 @@ def _oracle_mix(x, mixes):
     return [o.to(x.device) for o in outs]
 
 
-def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
+def _oracle_ln(x, norm):
+    # torch's layer norm in fp32, as autocast runs it
+    return torch.nn.functional.layer_norm(x.float(), norm.normalized_shape, norm.weight,
+                                          norm.bias, norm.eps)
+
+
+def _patch_oracle(mp, wkv=_oracle_wkv):
+    """Route the model's WKV, LIF, token-shift mix, fused layer norm + mix and
+    gates through the oracle's formulations (``wkv``: the WKV to use)."""
     import spikegpt_myelin_amd.model as M
 
+    mp.setattr(M, "weighted_key_value_gated",
+               lambda k, v, td, tf, r: torch.sigmoid(r) * wkv(k, v, td, tf))
+    mp.setattr(M, "lif_sequence", _oracle_lif)
+    mp.setattr(M, "lif_residual", lambda residual, x, **kw: residual + _oracle_lif(x, **kw))
+    mp.setattr(M, "token_shift_mix", _oracle_mix)
+    mp.setattr(M, "layer_norm_shift_mix", lambda x, norm, mix: _oracle_mix(_oracle_ln(x, norm), mix))
+    mp.setattr(M, "layer_norm_shift_mix_fork",
+               lambda x, norm, mix: [*_oracle_mix(_oracle_ln(x, norm), mix), x])
+    mp.setattr(M, "relu_square", lambda x: torch.relu(x).square())
+    mp.setattr(M, "sigmoid_gate", lambda r, x: torch.sigmoid(r) * x)
+
+
+def _loss(model, ids, tgt, autocast, oracle, monkeypatch):
     with monkeypatch.context() as mp:
         if oracle:
-            mp.setattr(M, "weighted_key_value_gated",
-                       lambda k, v, td, tf, r: torch.sigmoid(r) * _oracle_wkv(k, v, td, tf))
-            mp.setattr(M, "lif_sequence", _oracle_lif)
-            mp.setattr(M, "lif_residual", lambda residual, x, **kw: residual + _oracle_lif(x, **kw))
-            mp.setattr(M, "token_shift_mix", _oracle_mix)
-            # The block's fused layer norm + mix becomes torch's layer norm
-            # (fp32, as autocast runs it) and the oracle's mix.
-            mp.setattr(M, "layer_norm_shift_mix", lambda x, norm, mix: _oracle_mix(
-                torch.nn.functional.layer_norm(x.float(), norm.normalized_shape, norm.weight,
-                                               norm.bias, norm.eps), mix))
-            mp.setattr(M, "layer_norm_shift_mix_fork", lambda x, norm, mix: [*_oracle_mix(
-                torch.nn.functional.layer_norm(x.float(), norm.normalized_shape, norm.weight,
-                                               norm.bias, norm.eps), mix), x])
-            mp.setattr(M, "relu_square", lambda x: torch.relu(x).square())
-            mp.setattr(M, "sigmoid_gate", lambda r, x: torch.sigmoid(r) * x)
+            _patch_oracle(mp)
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
             loss, _ = model(ids, tgt)
     return loss
@@ -97,15 +107,20 @@ def test_loss_matches_oracle_recurrences(autocast, monkeypatch):
     assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
 
 
-@pytest.mark.parametrize("autocast,scale", [(True, 1.0), (False, 1.0), (True, 4.0), (True, 8.0),
-                                            (False, 8.0)])
+@pytest.mark.parametrize("autocast,scale", [(True, 1.0), (False, 1.0), (True, 4.0), (False, 4.0)])
 def test_loss_matches_oracle_recurrences_at_41m_depth(autocast, scale, monkeypatch):
     # The 41M configuration itself: 12 layers, 512 channels, byte vocabulary,
-    # random init (scale 1), and with the projection weights scaled up so
-    # that the LIFs fire and the recurrences shape the output (scales 4, 8);
-    # B=2, T=512 keeps the CPU oracle's twelve layers of loops within seconds.
-    import spikegpt_myelin_amd.model as M
-
+    # random init (scale 1), and with the projection weights scaled by 4 so
+    # that the time mixes' outputs approach the LIF threshold; B=2, T=512
+    # keeps the CPU oracle's twelve layers of loops within seconds.  Larger
+    # scales put the 12-layer spiking model in a regime where the loss is not
+    # a parity measure: at scale 8, the oracle model with its layer norm
+    # summed in fp64 instead of fp32 (no kernel involved) moves its own loss
+    # by 2-3e-3 under bf16 autocast, and a 2^-14 relative nudge of the WKV
+    # output moves it by up to 5e-3 in fp32 (spikes near the threshold flip
+    # and the flips compound over the layers); at scale 4 both stay below
+    # 2.5e-4.  The firing regime is compared layer by layer, teacher-forced,
+    # in test_layers_match_oracle_teacher_forced_at_41m_depth.
     model = _model(n_layer=12, n_embd=512, vocab=256, ctx=1024, seed=3).to(DEV)
     if scale != 1.0:
         with torch.no_grad():
@@ -117,20 +132,119 @@ def test_loss_matches_oracle_recurrences_at_41m_depth(autocast, scale, monkeypat
     with torch.no_grad():
         hip = _loss(model, ids, tgt, autocast, False, monkeypatch)
         ref = _loss(model, ids, tgt, autocast, True, monkeypatch)
-        with monkeypatch.context() as mp:
-            # Power of the check: the same model with the time mix's
-            # recurrence output zeroed.
-            mp.setattr(M, "weighted_key_value_gated", lambda k, v, td, tf, r: torch.zeros_like(k))
-            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
-                no_wkv, _ = model(ids, tgt)
     rel = abs(float(hip) - float(ref)) / abs(float(ref))
-    moved = abs(float(no_wkv) - float(ref)) / abs(float(ref))
-    print(f"41M depth loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e}); "
-          f"without the recurrence {float(no_wkv):.6f} (rel {moved:.2e})")
+    print(f"41M depth loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})")
     assert rel < 2e-3, f"loss {float(hip):.6f} vs oracle {float(ref):.6f} (rel {rel:.2e})"
-    if scale >= 8.0:
-        # here the recurrence moves the loss by far more than the bar
-        assert moved > 10 * 2e-3, f"the recurrence hardly moves the loss ({moved:.2e})"
+
+
+def _time_mix_half(block, x):
+    """The block's first half on ``x`` (model.py SpikeGPTBlock.forward): the
+    time mix's output before its LIF, and the residual with the spikes added.
+    Every op is looked up on the model module, so patches apply."""
+    import spikegpt_myelin_amd.model as M
+
+    residual = block.ln0(x) if block.ln0 is not None else x
+    *mixed, residual = M.layer_norm_shift_mix_fork(residual, block.ln1, block.att.mixes())
+    pre = block.att.project(*mixed)
+    return pre, M._add_lif(residual, block.lif1, pre)
+
+
+def _channel_mix_half(block, x):
+    import spikegpt_myelin_amd.model as M
+
+    *mixed, residual = M.layer_norm_shift_mix_fork(x, block.ln2, block.ffn.mixes())
+    pre = block.ffn.project(*mixed)
+    return pre, M._add_lif(residual, block.lif2, pre)
+
+
+def _wkv_dropped_bonus(key, value, time_decay, time_first):
+    # planted mistake: the current token's bonus e^(u + k) taken as e^k
+    return _oracle_wkv(key, value, time_decay, torch.zeros_like(time_first))
+
+
+def _wkv_decay_twice(key, value, time_decay, time_first):
+    # planted mistake: the decay applied twice per step (w -> 2 w)
+    return _oracle_wkv(key, value, time_decay + 0.6931471805599453, time_first)
+
+
+def _teacher_forced(model, ids, autocast, wkv=_oracle_wkv):
+    """Per layer: the oracle model's block input, then both halves on the HIP
+    path and on the oracle path from the same oracle inputs.  Returns a list
+    of (hip_att, ora_att, hip_att_out, ora_att_out, hip_ffn, ora_ffn,
+    hip_out, ora_out) per layer."""
+    out = []
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        x = model.embed_tokens(ids)
+        for block in model.blocks:
+            h_att, h_mid = _time_mix_half(block, x)
+            with pytest.MonkeyPatch.context() as mp:
+                _patch_oracle(mp, wkv)
+                o_att, o_mid = _time_mix_half(block, x)
+                o_ffn, o_out = _channel_mix_half(block, o_mid)
+            h_ffn, h_out = _channel_mix_half(block, o_mid)
+            out.append((h_att, o_att, h_mid, o_mid, h_ffn, o_ffn, h_out, o_out))
+            x = o_out
+    return out
+
+
+def _normwise(got, ref):
+    got, ref = got.double(), ref.double()
+    return float((got - ref).norm() / ref.norm()) if float(ref.norm()) > 0 else float(got.norm())
+
+
+# Bars of the teacher-forced comparison.  bf16 autocast: each half's output
+# before its LIF within 2e-3 normwise and 2e-2 * max|ref| elementwise (measured
+# on MI355X at most 4.8e-4 and 5.4e-3 over the twelve layers), at most 1e-3 of
+# the spikes flipped (measured 3.8e-5: membranes within a bf16 rounding of the
+# threshold).  fp32: 1e-5 normwise and elementwise relative to max|ref|
+# (measured 1.1e-6 and 1.4e-6), at most 1e-4 of the spikes flipped (measured
+# one in 524,288).  Planted mistakes in the oracle's WKV give 0.24-0.96
+# normwise in every layer, so the time-mix bar is met by a margin of more than
+# 100 against either.
+TEACHER_FORCED_TOL = {True: (2e-3, 2e-2, 1e-3), False: (1e-5, 1e-5, 1e-4)}
+
+
+@pytest.mark.parametrize("autocast", [True, False])
+def test_layers_match_oracle_teacher_forced_at_41m_depth(autocast):
+    # The firing regime of the 41M configuration (projection weights scaled
+    # by 8: 17-22 % of the time mixes' and 37-39 % of the channel mixes'
+    # outputs cross the LIF threshold), compared layer by layer with the
+    # oracle model's own block input fed to both paths: each half's
+    # continuous output before its LIF (the time mix carries the WKV
+    # recurrence) and the spikes each LIF adds.  Teacher forcing keeps a
+    # spike flipped in one layer from changing the next layer's input, which
+    # is what makes the loss of this configuration chaotic (see the 41M-depth
+    # loss test).
+    norm_tol, max_tol, flip_tol = TEACHER_FORCED_TOL[autocast]
+    model = _model(n_layer=12, n_embd=512, vocab=256, ctx=1024, seed=3).to(DEV)
+    with torch.no_grad():
+        for p in model.parameters():
+            if p.ndim == 2:
+                p.mul_(8.0)
+    ids, _ = (x.to(DEV) for x in _batch(2, 512, seed=11))
+    print(f"teacher-forced 41M depth autocast={autocast}", flush=True)
+    layers = _teacher_forced(model, ids, autocast)
+    for i, (h_att, o_att, h_mid, o_mid, h_ffn, o_ffn, h_out, o_out) in enumerate(layers):
+        for half, got, ref, h_spk, o_spk in (("time mix", h_att, o_att, h_mid, o_mid),
+                                             ("channel mix", h_ffn, o_ffn, h_out, o_out)):
+            err = _normwise(got, ref)
+            ref64 = ref.double()
+            mx = float((got.double() - ref64).abs().max() / ref64.abs().max())
+            flips = float(((h_spk - o_spk).abs() > 0.5).double().mean())
+            fired = float((ref.float() >= 1.0).double().mean())
+            print(f"layer {i:2d} {half}: normwise {err:.2e}, max {mx:.2e}, flips {flips:.2e}, "
+                  f"over threshold {fired:.3f}")
+            assert fired > 0.05, f"layer {i} {half}: the LIF hardly fires ({fired:.3f})"
+            assert err < norm_tol, f"layer {i} {half}: normwise {err:.2e}"
+            assert mx < max_tol, f"layer {i} {half}: max error / max|ref| {mx:.2e}"
+            assert flips < flip_tol, f"layer {i} {half}: {flips:.2e} of the spikes flipped"
+    # Power: the same comparison against an oracle with a planted mistake.
+    for name, wkv in (("dropped bonus", _wkv_dropped_bonus), ("decay twice", _wkv_decay_twice)):
+        bad = _teacher_forced(model, ids, autocast, wkv)
+        errs = [_normwise(h[0], m[1]) for h, m in zip(layers, bad)]
+        print(f"oracle with {name}: time mix normwise per layer " +
+              " ".join(f"{e:.1e}" for e in errs))
+        assert min(errs) > 50 * TEACHER_FORCED_TOL[True][0], f"{name}: {min(errs):.2e}"
 
 
 def test_loss_matches_oracle_recurrences_at_216m_shape(monkeypatch):

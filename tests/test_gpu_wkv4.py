@@ -551,3 +551,73 @@ def test_eager_path_equals_op_path(kdt, vdt, shape):
     traced = _grads(op_path, kd, vd, tdd, tfd, gyd)
     for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), eager, traced):
         assert a.dtype == b.dtype and torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("shape,split", [((8, 512, 256), "0"), ((4, 2304, 256), "1")])
+def test_c_abi_launches_replay_in_a_hip_graph(shape, split, monkeypatch):
+    # The C-ABI launches of a training step (forward with records, backward
+    # from them, and the allocation-free public backward) on preallocated
+    # buffers, captured in one HIP graph on the calling thread, as a caller
+    # that captures would issue them.  The split path's fill and fix-up are
+    # kernels too (no memset node is recorded).  Every replay, with unrelated
+    # eager work and synchronisation in between, equals the eager results.
+    from spikegpt_myelin_amd import _lib
+    from spikegpt_myelin_amd.wkv import checkpoint_shape
+
+    monkeypatch.setenv("WKV_SPLIT", split)
+    lib = _lib.load()
+    b, t, c = shape
+    print(f"graph replay B={b} T={t} C={c} split={split}", flush=True)
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(b, t, c, seed=40, dtype=torch.bfloat16))
+    w = -torch.exp(td)
+    code = _lib.DTYPE_BF16
+    fws_n = int(lib.wkv4_forward_workspace_bytes(b, t, c))
+    assert (fws_n > 0) == (split == "1")
+    fws = torch.empty(max(fws_n, 16), dtype=torch.uint8, device=DEV)
+    bws = torch.empty(int(lib.wkv4_backward_checkpointed_workspace_bytes(b, t, c)),
+                      dtype=torch.uint8, device=DEV)
+    y = torch.empty_like(k)
+    ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=DEV)
+    outs = [torch.empty_like(k), torch.empty_like(k), torch.empty(c, device=DEV),
+            torch.empty(c, device=DEV)]
+    outs2 = [torch.empty_like(k), torch.empty_like(k), torch.empty(c, device=DEV),
+             torch.empty(c, device=DEV)]
+
+    def step():
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.check(lib.wkv4_forward_checkpointed(
+            k.data_ptr(), v.data_ptr(), td.data_ptr(), tf.data_ptr(), y.data_ptr(), ck.data_ptr(),
+            fws.data_ptr() if fws_n else None, fws_n, b, t, c, code, s), "forward")
+        _lib.check(lib.wkv4_backward_checkpointed(
+            gy.data_ptr(), td.data_ptr(), tf.data_ptr(), k.data_ptr(), v.data_ptr(), ck.data_ptr(),
+            *(o.data_ptr() for o in outs), bws.data_ptr(), bws.numel(), b, t, c, code, s),
+            "backward")
+        _lib.check(lib.wkv4_backward_noalloc(
+            gy.data_ptr(), w.data_ptr(), tf.data_ptr(), k.data_ptr(), v.data_ptr(),
+            *(o.data_ptr() for o in outs2), b, t, c, code, s), "backward_noalloc")
+
+    step()
+    torch.cuda.synchronize()
+    eager = [x.clone() for x in (y, *outs, *outs2)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for rep in range(3):
+        for x in (y, *outs, *outs2):
+            x.zero_()
+        junk = torch.randn(1 << 20, device=DEV) * 3  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("y", "gk", "gv", "gtd", "gtf", "gk2", "gv2", "gtd2", "gtf2"),
+                                  (y, *outs, *outs2), eager):
+            assert torch.equal(got, ref), f"replay {rep}: {name} differs from the eager call"
+        del junk
+    # the records and outputs agree with the oracle, too
+    ref = _oracle64_fast(*(x.cpu() for x in (k, v, td, tf, gy)))
+    for got, r, name in zip((y, *outs), ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(got, r, what=f"graph {name}", **_bf16_tol(name))
