@@ -340,3 +340,51 @@ def test_split_k_linear_matches_linear(autocast):
     assert torch.allclose(gx1, gx0, **tol)
     rel = float((gw1 - gw0).norm() / gw0.norm())
     assert rel < (1e-2 if autocast else 1e-5), rel
+
+
+def test_reduce_overhead_compiled_model_matches_eager():
+    # The reference's trainer compiles the whole model with
+    # torch.compile(model, mode="reduce-overhead", fullgraph=True)
+    # (examples/example_utils.py:166-169): one graph, inductor, and the
+    # forward and backward each captured in a HIP graph and replayed.  A new
+    # batch every step (so a replay that reused stale inputs would show); the
+    # compiled model's loss and gradients against the eager model's.
+    # Inductor generates its own kernels for the torch ops between the HIP
+    # ops (embedding, layer norms, head, cross entropy), so the bar is the
+    # end-model one: loss within 2e-3, gradient cosine > 0.999.
+    from hip_graphs import recorded_hip_graphs, reset
+    from torch._dynamo.utils import counters
+
+    reset()
+    counters.clear()
+    model = _model(n_layer=2, n_embd=128).to(DEV)
+    with torch.no_grad():
+        for p in model.parameters():
+            if p.ndim == 2:
+                p.mul_(8.0)
+    twin = copy.deepcopy(model)
+    compiled = torch.compile(twin, mode="reduce-overhead", fullgraph=True)
+    for step in range(5):
+        print(f"reduce-overhead model step {step}", flush=True)
+        ids, tgt = (x.to(DEV) for x in _batch(4, 64, seed=30 + step))
+        losses = []
+        for m, params in ((model, model), (compiled, twin)):
+            params.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss, _ = m(ids, tgt)
+            loss.backward()
+            losses.append(float(loss.detach()))
+        torch.cuda.synchronize()
+        rel = abs(losses[1] - losses[0]) / abs(losses[0])
+        print(f"step {step}: eager {losses[0]:.6f} compiled {losses[1]:.6f} (rel {rel:.2e})")
+        assert rel < 2e-3, f"step {step}: loss rel {rel:.2e}"
+        for (name, p), q in zip(model.named_parameters(), twin.parameters()):
+            a, b = p.grad.double().flatten(), q.grad.double().flatten()
+            if float(a.norm()) == 0.0:
+                assert float(b.norm()) == 0.0, name
+                continue
+            cos = float(a @ b / (a.norm() * b.norm()))
+            assert cos > 0.999, f"step {step} {name}: cosine {cos:.6f}"
+    assert counters["inductor"]["cudagraph_skips"] == 0, dict(counters["inductor"])
+    assert recorded_hip_graphs() >= 2  # the forward and the backward graph
+    torch._dynamo.reset()

@@ -461,6 +461,47 @@ def test_compiles_without_graph_breaks():
     assert torch.equal(cf(kd, vd, tdd, tfd), f(kd, vd, tdd, tfd))
 
 
+def test_reduce_overhead_compile_replays_match_eager():
+    # The reference trains under torch.compile(mode="reduce-overhead",
+    # fullgraph=True) (examples/example_utils.py:166-169): inductor, with the
+    # forward and the backward graph each captured in a HIP graph (cudagraph
+    # trees) and replayed.  The training ops run inside those captures; every
+    # replayed step must equal the eager step, and no capture may be skipped.
+    from torch._dynamo.utils import counters
+
+    from hip_graphs import recorded_hip_graphs, reset
+
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    reset()
+    counters.clear()
+    print("reduce-overhead compile B=4 T=300 C=256 bf16", flush=True)
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(4, 300, 256, seed=16, dtype=torch.bfloat16))
+
+    def f(k, v, td, tf):
+        return weighted_key_value_hip_bf16io(k, v, td, tf)
+
+    def run(fn):
+        leaves = [x.detach().clone().requires_grad_(True) for x in (k, v, td, tf)]
+        y = fn(*leaves)
+        y.backward(gy)
+        return [y.detach().clone()] + [x.grad.clone() for x in leaves]
+
+    eager = run(f)
+    cf = torch.compile(f, mode="reduce-overhead", fullgraph=True)
+    for step in range(5):
+        junk = torch.randn(1 << 20, device=DEV) * 3  # unrelated eager work between steps
+        got = run(cf)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), got, eager):
+            assert torch.equal(a, b), f"step {step}: {name} differs from the eager step"
+        del junk
+    assert counters["inductor"]["cudagraph_skips"] == 0, dict(counters["inductor"])
+    # the forward and the backward graph were each recorded (and then replayed)
+    assert recorded_hip_graphs() >= 2
+    torch._dynamo.reset()
+
+
 @pytest.mark.parametrize("fwd,bwd,dtype", [("wkv_forward", "wkv_backward", torch.float32),
                                            ("wkv_forward_bf16io", "wkv_backward_bf16io",
                                             torch.bfloat16)])
