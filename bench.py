@@ -584,11 +584,13 @@ def bench_lif(args) -> dict:
     code = _lib.dtype_code(torch.bfloat16)
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
-    xp, spkp, ckp, gsp, gxp = (t.data_ptr() for t in (x, spk, ck, gs, gx))
+    ws_bytes = int(lib.lif_forward_workspace_bytes(B, T, C))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    xp, spkp, ckp, gsp, gxp, wsp = (t.data_ptr() for t in (x, spk, ck, gs, gx, ws))
 
     def fwd():
-        _lib.check(lib.lif_forward(xp, spkp, ckp, B, T, C, decay, thr, reset, slope, code, sp),
-                   "lif forward")
+        _lib.check(lib.lif_forward(xp, spkp, ckp, wsp, ws_bytes, B, T, C, decay, thr, reset, slope,
+                                   code, sp), "lif forward")
 
     def bwd():
         _lib.check(lib.lif_backward(xp, gsp, ckp, gxp, B, T, C, decay, thr, reset, slope, code, sp),
@@ -599,20 +601,25 @@ def bench_lif(args) -> dict:
         fwd()
         bwd()
     torch.cuda.synchronize()
-    evs = []
+    evs, fevs = [], []
     t0 = time.perf_counter()
     for i in range(args.steps):
-        fwd()
         if i % args.event_every == 0:
+            s_ev, e_ev = pool.take(), pool.take()
+            _lib.arm_events(s_ev, e_ev)
+            fwd()
+            fevs.append((s_ev, e_ev))
             s_ev, e_ev = pool.take(), pool.take()
             _lib.arm_events(s_ev, e_ev)
             bwd()
             evs.append((s_ev, e_ev))
         else:
+            fwd()
             bwd()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     bwd_t = statistics.mean(s.elapsed_time(e) * 1e-3 for s, e in evs)
+    fwd_t = statistics.mean(s.elapsed_time(e) * 1e-3 for s, e in fevs)
     step_s = elapsed / args.steps
     n = B * T * C
     bwd_bytes = 6 * n  # x, grad_spikes read; grad_x written (bf16)
@@ -626,6 +633,9 @@ def bench_lif(args) -> dict:
                    "state_dtype": "float32", "tau": 2.0, "threshold": thr, "reset": reset,
                    "slope": slope},
         "hbm_gbps_algorithmic": 10 * n / step_s / 1e9,
+        "fwd_launch_us": fwd_t * 1e6, "bwd_launch_us": bwd_t * 1e6,
+        "fwd_gbps_algorithmic": 4 * n / fwd_t / 1e9,
+        "fwd_time_segments": int(ws_bytes // (8 * B * C)) + 1 if ws_bytes else 1,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "lif_bwd_kernel",
                      "algorithmic_bytes_per_launch": bwd_bytes, "avg_launch_us": bwd_t * 1e6},
@@ -691,20 +701,25 @@ def bench_timemix(args) -> dict:
         fwd()
         bwd()
     torch.cuda.synchronize()
-    evs = []
+    evs, fevs = [], []
     t0 = time.perf_counter()
     for i in range(args.steps):
-        fwd()
         if i % args.event_every == 0:
+            s_ev, e_ev = pool.take(), pool.take()
+            _lib.arm_events(s_ev, e_ev)
+            fwd()
+            fevs.append((s_ev, e_ev))
             s_ev, e_ev = pool.take(), pool.take()
             _lib.arm_events(s_ev, e_ev)
             bwd()
             evs.append((s_ev, e_ev))
         else:
+            fwd()
             bwd()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     bwd_t = statistics.mean(s.elapsed_time(e) * 1e-3 for s, e in evs)
+    fwd_t = statistics.mean(s.elapsed_time(e) * 1e-3 for s, e in fevs)
     step_s = elapsed / args.steps
     ne = B * T * C
     fwd_bytes, bwd_bytes = (4 + 2 * n) * ne, (4 + 2 * n + 4) * ne

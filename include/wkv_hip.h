@@ -226,6 +226,13 @@ int wkv7_backward_checkpointed(const void* r, const void* w, const void* k, cons
  * [B][ceil(T/32)][C], the membrane at the start of every 32-step block. */
 size_t lif_checkpoint_bytes(int64_t B, int64_t T, int64_t C);
 
+/* Bytes of device workspace lif_forward and lif_residual_forward use to split
+ * the sequence over time for these sizes (the membranes at the segment
+ * boundaries, fp32); 0 when these sizes are not split.  With a smaller or
+ * NULL workspace the forward runs as one pass over time, with the same
+ * results bit for bit. */
+size_t lif_forward_workspace_bytes(int64_t B, int64_t T, int64_t C);
+
 /* Sequence LIF activation forward (SpikeGPT's spiking residual gate).
  *
  * Replaces the fused LIF launch inside SpikingSequenceLIF.forward
@@ -236,10 +243,11 @@ size_t lif_checkpoint_bytes(int64_t B, int64_t T, int64_t C);
  * starting at 0: h = m*decay + x, spike = [slope*(h - threshold) >= 0],
  * m = h*(1 - spike) + reset*spike.  Spikes are exact 0/1.  membrane_checkpoint
  * (may be NULL) receives lif_checkpoint_bytes() bytes for lif_backward.
- * decay = 1 - 1/tau; slope > 0. */
-int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, int64_t B, int64_t T,
-                int64_t C, float decay, float threshold, float reset, float slope, int dtype,
-                void* stream);
+ * workspace (may be NULL): lif_forward_workspace_bytes() bytes let the
+ * sequence be split over time (same results).  decay = 1 - 1/tau; slope > 0. */
+int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, void* workspace,
+                size_t workspace_bytes, int64_t B, int64_t T, int64_t C, float decay,
+                float threshold, float reset, float slope, int dtype, void* stream);
 
 /* Sequence LIF backward: grad_x [B,T,C] in `dtype` from x, grad_spikes and the
  * forward's membrane checkpoints, with the arctan surrogate derivative
@@ -315,11 +323,14 @@ int sigmoid_gate_backward(const void* r, const void* x, const void* grad_y, void
 
 /* LIF forward fused with the block's residual add (src/spikegpt/language.py:
  * 1326-1330, residual + lif(...)): out = residual + spikes(x), fp32
- * [B,T,C]; x in `dtype`; residual fp32 (out may alias it); membrane
- * checkpoint as lif_forward.  C a multiple of 8, T*C*4 < 2^31. */
+ * [B,T,C]; x in `dtype`; residual fp32 (out may alias it: then the sequence
+ * is not split over time); membrane checkpoint as lif_forward; workspace as
+ * lif_forward (lif_forward_workspace_bytes).  C a multiple of 8,
+ * T*C*4 < 2^31. */
 int lif_residual_forward(const void* x, const float* residual, float* out,
-                         float* membrane_checkpoint, int64_t B, int64_t T, int64_t C, float decay,
-                         float threshold, float reset, float slope, int dtype, void* stream);
+                         float* membrane_checkpoint, void* workspace, size_t workspace_bytes,
+                         int64_t B, int64_t T, int64_t C, float decay, float threshold,
+                         float reset, float slope, int dtype, void* stream);
 
 /* Backward of lif_residual_forward for x: grad_x (`dtype`) from grad_out
  * (fp32, the gradient of out; the residual's gradient is grad_out itself). */

@@ -94,16 +94,17 @@ SIGNATURES = {
         [_P] * 16 + [_I64, _I64, _I64, _I64, _INT, _P],
     ),
     "lif_checkpoint_bytes": (_SZ, [_I64, _I64, _I64]),
+    "lif_forward_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "lif_forward": (
         _INT,
-        [_P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
+        [_P, _P, _P, _P, _SZ, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
     ),
     "lif_backward": (
         _INT,
         [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
     ),
     "lif_residual_forward": (
-        _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P]),
+        _INT, [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P]),
     "lif_residual_backward": (
         _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P]),
     "token_shift_mix_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),

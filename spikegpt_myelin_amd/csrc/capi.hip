@@ -490,14 +490,19 @@ size_t lif_checkpoint_bytes(int64_t B, int64_t T, int64_t C) {
   return lif_checkpoint_floats(B, T, C) * sizeof(float);
 }
 
+size_t lif_forward_workspace_bytes(int64_t B, int64_t T, int64_t C) {
+  if (!dims_ok(B, T, C)) return 0;
+  return lif_fwd_workspace_bytes_impl(B, T, C);
+}
+
 static bool lif_params_ok(float decay, float threshold, float reset, float slope) {
   return std::isfinite(decay) && std::isfinite(threshold) && std::isfinite(reset) &&
          std::isfinite(slope) && slope > 0.f;
 }
 
-int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, int64_t B, int64_t T,
-                int64_t C, float decay, float threshold, float reset, float slope, int dtype,
-                void* stream) {
+int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, void* workspace,
+                size_t workspace_bytes, int64_t B, int64_t T, int64_t C, float decay,
+                float threshold, float reset, float slope, int dtype, void* stream) {
   set_error("");
   TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: unknown dtype");
@@ -507,15 +512,17 @@ int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, int64_t
                 "lif_forward: parameters must be finite and surrogate_slope positive");
   if (B == 0 || T == 0 || C == 0) return WKV_OK;
   if (!x || !spikes) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: null pointer");
-  if (!aligned16({x, spikes, membrane_checkpoint}))
+  if (!aligned16({x, spikes, membrane_checkpoint, workspace}))
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_forward: tensors must be 16-byte aligned");
-  return lif_forward_impl(x, spikes, membrane_checkpoint, int(B), int(T), int(C), decay, threshold,
-                          reset, slope, dtype, static_cast<hipStream_t>(stream));
+  return lif_forward_impl(x, spikes, membrane_checkpoint, workspace, workspace_bytes, int(B),
+                          int(T), int(C), decay, threshold, reset, slope, dtype,
+                          static_cast<hipStream_t>(stream));
 }
 
 int lif_residual_forward(const void* x, const float* residual, float* out,
-                         float* membrane_checkpoint, int64_t B, int64_t T, int64_t C, float decay,
-                         float threshold, float reset, float slope, int dtype, void* stream) {
+                         float* membrane_checkpoint, void* workspace, size_t workspace_bytes,
+                         int64_t B, int64_t T, int64_t C, float decay, float threshold,
+                         float reset, float slope, int dtype, void* stream) {
   set_error("");
   TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: unknown dtype");
@@ -529,11 +536,11 @@ int lif_residual_forward(const void* x, const float* residual, float* out,
                 "lif_residual_forward: C must be a multiple of 8 and T*C*4 below 2^31");
   if (!x || !residual || !out || !membrane_checkpoint)
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: null pointer");
-  if (!aligned16({x, residual, out, membrane_checkpoint}))
+  if (!aligned16({x, residual, out, membrane_checkpoint, workspace}))
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_forward: tensors must be 16-byte aligned");
-  return lif_residual_forward_impl(x, residual, out, membrane_checkpoint, int(B), int(T), int(C),
-                                   decay, threshold, reset, slope, dtype,
-                                   static_cast<hipStream_t>(stream));
+  return lif_residual_forward_impl(x, residual, out, membrane_checkpoint, workspace,
+                                   workspace_bytes, int(B), int(T), int(C), decay, threshold,
+                                   reset, slope, dtype, static_cast<hipStream_t>(stream));
 }
 
 int lif_residual_backward(const void* x, const float* grad_out, const float* membrane_checkpoint,

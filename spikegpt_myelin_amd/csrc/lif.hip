@@ -29,6 +29,9 @@
 // backward walks the blocks last to first, recomputes each block's h_t from
 // its record into registers and runs the reverse recurrence over it, so x is
 // read once by each pass and no per-step state is stored.
+#include <algorithm>
+#include <cstdlib>
+
 #include "wkv_common.h"
 
 namespace wkv {
@@ -303,12 +306,15 @@ struct Staged {
   }
 
   // Writes block `blk` of an output from LDS (steps past T and pieces past
-  // C fall outside the descriptor and are dropped).
+  // C fall outside the descriptor and are dropped; with `emit` false the
+  // descriptor is empty and every store is dropped, so that every block
+  // issues the same instructions).
   __device__ static __forceinline__ void store(raw* __restrict__ p, const u32x4* __restrict__ lds,
                                                size_t row_base, size_t row_tail, unsigned loff,
-                                               int blk, int C, int lane) {
+                                               int blk, int C, int lane, bool emit = true) {
     const int t0 = blk * kLifBlock;
-    const rsrc_t r = make_rsrc(p + row_base + size_t(t0) * C, span_bytes(row_tail, t0, C, kEs));
+    const rsrc_t r = make_rsrc(p + row_base + size_t(t0) * C,
+                               emit ? span_bytes(row_tail, t0, C, kEs) : 0u);
     const unsigned stride = unsigned(kSpi) * unsigned(C) * unsigned(kEs);
 #pragma unroll
     for (int j = 0; j < kInstr; ++j)
@@ -317,38 +323,90 @@ struct Staged {
   }
 };
 
+// ------------------------------------------- forward split over time ----
+// The membrane forgets its past at every spike (m is set to `reset`) and
+// decays by `decay` otherwise, so two runs of the recurrence from different
+// membranes over the same inputs become bit-identical after a few dozen
+// steps and then stay identical.  The forward therefore splits the sequence
+// into G.nseg segments of G.bps blocks and runs them at the same time: the
+// workgroups of segment k > 0 start G.wb blocks before the segment from a
+// zero membrane (warm-up: nothing written), then write the segment's
+// outputs and records as the sequential kernel does.  Each publishes the
+// membrane it holds at its segment's start (G.start) and after its last
+// block (G.fin).  lif_fwd_fixup_kernel then walks the boundaries in order
+// with the exact membrane; where the speculated one differs bit for bit, it
+// reruns the segment from the exact membrane beside the speculated one,
+// rewriting outputs and records that differ, until the two coincide (or to
+// the segment's end).  The results are bit-identical to the sequential
+// kernel for any input; the repair is short when the runs converge within
+// the warm-up, as they do unless |decay| is close to 1 and no spike resets
+// them.
+struct LifSeg {
+  int nseg;      // time segments (1: one pass over the whole sequence)
+  int bps;       // checkpoint blocks per segment
+  int wb;        // warm-up blocks before a segment's first block
+  float* start;  // [nseg-1][B][C]: the membrane at the start of segment k+1 as speculated
+  float* fin;    // [nseg-1][B][C]: the membrane after segment k (k < nseg-1) as computed
+};
+
+// This workgroup's segment: output blocks [lo, hi), processing from block
+// `first` (warm-up blocks [first, lo)).  Grid: nseg x B x n_cg workgroups.
+struct LifSegPos {
+  int seg, b, cg, lo, hi, first;
+  __device__ __forceinline__ LifSegPos(const LifSeg& G, int n_cg, int nblk) {
+    const int rows = int(gridDim.x) / G.nseg;
+    seg = int(blockIdx.x) / rows;
+    const int rid = int(blockIdx.x) - seg * rows;
+    b = rid / n_cg;
+    cg = rid - b * n_cg;
+    lo = seg * G.bps;
+    hi = min(nblk, lo + G.bps);
+    first = seg == 0 ? 0 : max(0, lo - G.wb);
+  }
+};
+
 template <typename E, bool CK>
 __global__ __launch_bounds__(64) void lif_fwd_staged_kernel(const typename E::raw* __restrict__ x,
                                                             typename E::raw* __restrict__ spk,
                                                             float* __restrict__ ck, int T, int C,
-                                                            LifParams P) {
+                                                            LifParams P, LifSeg G) {
   using S = Staged<E>;
   constexpr int PF = S::kPf;
   __shared__ u32x4 xs[S::kInstr * 64];
   __shared__ u32x4 os[S::kInstr * 64];
   const int n_cg = (C + 63) / 64;
-  const int b = blockIdx.x / n_cg;
-  const int cg = blockIdx.x - b * n_cg;
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const LifSegPos sp_(G, n_cg, nblk);
+  const int b = sp_.b, cg = sp_.cg, lo = sp_.lo, hi = sp_.hi;
   const int lane = threadIdx.x;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
   const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
   const unsigned loff = S::lane_off(lane, C, cg);
-  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const bool lane_ok = cg * 64 + lane < C;
   // Membrane records through a descriptor over this group's records; lanes
   // past C get an out-of-range offset (their stores are dropped).
   const size_t ck_base = size_t(b) * nblk * C + size_t(cg) * 64;
   const rsrc_t rck = make_rsrc(CK ? ck + ck_base : ck, CK ? uint32_t(((size_t(nblk) - 1) * C + 64) * 4) : 0u);
-  const unsigned ck_off = cg * 64 + lane < C ? unsigned(lane) * 4u : kOutOfRange;
+  const unsigned ck_off = lane_ok ? unsigned(lane) * 4u : kOutOfRange;
+  // The speculated membrane at this segment's start (segments after the first).
+  const size_t bc = size_t(gridDim.x / G.nseg / n_cg) * C;
+  const rsrc_t rst = make_rsrc(sp_.seg > 0 ? G.start + size_t(sp_.seg - 1) * bc + size_t(b) * C + cg * 64 : nullptr,
+                               sp_.seg > 0 ? 256u : 0u);
 
   float m = 0.f;
   // Inputs P blocks ahead wait in registers; every block issues the same
-  // loads and stores (past the end the descriptors are empty), so the
-  // compiler's wait before a block's LDS write covers only that block.
+  // loads and stores (past the segment's end, and for warm-up blocks, the
+  // descriptors or offsets are empty), so the compiler's wait before a
+  // block's LDS write covers only that block.
   auto block = [&](u32x4 (&st)[S::kInstr], int blk) {
+    const bool emit = blk >= lo;
     S::to_lds(xs, st, lane);
-    S::load(st, x, row_base, row_tail, loff, blk + PF, nblk, C);
+    S::load(st, x, row_base, row_tail, loff, blk + PF, hi, C);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rst,
+                                          blk == lo && lane_ok ? unsigned(lane) * 4u : kOutOfRange,
+                                          0, 0);
     if constexpr (CK)
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rck, ck_off,
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rck, emit ? ck_off : kOutOfRange,
                                             unsigned(blk) * unsigned(C) * 4u, kAuxNT);
 #pragma unroll
     for (int s = 0; s < kLifBlock; ++s) {
@@ -357,56 +415,69 @@ __global__ __launch_bounds__(64) void lif_fwd_staged_kernel(const typename E::ra
       m = h * (1.f - sp) + P.reset * sp;
       S::put(os, s, lane, sp);
     }
-    S::store(spk, os, row_base, row_tail, loff, blk, C, lane);
+    S::store(spk, os, row_base, row_tail, loff, blk, C, lane, emit);
   };
 
+  const int first = sp_.first;
+  const int nb = hi - first;
   u32x4 st[PF][S::kInstr];
 #pragma unroll
-  for (int q = 0; q < PF; ++q) S::load(st[q], x, row_base, row_tail, loff, q, nblk, C);
-  const int nfull = nblk - nblk % PF;
+  for (int q = 0; q < PF; ++q) S::load(st[q], x, row_base, row_tail, loff, first + q, hi, C);
+  const int nfull = nb - nb % PF;
   for (int base = 0; base < nfull; base += PF) {
 #pragma unroll
-    for (int q = 0; q < PF; ++q) block(st[q], base + q);
+    for (int q = 0; q < PF; ++q) block(st[q], first + base + q);
   }
 #pragma unroll
   for (int q = 0; q < PF - 1; ++q)
-    if (nfull + q < nblk) block(st[q], nfull + q);
+    if (nfull + q < nb) block(st[q], first + nfull + q);
+  if (sp_.seg < G.nseg - 1 && lane_ok)
+    G.fin[size_t(sp_.seg) * bc + size_t(b) * C + cg * 64 + lane] = m;
 }
 
 // Forward with the residual add of the block (language.py:1326-1330,
 // residual + spike): writes out = residual + s_t in fp32 instead of the
 // spikes, from fp32 residual rows staged like x.  out may alias residual
-// (each block is written after its own residual was read).
+// (each block is written after its own residual was read) when the
+// sequence is not split (G.nseg = 1).
 template <typename E>
 __global__ __launch_bounds__(64) void lif_fwd_residual_kernel(const typename E::raw* __restrict__ x,
                                                               const float* res, float* out,
                                                               float* __restrict__ ck, int T,
-                                                              int C, LifParams P) {
+                                                              int C, LifParams P, LifSeg G) {
   using S = Staged<E>;
   using SF = Staged<F32>;
   constexpr int PF = 3;  // blocks in flight (x and the wider residual pieces)
   __shared__ u32x4 xs[S::kInstr * 64];
   __shared__ u32x4 rs[SF::kInstr * 64];
   const int n_cg = (C + 63) / 64;
-  const int b = blockIdx.x / n_cg;
-  const int cg = blockIdx.x - b * n_cg;
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const LifSegPos sp_(G, n_cg, nblk);
+  const int b = sp_.b, cg = sp_.cg, lo = sp_.lo, hi = sp_.hi;
   const int lane = threadIdx.x;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
   const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
   const unsigned loff = S::lane_off(lane, C, cg);
   const unsigned loffr = SF::lane_off(lane, C, cg);
-  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const bool lane_ok = cg * 64 + lane < C;
   const rsrc_t rck = make_rsrc(ck + size_t(b) * nblk * C + size_t(cg) * 64,
                                uint32_t(((size_t(nblk) - 1) * C + 64) * 4));
-  const unsigned ck_off = cg * 64 + lane < C ? unsigned(lane) * 4u : kOutOfRange;
+  const unsigned ck_off = lane_ok ? unsigned(lane) * 4u : kOutOfRange;
+  const size_t bc = size_t(gridDim.x / G.nseg / n_cg) * C;
+  const rsrc_t rst = make_rsrc(sp_.seg > 0 ? G.start + size_t(sp_.seg - 1) * bc + size_t(b) * C + cg * 64 : nullptr,
+                               sp_.seg > 0 ? 256u : 0u);
 
   float m = 0.f;
   auto block = [&](u32x4 (&st)[S::kInstr], u32x4 (&sr)[SF::kInstr], int blk) {
+    const bool emit = blk >= lo;
     S::to_lds(xs, st, lane);
     SF::to_lds(rs, sr, lane);
-    S::load(st, x, row_base, row_tail, loff, blk + PF, nblk, C);
-    SF::load(sr, res, row_base, row_tail, loffr, blk + PF, nblk, C);
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rck, ck_off,
+    S::load(st, x, row_base, row_tail, loff, blk + PF, hi, C);
+    SF::load(sr, res, row_base, row_tail, loffr, blk + PF, hi, C);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rst,
+                                          blk == lo && lane_ok ? unsigned(lane) * 4u : kOutOfRange,
+                                          0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rck, emit ? ck_off : kOutOfRange,
                                           unsigned(blk) * unsigned(C) * 4u, kAuxNT);
 #pragma unroll
     for (int s = 0; s < kLifBlock; ++s) {
@@ -415,23 +486,122 @@ __global__ __launch_bounds__(64) void lif_fwd_residual_kernel(const typename E::
       m = h * (1.f - sp) + P.reset * sp;
       SF::put(rs, s, lane, SF::get(rs, s, lane) + sp);
     }
-    SF::store(out, rs, row_base, row_tail, loffr, blk, C, lane);
+    SF::store(out, rs, row_base, row_tail, loffr, blk, C, lane, emit);
   };
 
+  const int first = sp_.first;
+  const int nb = hi - first;
   u32x4 st[PF][S::kInstr], sr[PF][SF::kInstr];
 #pragma unroll
   for (int q = 0; q < PF; ++q) {
-    S::load(st[q], x, row_base, row_tail, loff, q, nblk, C);
-    SF::load(sr[q], res, row_base, row_tail, loffr, q, nblk, C);
+    S::load(st[q], x, row_base, row_tail, loff, first + q, hi, C);
+    SF::load(sr[q], res, row_base, row_tail, loffr, first + q, hi, C);
   }
-  const int nfull = nblk - nblk % PF;
+  const int nfull = nb - nb % PF;
   for (int base = 0; base < nfull; base += PF) {
 #pragma unroll
-    for (int q = 0; q < PF; ++q) block(st[q], sr[q], base + q);
+    for (int q = 0; q < PF; ++q) block(st[q], sr[q], first + base + q);
   }
 #pragma unroll
   for (int q = 0; q < PF - 1; ++q)
-    if (nfull + q < nblk) block(st[q], sr[q], nfull + q);
+    if (nfull + q < nb) block(st[q], sr[q], first + nfull + q);
+  if (sp_.seg < G.nseg - 1 && lane_ok)
+    G.fin[size_t(sp_.seg) * bc + size_t(b) * C + cg * 64 + lane] = m;
+}
+
+// Repair pass of the split forward: one wave per (batch, 64 channels), one
+// lane per channel, boundaries in time order.  RES: `out` = residual +
+// spike in fp32 (`res` must not alias `out`), else `spk` = spike.
+constexpr int kLifMaxSeg = 16;
+constexpr int kLifFixChunk = 16;  // steps loaded at once while rerunning
+
+template <typename E, bool CK, bool RES>
+__global__ __launch_bounds__(64) void lif_fwd_fixup_kernel(const typename E::raw* __restrict__ x,
+                                                           const float* __restrict__ res,
+                                                           typename E::raw* __restrict__ spk,
+                                                           float* __restrict__ out,
+                                                           float* __restrict__ ck, int B, int T,
+                                                           int C, LifParams P, LifSeg G) {
+  const int n_cg = (C + 63) / 64;
+  const int b = int(blockIdx.x) / n_cg;
+  const int cg = int(blockIdx.x) - b * n_cg;
+  const int c = cg * 64 + int(threadIdx.x);
+  const bool ok = c < C;
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const size_t bc = size_t(B) * C;
+  const size_t at = size_t(b) * C + size_t(ok ? c : 0);
+  // Fast path: when every segment's speculated start equals the membrane
+  // the previous segment ended with, each segment ran from the exact
+  // membrane (by induction from segment 0, which starts at m = 0), and
+  // nothing needs repair.  All boundary values are loaded at once.
+  // (No short-circuit: the loads of all boundaries are issued together.)
+  // The values are kept in LDS for the general path, which indexes them by a
+  // run-time boundary number.
+  __shared__ float lst[kLifMaxSeg - 1][64], lfi[kLifMaxSeg - 1][64];
+  const int lane = int(threadIdx.x);
+  // Every slot loads (past the last boundary it re-reads the last one), so
+  // the loads form one straight run with a single wait.
+  unsigned differ = 0;
+#pragma unroll
+  for (int k = 0; k < kLifMaxSeg - 1; ++k) {
+    const int kk = min(k, G.nseg - 2);
+    const float s0 = G.start[size_t(kk) * bc + at];
+    const float f0 = G.fin[size_t(kk) * bc + at];
+    differ |= __float_as_uint(s0) ^ __float_as_uint(f0);
+    lst[k][lane] = s0;
+    lfi[k][lane] = f0;
+  }
+  const bool verified = differ == 0;
+  if (!__any(ok && !verified)) return;
+  // General path: boundaries in order with the exact membrane.  (One wave
+  // per workgroup: the LDS values above are this wave's own, in order.)
+  float carry = lfi[0][lane];  // segment 0 starts from the exact membrane
+  for (int k = 1; k < G.nseg; ++k) {
+    const float spec = lst[k - 1][lane];
+    bool todo = ok && __float_as_uint(carry) != __float_as_uint(spec);
+    float m = carry, ms = spec;
+    const int t_lo = k * G.bps * kLifBlock;
+    const int t_hi = min(T, t_lo + G.bps * kLifBlock);
+    for (int t0 = t_lo; t0 < t_hi && __any(todo); t0 += kLifFixChunk) {
+      float xv[kLifFixChunk], rv[kLifFixChunk];
+#pragma unroll
+      for (int j = 0; j < kLifFixChunk; ++j) {
+        const int t = t0 + j;
+        const size_t i = (size_t(b) * T + size_t(t)) * C + size_t(c);
+        xv[j] = todo && t < t_hi ? load_scalar<E>(x + i) : 0.f;
+        rv[j] = RES && todo && t < t_hi ? res[i] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kLifFixChunk; ++j) {
+        const int t = t0 + j;
+        // Steps past the segment leave every value unchanged (todo is off).
+        const bool live = todo && t < t_hi;
+        if (CK && live && t % kLifBlock == 0) ck[(size_t(b) * nblk + t / kLifBlock) * C + c] = m;
+        const float h = m * P.decay + xv[j];
+        const float s = P.slope * (h - P.threshold) >= 0.f ? 1.f : 0.f;
+        const float mn = h * (1.f - s) + P.reset * s;
+        const float hs = ms * P.decay + xv[j];
+        const float ss = P.slope * (hs - P.threshold) >= 0.f ? 1.f : 0.f;
+        const float msn = hs * (1.f - ss) + P.reset * ss;
+        if (live && s != ss) {
+          const size_t i = (size_t(b) * T + size_t(t)) * C + size_t(c);
+          if constexpr (RES) {
+            out[i] = rv[j] + s;
+          } else {
+            store_scalar<E>(spk + i, s);
+          }
+        }
+        if (t < t_hi) {
+          m = mn;
+          ms = msn;
+        }
+        if (live && __float_as_uint(m) == __float_as_uint(ms)) todo = false;
+      }
+    }
+    // Into segment k+1: the computed membrane after segment k is exact
+    // unless this lane never coincided with the speculated run.
+    if (k < G.nseg - 1) carry = todo ? m : lfi[k][lane];
+  }
 }
 
 // G is the type of the incoming gradient: E, or fp32 when the spikes were
@@ -575,20 +745,87 @@ static bool lif_staged_ok(int T, int C) {
   return C % (16 / int(sizeof(typename E::raw))) == 0 && span < (size_t(1) << 31);
 }
 
+// Split forward: time segments for these sizes (1: no split).  Enough
+// segments for ~4096 waves (four per SIMD) while every segment keeps at
+// least 4 blocks (128 steps); WKV_LIF_SEGS overrides (measurement).
+// Measured at B=64 T=1024 C=512 bf16 (forward, warm-up 2 blocks): one pass
+// 56.6 us; 2 segments 40.1, 4 segments 33.5, 8 segments 31.8 us.
+static int lif_fwd_nseg(int64_t B, int64_t T, int64_t C) {
+  const int64_t nblk = (T + wkv::kLifBlock - 1) / wkv::kLifBlock;
+  const int64_t rows = B * ((C + 63) / 64);
+  if (nblk <= 1 || rows <= 0) return 1;  // empty or one block: nothing to split
+  int64_t n = 1;
+  if (const char* e = getenv("WKV_LIF_SEGS")) {
+    n = std::min<int64_t>(std::max(atoi(e), 1), wkv::kLifMaxSeg);
+  } else {
+    while (n < wkv::kLifMaxSeg && rows * n < 4096 && 2 * n * 4 <= nblk) n *= 2;
+  }
+  n = std::min<int64_t>(n, nblk);
+  const int64_t bps = (nblk + n - 1) / n;  // >= 1
+  return int((nblk + bps - 1) / bps);
+}
+
+// Warm-up blocks of a segment after the first (WKV_LIF_WARMUP overrides).
+// Two (64 steps): with one, enough channels still differ at the boundary
+// that the repair costs more than the second block (B=64 T=1024 C=512, 4
+// segments: repair 10.8 us after one block, 4.6 us after two or three).
+static int lif_fwd_warmup() {
+  if (const char* e = getenv("WKV_LIF_WARMUP")) return std::min(std::max(atoi(e), 0), 8);
+  return 2;
+}
+
+size_t lif_fwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
+  const int n = lif_fwd_nseg(B, T, C);
+  if (n <= 1) return 0;
+  return size_t(2) * size_t(n - 1) * size_t(B) * size_t(C) * sizeof(float);
+}
+
+// The split's layout for these sizes when `ws` holds enough bytes, else one
+// segment (the sequential pass).
+static wkv::LifSeg lif_fwd_seg(void* ws, size_t ws_bytes, int B, int T, int C) {
+  const int nblk = (T + wkv::kLifBlock - 1) / wkv::kLifBlock;
+  wkv::LifSeg G{1, nblk, 0, nullptr, nullptr};
+  const size_t need = lif_fwd_workspace_bytes_impl(B, T, C);
+  if (need == 0 || ws == nullptr || ws_bytes < need) return G;
+  const int n = lif_fwd_nseg(B, T, C);
+  G.nseg = n;
+  G.bps = (nblk + n - 1) / n;
+  G.wb = lif_fwd_warmup();
+  G.start = static_cast<float*>(ws);
+  G.fin = G.start + size_t(n - 1) * size_t(B) * size_t(C);
+  return G;
+}
+
 template <typename E>
-static int lif_fwd_dispatch(const void* x, void* spk, float* ck, int B, int T, int C,
-                            const wkv::LifParams& P, hipStream_t stream) {
+static int lif_fwd_dispatch(const void* x, void* spk, float* ck, void* ws, size_t ws_bytes, int B,
+                            int T, int C, const wkv::LifParams& P, hipStream_t stream) {
   using raw = typename E::raw;
   if (lif_staged_ok<E>(T, C)) {
-    const dim3 grid(unsigned(B) * unsigned((C + 63) / 64));
+    const wkv::LifSeg G = lif_fwd_seg(ws, ws_bytes, B, T, C);
+    const unsigned rows = unsigned(B) * unsigned((C + 63) / 64);
+    const dim3 grid(rows * unsigned(G.nseg));
+    const bool last = G.nseg == 1;
     if (ck != nullptr) {
-      launch(wkv::lif_fwd_staged_kernel<E, true>, grid, dim3(64), stream, true,
-             static_cast<const raw*>(x), static_cast<raw*>(spk), ck, T, C, P);
+      launch(wkv::lif_fwd_staged_kernel<E, true>, grid, dim3(64), stream, last,
+             static_cast<const raw*>(x), static_cast<raw*>(spk), ck, T, C, P, G);
     } else {
-      launch(wkv::lif_fwd_staged_kernel<E, false>, grid, dim3(64), stream, true,
-             static_cast<const raw*>(x), static_cast<raw*>(spk), ck, T, C, P);
+      launch(wkv::lif_fwd_staged_kernel<E, false>, grid, dim3(64), stream, last,
+             static_cast<const raw*>(x), static_cast<raw*>(spk), ck, T, C, P, G);
     }
-    return check_launch("lif_fwd_staged_kernel");
+    if (const int rc = check_launch("lif_fwd_staged_kernel")) return rc;
+    if (G.nseg > 1) {
+      if (ck != nullptr) {
+        launch(wkv::lif_fwd_fixup_kernel<E, true, false>, dim3(rows), dim3(64), stream, true,
+               static_cast<const raw*>(x), static_cast<const float*>(nullptr),
+               static_cast<raw*>(spk), static_cast<float*>(nullptr), ck, B, T, C, P, G);
+      } else {
+        launch(wkv::lif_fwd_fixup_kernel<E, false, false>, dim3(rows), dim3(64), stream, true,
+               static_cast<const raw*>(x), static_cast<const float*>(nullptr),
+               static_cast<raw*>(spk), static_cast<float*>(nullptr), ck, B, T, C, P, G);
+      }
+      return check_launch("lif_fwd_fixup_kernel");
+    }
+    return 0;
   }
   return lif_vec(B, C, int(sizeof(typename E::raw))) == 2 ? lif_fwd_launch<E, 2>(x, spk, ck, B, T, C, P, stream)
                             : lif_fwd_launch<E, 1>(x, spk, ck, B, T, C, P, stream);
@@ -609,12 +846,26 @@ static int lif_bwd_dispatch(const void* x, const void* gs, const float* ck, void
 }
 
 // Residual variants: staged kernels only (the caller checks lif_residual_ok).
+// The split needs `out` and `res` disjoint (the repair reads the residual).
 template <typename E>
-static int lif_residual_fwd(const void* x, const float* res, float* out, float* ck, int B, int T,
-                            int C, const wkv::LifParams& P, hipStream_t stream) {
-  launch(wkv::lif_fwd_residual_kernel<E>, dim3(unsigned(B) * unsigned((C + 63) / 64)), dim3(64),
-         stream, true, static_cast<const typename E::raw*>(x), res, out, ck, T, C, P);
-  return check_launch("lif_fwd_residual_kernel");
+static int lif_residual_fwd(const void* x, const float* res, float* out, float* ck, void* ws,
+                            size_t ws_bytes, int B, int T, int C, const wkv::LifParams& P,
+                            hipStream_t stream) {
+  using raw = typename E::raw;
+  const size_t n = size_t(B) * size_t(T) * size_t(C);
+  const bool disjoint = out + n <= res || res + n <= out;
+  const wkv::LifSeg G = disjoint ? lif_fwd_seg(ws, ws_bytes, B, T, C)
+                                 : lif_fwd_seg(nullptr, 0, B, T, C);
+  const unsigned rows = unsigned(B) * unsigned((C + 63) / 64);
+  launch(wkv::lif_fwd_residual_kernel<E>, dim3(rows * unsigned(G.nseg)), dim3(64), stream,
+         G.nseg == 1, static_cast<const raw*>(x), res, out, ck, T, C, P, G);
+  if (const int rc = check_launch("lif_fwd_residual_kernel")) return rc;
+  if (G.nseg > 1) {
+    launch(wkv::lif_fwd_fixup_kernel<E, true, true>, dim3(rows), dim3(64), stream, true,
+           static_cast<const raw*>(x), res, static_cast<raw*>(nullptr), out, ck, B, T, C, P, G);
+    return check_launch("lif_fwd_fixup_kernel");
+  }
+  return 0;
 }
 
 template <typename E>
@@ -634,14 +885,14 @@ bool lif_residual_ok(int64_t T, int64_t C, int dtype) {
   return C % 8 == 0 && size_t(T) * size_t(C) * 4 < (size_t(1) << 31);
 }
 
-int lif_residual_forward_impl(const void* x, const float* res, float* out, float* ck, int B,
-                              int T, int C, float decay, float threshold, float reset,
-                              float slope, int dtype, hipStream_t stream) {
+int lif_residual_forward_impl(const void* x, const float* res, float* out, float* ck, void* ws,
+                              size_t ws_bytes, int B, int T, int C, float decay, float threshold,
+                              float reset, float slope, int dtype, hipStream_t stream) {
   const wkv::LifParams P{decay, threshold, reset, slope};
   switch (dtype) {
-    case 0: return lif_residual_fwd<wkv::F32>(x, res, out, ck, B, T, C, P, stream);
-    case 1: return lif_residual_fwd<wkv::BF16>(x, res, out, ck, B, T, C, P, stream);
-    case 2: return lif_residual_fwd<wkv::F16>(x, res, out, ck, B, T, C, P, stream);
+    case 0: return lif_residual_fwd<wkv::F32>(x, res, out, ck, ws, ws_bytes, B, T, C, P, stream);
+    case 1: return lif_residual_fwd<wkv::BF16>(x, res, out, ck, ws, ws_bytes, B, T, C, P, stream);
+    case 2: return lif_residual_fwd<wkv::F16>(x, res, out, ck, ws, ws_bytes, B, T, C, P, stream);
     default: return fail(1, "lif_residual_forward: unknown dtype");
   }
 }
@@ -658,13 +909,14 @@ int lif_residual_backward_impl(const void* x, const float* g, const float* ck, v
   }
 }
 
-int lif_forward_impl(const void* x, void* spk, float* ck, int B, int T, int C, float decay,
-                     float threshold, float reset, float slope, int dtype, hipStream_t stream) {
+int lif_forward_impl(const void* x, void* spk, float* ck, void* ws, size_t ws_bytes, int B, int T,
+                     int C, float decay, float threshold, float reset, float slope, int dtype,
+                     hipStream_t stream) {
   const wkv::LifParams P{decay, threshold, reset, slope};
   switch (dtype) {
-    case 0: return lif_fwd_dispatch<wkv::F32>(x, spk, ck, B, T, C, P, stream);
-    case 1: return lif_fwd_dispatch<wkv::BF16>(x, spk, ck, B, T, C, P, stream);
-    case 2: return lif_fwd_dispatch<wkv::F16>(x, spk, ck, B, T, C, P, stream);
+    case 0: return lif_fwd_dispatch<wkv::F32>(x, spk, ck, ws, ws_bytes, B, T, C, P, stream);
+    case 1: return lif_fwd_dispatch<wkv::BF16>(x, spk, ck, ws, ws_bytes, B, T, C, P, stream);
+    case 2: return lif_fwd_dispatch<wkv::F16>(x, spk, ck, ws, ws_bytes, B, T, C, P, stream);
     default: return fail(1, "lif_forward: unknown dtype");
   }
 }

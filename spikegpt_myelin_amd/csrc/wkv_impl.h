@@ -85,12 +85,17 @@ int shift_mix_forward_impl(const void*, int, const float*, void* const*, int, in
                            hipStream_t);
 int shift_mix_backward_impl(const void*, int, const float*, const void* const*, int, void*, float*,
                             float*, int, int, int, int, hipStream_t);
-int lif_forward_impl(const void*, void*, float*, int, int, int, float, float, float, float, int,
-                     hipStream_t);
+// Sequence LIF (lif.hip).  ws (may be null): workspace of the split
+// forward, lif_fwd_workspace_bytes_impl bytes (0: no split for these sizes).
+int lif_forward_impl(const void* x, void* spk, float* ck, void* ws, size_t ws_bytes, int B, int T,
+                     int C, float decay, float threshold, float reset, float slope, int dtype,
+                     hipStream_t stream);
+size_t lif_fwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C);
 int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
                       float, float, int, hipStream_t);
-int lif_residual_forward_impl(const void*, const float*, float*, float*, int, int, int, float,
-                              float, float, float, int, hipStream_t);
+int lif_residual_forward_impl(const void* x, const float* res, float* out, float* ck, void* ws,
+                              size_t ws_bytes, int B, int T, int C, float decay, float threshold,
+                              float reset, float slope, int dtype, hipStream_t stream);
 int lif_residual_backward_impl(const void*, const float*, const float*, void*, int, int, int,
                                float, float, float, float, int, hipStream_t);
 bool lif_residual_ok(int64_t, int64_t, int);

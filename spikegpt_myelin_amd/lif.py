@@ -39,6 +39,15 @@ def checkpoint_shape(b: int, t: int, c: int) -> tuple[int, int, int]:
     return (b, (t + CKPT_BLOCK - 1) // CKPT_BLOCK, c)
 
 
+def _forward_workspace(lib, b: int, t: int, c: int, device) -> tuple[Tensor | None, int]:
+    """Workspace of the forward's split over time (boundary membranes), or
+    (None, 0) for sizes that run as one pass."""
+    nbytes = int(lib.lif_forward_workspace_bytes(b, t, c))
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
 def _native(x: Tensor) -> Tensor:
     return _lib.aligned(x if x.dtype in _NATIVE else x.float())
 
@@ -55,9 +64,10 @@ def _lif_forward(
     spikes = torch.empty_like(xs)
     ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=x.device)
     lib = _lib.load()
+    ws, nbytes = _forward_workspace(lib, b, t, c, x.device)
     rc = _lib.timed("lif_forward", x.device, lambda: lib.lif_forward(
-        xs.data_ptr(), spikes.data_ptr(), ck.data_ptr(), b, t, c, decay, threshold, reset, slope,
-        _lib.dtype_code(xs.dtype), _lib.stream_of(xs),
+        xs.data_ptr(), spikes.data_ptr(), ck.data_ptr(), _lib.ptr(ws), nbytes, b, t, c, decay,
+        threshold, reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs),
     ))
     _lib.check(rc, "lif_forward")
     return spikes, ck
@@ -160,9 +170,10 @@ def _lif_res_forward(x: Tensor, residual: Tensor, decay: float, threshold: float
     out = torch.empty_like(rs)
     ck = torch.empty(checkpoint_shape(b, t, c), dtype=torch.float32, device=x.device)
     lib = _lib.load()
+    ws, nbytes = _forward_workspace(lib, b, t, c, x.device)
     rc = _lib.timed("lif_residual_forward", x.device, lambda: lib.lif_residual_forward(
-        xs.data_ptr(), rs.data_ptr(), out.data_ptr(), ck.data_ptr(), b, t, c, decay, threshold,
-        reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs)))
+        xs.data_ptr(), rs.data_ptr(), out.data_ptr(), ck.data_ptr(), _lib.ptr(ws), nbytes, b, t, c,
+        decay, threshold, reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs)))
     _lib.check(rc, "lif_residual_forward")
     return out, ck
 

@@ -79,6 +79,22 @@ def test_backward_workspace_size_and_check(lib):
     assert rc == 3 and b"workspace" in lib.wkv_last_error_string()
 
 
+def test_lif_forward_workspace_sizes(lib, monkeypatch):
+    # Empty and one-block sequences are never split (no workspace); the 41M
+    # activation shape splits into eight segments: the start and end
+    # membranes of the seven inner boundaries, fp32.  Forced segment counts are capped
+    # by the number of 32-step blocks.
+    for b, t, c in [(0, 5, 8), (2, 0, 8), (2, 5, 0), (3, 1, 96), (4, 32, 64), (1, 1, 1)]:
+        assert lib.lif_forward_workspace_bytes(b, t, c) == 0, (b, t, c)
+    assert lib.lif_forward_workspace_bytes(64, 1024, 512) == 2 * 7 * 64 * 512 * 4
+    assert lib.lif_forward_workspace_bytes(16, 1024, 768) == 2 * 7 * 16 * 768 * 4
+    monkeypatch.setenv("WKV_LIF_SEGS", "16")
+    assert lib.lif_forward_workspace_bytes(2, 100, 70) == 2 * 3 * 2 * 70 * 4  # 4 blocks
+    assert lib.lif_forward_workspace_bytes(2, 0, 70) == 0
+    monkeypatch.setenv("WKV_LIF_SEGS", "1")
+    assert lib.lif_forward_workspace_bytes(64, 1024, 512) == 0
+
+
 def test_step_row_args_layout_matches_header(tmp_path):
     # The ctypes mirror of wkv_step_row_args has the C struct's size and field
     # offsets (compiled with the host C compiler from the header).

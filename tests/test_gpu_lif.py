@@ -164,3 +164,104 @@ def test_residual_full_size():
     (gx,) = torch.autograd.grad(out, xd, gout.to(DEV))
     _check_grad(gx, L.lif_reverse(x.float(), gout, forward_dtype=torch.float32),
                 torch.bfloat16, "residual grad_x full size")
+
+
+# Split over time of the forward: segments run at once from a guessed
+# membrane and a repair pass makes them exact, so every output and record
+# must equal the one-pass kernel's bit for bit.  Parameter sets: the model's
+# (the runs converge within the warm-up), a negative decay (tau 0.7), and a
+# slow leak with a constant drive (tau 100: the guessed and exact runs spike
+# with different phases and never coincide, so the repair reruns whole
+# segments).
+LIF_PARAMS = {
+    "model": dict(tau=2.0, threshold=1.0, reset=0.0, slope=2.0, scale=1.5, const=None),
+    "negative_decay": dict(tau=0.7, threshold=1.0, reset=-0.5, slope=2.0, scale=1.5, const=None),
+    "no_convergence": dict(tau=100.0, threshold=1.0, reset=0.0, slope=2.0, scale=0.0,
+                           const=0.02),
+}
+
+
+def _lif_case(b, t, c, dtype, kind, seed):
+    p = LIF_PARAMS[kind]
+    if p["const"] is not None:
+        x = torch.full((b, t, c), p["const"]).to(dtype)
+        # channels start from different drives so their phases differ
+        x = (x.float() * (1 + torch.arange(c) / (2 * c))).to(dtype)
+    else:
+        x, _ = _inputs(b, t, c, dtype, seed=seed, scale=p["scale"])
+    return x, p
+
+
+def _forward(x, p):
+    ops = _ops()
+    s, ck = ops.lif_sequence_forward(x.to(DEV), 1.0 - 1.0 / p["tau"], p["threshold"], p["reset"],
+                                     p["slope"])
+    torch.cuda.synchronize()
+    return s.cpu(), ck.cpu()
+
+
+@pytest.mark.parametrize("kind", list(LIF_PARAMS))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 100, 70), (3, 257, 256), (1, 1000, 128), (2, 300, 136)])
+def test_split_forward_equals_one_pass(kind, dtype, shape, monkeypatch):
+    b, t, c = shape
+    x, p = _lif_case(b, t, c, dtype, kind, seed=t + c)
+    print(f"lif split {kind} {dtype} {shape}", flush=True)
+    monkeypatch.setenv("WKV_LIF_SEGS", "1")
+    s1, ck1 = _forward(x, p)
+    ref = L.lif_loop(x.float(), p["tau"], p["threshold"], p["reset"], p["slope"]).to(dtype)
+    assert torch.equal(s1, ref)
+    for segs in ("2", "3", "5", "16"):
+        for warm in ("0", "1", "2"):
+            monkeypatch.setenv("WKV_LIF_SEGS", segs)
+            monkeypatch.setenv("WKV_LIF_WARMUP", warm)
+            s2, ck2 = _forward(x, p)
+            assert torch.equal(s2, s1), f"spikes: {segs} segments, warm-up {warm}"
+            assert torch.equal(ck2.view(torch.int32), ck1.view(torch.int32)), \
+                f"records: {segs} segments, warm-up {warm}"
+
+
+@pytest.mark.parametrize("kind", list(LIF_PARAMS))
+@pytest.mark.parametrize("shape", [(2, 100, 64), (3, 257, 256), (1, 1000, 136)])
+def test_split_residual_forward_equals_one_pass(kind, shape, monkeypatch):
+    from spikegpt_myelin_amd import _lib
+
+    ops = _ops()
+    b, t, c = shape
+    x, p = _lif_case(b, t, c, torch.bfloat16, kind, seed=b + t)
+    residual = torch.randn(b, t, c, generator=torch.Generator().manual_seed(t))
+    decay = 1.0 - 1.0 / p["tau"]
+    args = (decay, p["threshold"], p["reset"], p["slope"])
+    print(f"lif residual split {kind} {shape}", flush=True)
+    monkeypatch.setenv("WKV_LIF_SEGS", "1")
+    o1, ck1 = ops.lif_residual_forward(x.to(DEV), residual.to(DEV), *args)
+    spikes = L.lif_loop(x.float(), p["tau"], p["threshold"], p["reset"], p["slope"])
+    assert torch.equal(o1.cpu(), residual + spikes)
+    for segs in ("2", "5", "16"):
+        monkeypatch.setenv("WKV_LIF_SEGS", segs)
+        o2, ck2 = ops.lif_residual_forward(x.to(DEV), residual.to(DEV), *args)
+        assert torch.equal(o2, o1), f"out: {segs} segments"
+        assert torch.equal(ck2.view(torch.int32), ck1.view(torch.int32)), f"records: {segs}"
+    # In place (out aliasing the residual) through the C ABI: the one-pass
+    # kernel runs whatever the workspace, with the same result.
+    lib = _lib.load()
+    inplace = residual.to(DEV).clone()
+    xd = x.to(DEV)
+    ck = torch.empty_like(ck1, device=DEV)
+    nbytes = int(lib.lif_forward_workspace_bytes(b, t, c))
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=DEV)
+    _lib.check(lib.lif_residual_forward(
+        xd.data_ptr(), inplace.data_ptr(), inplace.data_ptr(), ck.data_ptr(), ws.data_ptr(), nbytes,
+        b, t, c, *args, _lib.dtype_code(xd.dtype), torch.cuda.current_stream().cuda_stream),
+        "lif_residual_forward in place")
+    torch.cuda.synchronize()
+    assert torch.equal(inplace, o1)
+    assert torch.equal(ck.cpu().view(torch.int32), ck1.cpu().view(torch.int32))
+
+
+def test_default_split_at_the_benchmark_shape():
+    # B=64, T=1024, C=512: the sizes alone pick the split (eight segments),
+    # and the full-size tests above ran it.
+    from spikegpt_myelin_amd import _lib
+
+    assert int(_lib.load().lif_forward_workspace_bytes(64, 1024, 512)) == 2 * 7 * 64 * 512 * 4

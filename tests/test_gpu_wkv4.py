@@ -132,7 +132,8 @@ def test_fp32_op_channels_not_multiple_of_block():
 
 @pytest.mark.parametrize(
     "b,t,c,seed",
-    [(2, 128, 512, 0), (3, 300, 96, 1), (2, 513, 64, 2), (1, 5, 33, 3), (4, 1000, 130, 4)],
+    [(2, 128, 512, 0), (3, 300, 96, 1), (2, 513, 64, 2), (1, 5, 33, 3), (4, 1000, 130, 4),
+     (2, 1024, 768, 5)],  # the last: the 216M class's width in fp32
 )
 def test_fp32_op_benchmark_distributions(b, t, c, seed):
     # config distributions: td ~ U(-5, 1), tf ~ N(0, 0.5), k clamped to +-30.
