@@ -586,15 +586,17 @@ def bench_lif(args) -> dict:
     sp = stream.cuda_stream
     ws_bytes = int(lib.lif_forward_workspace_bytes(B, T, C))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    xp, spkp, ckp, gsp, gxp, wsp = (t.data_ptr() for t in (x, spk, ck, gs, gx, ws))
+    bws_bytes = int(lib.lif_backward_workspace_bytes(B, T, C))
+    bws = torch.empty(max(bws_bytes, 16), dtype=torch.uint8, device=dev)
+    xp, spkp, ckp, gsp, gxp, wsp, bwsp = (t.data_ptr() for t in (x, spk, ck, gs, gx, ws, bws))
 
     def fwd():
         _lib.check(lib.lif_forward(xp, spkp, ckp, wsp, ws_bytes, B, T, C, decay, thr, reset, slope,
                                    code, sp), "lif forward")
 
     def bwd():
-        _lib.check(lib.lif_backward(xp, gsp, ckp, gxp, B, T, C, decay, thr, reset, slope, code, sp),
-                   "lif backward")
+        _lib.check(lib.lif_backward(xp, gsp, ckp, gxp, bwsp, bws_bytes, B, T, C, decay, thr, reset,
+                                    slope, code, sp), "lif backward")
 
     pool = EventPool(4 * args.steps, stream)
     for _ in range(args.warmup):
@@ -636,6 +638,7 @@ def bench_lif(args) -> dict:
         "fwd_launch_us": fwd_t * 1e6, "bwd_launch_us": bwd_t * 1e6,
         "fwd_gbps_algorithmic": 4 * n / fwd_t / 1e9,
         "fwd_time_segments": int(ws_bytes // (8 * B * C)) + 1 if ws_bytes else 1,
+        "bwd_time_segments": int(bws_bytes // (8 * B * C)) + 1 if bws_bytes else 1,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "lif_bwd_kernel",
                      "algorithmic_bytes_per_launch": bwd_bytes, "avg_launch_us": bwd_t * 1e6},

@@ -249,16 +249,24 @@ int lif_forward(const void* x, void* spikes, float* membrane_checkpoint, void* w
                 size_t workspace_bytes, int64_t B, int64_t T, int64_t C, float decay,
                 float threshold, float reset, float slope, int dtype, void* stream);
 
+/* Bytes of device workspace lif_backward and lif_residual_backward use to
+ * split the sequence over time (the gradient carries at the segment
+ * boundaries, fp32); 0 when these sizes are not split.  With a smaller or
+ * NULL workspace the backward runs as one pass, with the same results bit
+ * for bit. */
+size_t lif_backward_workspace_bytes(int64_t B, int64_t T, int64_t C);
+
 /* Sequence LIF backward: grad_x [B,T,C] in `dtype` from x, grad_spikes and the
  * forward's membrane checkpoints, with the arctan surrogate derivative
  * ds/dh = slope * 0.5 / (1 + (pi/2 * slope*(h - threshold))^2) and the reset
  * path differentiated (autograd through language.py:833-839).  The
  * surrogate's exact form lives in the external myelin package, absent from
  * the reference tree; this is SpikingJelly's ATan surrogate with alpha =
- * slope. */
+ * slope.  workspace (may be NULL): lif_backward_workspace_bytes() bytes. */
 int lif_backward(const void* x, const void* grad_spikes, const float* membrane_checkpoint,
-                 void* grad_x, int64_t B, int64_t T, int64_t C, float decay, float threshold,
-                 float reset, float slope, int dtype, void* stream);
+                 void* grad_x, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                 int64_t C, float decay, float threshold, float reset, float slope, int dtype,
+                 void* stream);
 
 /* Bytes of device workspace token_shift_mix_backward needs for n mixing
  * vectors (per-(batch, 64-step chunk) partial sums, fp32). */
@@ -333,10 +341,12 @@ int lif_residual_forward(const void* x, const float* residual, float* out,
                          float reset, float slope, int dtype, void* stream);
 
 /* Backward of lif_residual_forward for x: grad_x (`dtype`) from grad_out
- * (fp32, the gradient of out; the residual's gradient is grad_out itself). */
+ * (fp32, the gradient of out; the residual's gradient is grad_out itself);
+ * workspace as lif_backward. */
 int lif_residual_backward(const void* x, const float* grad_out, const float* membrane_checkpoint,
-                          void* grad_x, int64_t B, int64_t T, int64_t C, float decay,
-                          float threshold, float reset, float slope, int dtype, void* stream);
+                          void* grad_x, void* workspace, size_t workspace_bytes, int64_t B,
+                          int64_t T, int64_t C, float decay, float threshold, float reset,
+                          float slope, int dtype, void* stream);
 
 /* ---- Layer norm fused into the token-shift mix -----------------------------
  *

@@ -99,14 +99,15 @@ SIGNATURES = {
         _INT,
         [_P, _P, _P, _P, _SZ, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
     ),
+    "lif_backward_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "lif_backward": (
         _INT,
-        [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
+        [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P],
     ),
     "lif_residual_forward": (
         _INT, [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P]),
     "lif_residual_backward": (
-        _INT, [_P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P]),
+        _INT, [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _F, _F, _F, _F, _INT, _P]),
     "token_shift_mix_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "token_shift_mix_forward": (
         _INT,

@@ -495,6 +495,11 @@ size_t lif_forward_workspace_bytes(int64_t B, int64_t T, int64_t C) {
   return lif_fwd_workspace_bytes_impl(B, T, C);
 }
 
+size_t lif_backward_workspace_bytes(int64_t B, int64_t T, int64_t C) {
+  if (!dims_ok(B, T, C)) return 0;
+  return lif_bwd_workspace_bytes_impl(B, T, C);
+}
+
 static bool lif_params_ok(float decay, float threshold, float reset, float slope) {
   return std::isfinite(decay) && std::isfinite(threshold) && std::isfinite(reset) &&
          std::isfinite(slope) && slope > 0.f;
@@ -544,8 +549,9 @@ int lif_residual_forward(const void* x, const float* residual, float* out,
 }
 
 int lif_residual_backward(const void* x, const float* grad_out, const float* membrane_checkpoint,
-                          void* grad_x, int64_t B, int64_t T, int64_t C, float decay,
-                          float threshold, float reset, float slope, int dtype, void* stream) {
+                          void* grad_x, void* workspace, size_t workspace_bytes, int64_t B,
+                          int64_t T, int64_t C, float decay, float threshold, float reset,
+                          float slope, int dtype, void* stream) {
   set_error("");
   TimingScope timing;
   if (!dtype_ok(dtype))
@@ -560,16 +566,17 @@ int lif_residual_backward(const void* x, const float* grad_out, const float* mem
                 "lif_residual_backward: C must be a multiple of 8 and T*C*4 below 2^31");
   if (!x || !grad_out || !membrane_checkpoint || !grad_x)
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_backward: null pointer");
-  if (!aligned16({x, grad_out, membrane_checkpoint, grad_x}))
+  if (!aligned16({x, grad_out, membrane_checkpoint, grad_x, workspace}))
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_residual_backward: tensors must be 16-byte aligned");
-  return lif_residual_backward_impl(x, grad_out, membrane_checkpoint, grad_x, int(B), int(T),
-                                    int(C), decay, threshold, reset, slope, dtype,
-                                    static_cast<hipStream_t>(stream));
+  return lif_residual_backward_impl(x, grad_out, membrane_checkpoint, grad_x, workspace,
+                                    workspace_bytes, int(B), int(T), int(C), decay, threshold,
+                                    reset, slope, dtype, static_cast<hipStream_t>(stream));
 }
 
 int lif_backward(const void* x, const void* grad_spikes, const float* membrane_checkpoint,
-                 void* grad_x, int64_t B, int64_t T, int64_t C, float decay, float threshold,
-                 float reset, float slope, int dtype, void* stream) {
+                 void* grad_x, void* workspace, size_t workspace_bytes, int64_t B, int64_t T,
+                 int64_t C, float decay, float threshold, float reset, float slope, int dtype,
+                 void* stream) {
   set_error("");
   TimingScope timing;
   if (!dtype_ok(dtype)) return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: unknown dtype");
@@ -580,11 +587,11 @@ int lif_backward(const void* x, const void* grad_spikes, const float* membrane_c
   if (B == 0 || T == 0 || C == 0) return WKV_OK;
   if (!x || !grad_spikes || !membrane_checkpoint || !grad_x)
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: null pointer");
-  if (!aligned16({x, grad_spikes, membrane_checkpoint, grad_x}))
+  if (!aligned16({x, grad_spikes, membrane_checkpoint, grad_x, workspace}))
     return fail(WKV_ERR_INVALID_ARGUMENT, "lif_backward: tensors must be 16-byte aligned");
-  return lif_backward_impl(x, grad_spikes, membrane_checkpoint, grad_x, int(B), int(T), int(C),
-                           decay, threshold, reset, slope, dtype,
-                           static_cast<hipStream_t>(stream));
+  return lif_backward_impl(x, grad_spikes, membrane_checkpoint, grad_x, workspace,
+                           workspace_bytes, int(B), int(T), int(C), decay, threshold, reset,
+                           slope, dtype, static_cast<hipStream_t>(stream));
 }
 
 size_t token_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int64_t C) {

@@ -270,11 +270,11 @@ struct Staged {
   }
 
   // Loads the kInstr pieces of block `blk` (steps past T, and blocks outside
-  // [0, nblk), read as zero).
+  // [lo, nblk), read as zero).
   __device__ static __forceinline__ void load(u32x4 (&st)[kInstr], const raw* __restrict__ p,
                                               size_t row_base, size_t row_tail, unsigned loff,
-                                              int blk, int nblk, int C) {
-    const bool in = blk >= 0 && blk < nblk;
+                                              int blk, int nblk, int C, int lo = 0) {
+    const bool in = blk >= lo && blk < nblk;
     const int t0 = in ? blk * kLifBlock : 0;
     const uint32_t bytes = in ? span_bytes(row_tail, t0, C, kEs) : 0u;
     const rsrc_t r = make_rsrc(p + row_base + size_t(t0) * C, bytes);
@@ -473,7 +473,8 @@ __global__ __launch_bounds__(64) void lif_fwd_residual_kernel(const typename E::
     S::to_lds(xs, st, lane);
     SF::to_lds(rs, sr, lane);
     S::load(st, x, row_base, row_tail, loff, blk + PF, hi, C);
-    SF::load(sr, res, row_base, row_tail, loffr, blk + PF, hi, C);
+    // (warm-up blocks need no residual: those read as zero, moving nothing)
+    SF::load(sr, res, row_base, row_tail, loffr, blk + PF, hi, C, lo);
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), rst,
                                           blk == lo && lane_ok ? unsigned(lane) * 4u : kOutOfRange,
                                           0, 0);
@@ -495,7 +496,7 @@ __global__ __launch_bounds__(64) void lif_fwd_residual_kernel(const typename E::
 #pragma unroll
   for (int q = 0; q < PF; ++q) {
     S::load(st[q], x, row_base, row_tail, loff, first + q, hi, C);
-    SF::load(sr[q], res, row_base, row_tail, loffr, first + q, hi, C);
+    SF::load(sr[q], res, row_base, row_tail, loffr, first + q, hi, C, lo);
   }
   const int nfull = nb - nb % PF;
   for (int base = 0; base < nfull; base += PF) {
@@ -607,12 +608,24 @@ __global__ __launch_bounds__(64) void lif_fwd_fixup_kernel(const typename E::raw
 // G is the type of the incoming gradient: E, or fp32 when the spikes were
 // added into an fp32 residual (lif_fwd_residual_kernel), whose gradient
 // arrives in fp32.
+//
+// Split over time (G.nseg > 1), the mirror of the forward's: the carried
+// gradient gm obeys a linear recurrence, gm <- decay (g ds/dh + gm A_t) with
+// A_t = (1 - s_t) + (reset - h_t) ds/dh, whose factor |decay A_t| is at most
+// about 0.51 for any membrane (the surrogate derivative is at most slope/2
+// and falls off as 1/h^2), so runs from different carries coincide bit for
+// bit after a few dozen steps.  Segment k (output blocks [lo, hi)) starts
+// G.wb blocks after its end from gm = 0, runs those warm-up blocks without
+// writing, publishes the carry it then holds (G.start[k], k < nseg-1), runs
+// its own blocks last to first and publishes the carry it hands to earlier
+// time (G.fin[k-1], k > 0).  lif_bwd_fixup_kernel repairs the boundaries
+// from the last to the first.
 template <typename E, typename G>
 __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::raw* __restrict__ x,
                                                             const typename G::raw* __restrict__ gs,
                                                             const float* __restrict__ ck,
                                                             typename E::raw* __restrict__ gx,
-                                                            int T, int C, LifParams P) {
+                                                            int T, int C, LifParams P, LifSeg Sg) {
   using S = Staged<E>;
   using SG = Staged<G>;
   // Blocks in flight: one fewer when the gradient pieces are wider than x's.
@@ -621,33 +634,43 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
   __shared__ u32x4 gl[SG::kInstr * 64];
   __shared__ u32x4 os[S::kInstr * 64];
   const int n_cg = (C + 63) / 64;
-  const int b = blockIdx.x / n_cg;
-  const int cg = blockIdx.x - b * n_cg;
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const LifSegPos sp_(Sg, n_cg, nblk);
+  const int b = sp_.b, cg = sp_.cg, lo = sp_.lo, hi = sp_.hi, seg = sp_.seg;
+  // Blocks processed: [lo, top], the warm-up ones (after hi - 1) first.
+  const int top = min(nblk, hi + (seg == Sg.nseg - 1 ? 0 : Sg.wb)) - 1;
   const int lane = threadIdx.x;
   const size_t row_base = size_t(b) * T * C + size_t(cg) * 64;
   const size_t row_tail = size_t(T) * C - size_t(cg) * 64;
   const unsigned loff = S::lane_off(lane, C, cg);
   const unsigned loffg = SG::lane_off(lane, C, cg);
-  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const bool lane_ok = cg * 64 + lane < C;
   // Membrane records (lanes past C read as zero and never store).
   const rsrc_t rck = make_rsrc(ck + size_t(b) * nblk * C + size_t(cg) * 64,
                                uint32_t(((size_t(nblk) - 1) * C + 64) * 4));
-  const unsigned ck_off = cg * 64 + lane < C ? unsigned(lane) * 4u : kOutOfRange;
+  const unsigned ck_off = lane_ok ? unsigned(lane) * 4u : kOutOfRange;
   auto rec = [&](int blk) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         rck, ck_off, unsigned(max(blk, 0)) * unsigned(C) * 4u, 0));
   };
+  const size_t bc = size_t(gridDim.x / Sg.nseg / n_cg) * C;
+  const rsrc_t rst = make_rsrc(seg < Sg.nseg - 1 ? Sg.start + size_t(seg) * bc + size_t(b) * C + cg * 64 : nullptr,
+                               seg < Sg.nseg - 1 ? 256u : 0u);
 
   float gm = 0.f;
   // Blocks are visited last to first; the inputs PB blocks ahead (earlier in
-  // time) wait in registers.  Blocks before 0 read as zero.
+  // time) wait in registers.  Blocks before lo read as zero.
   auto block = [&](u32x4 (&sx)[S::kInstr], u32x4 (&sg)[SG::kInstr], float& sm, int blk) {
+    const bool emit = blk < hi;
     S::to_lds(xs, sx, lane);
     SG::to_lds(gl, sg, lane);
     float m = sm;
-    S::load(sx, x, row_base, row_tail, loff, blk - PB, nblk, C);
-    SG::load(sg, gs, row_base, row_tail, loffg, blk - PB, nblk, C);
+    S::load(sx, x, row_base, row_tail, loff, blk - PB, nblk, C, lo);
+    SG::load(sg, gs, row_base, row_tail, loffg, blk - PB, nblk, C, lo);
     sm = rec(blk - PB);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gm), rst,
+                                          blk == hi - 1 && lane_ok ? unsigned(lane) * 4u : kOutOfRange,
+                                          0, 0);
     // Recompute the block's pre-spike membranes h and c = slope (h - theta)
     // (the forward's operations, so the spikes are the forward's; the wave
     // is alone on its SIMD, so the 64 registers cost no occupancy).
@@ -671,20 +694,21 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
       gm = P.decay * gh;
       S::put(os, s, lane, gh);
     }
-    S::store(gx, os, row_base, row_tail, loff, blk, C, lane);
+    S::store(gx, os, row_base, row_tail, loff, blk, C, lane, emit);
   };
 
+  const int nb = top - lo + 1;
   u32x4 sx[PB][S::kInstr], sg[PB][SG::kInstr];
   float sm[PB];
 #pragma unroll
   for (int q = 0; q < PB; ++q) {
-    const int blk = nblk - 1 - q;
-    S::load(sx[q], x, row_base, row_tail, loff, blk, nblk, C);
-    SG::load(sg[q], gs, row_base, row_tail, loffg, blk, nblk, C);
+    const int blk = top - q;
+    S::load(sx[q], x, row_base, row_tail, loff, blk, nblk, C, lo);
+    SG::load(sg[q], gs, row_base, row_tail, loffg, blk, nblk, C, lo);
     sm[q] = rec(blk);
   }
-  const int nfull = nblk - nblk % PB;
-  int blk = nblk - 1;
+  const int nfull = nb - nb % PB;
+  int blk = top;
   for (int i = 0; i < nfull; i += PB) {
 #pragma unroll
     for (int q = 0; q < PB; ++q) block(sx[q], sg[q], sm[q], blk - q);
@@ -692,7 +716,97 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
   }
 #pragma unroll
   for (int q = 0; q < PB - 1; ++q)
-    if (q < nblk - nfull) block(sx[q], sg[q], sm[q], blk - q);
+    if (q < nb - nfull) block(sx[q], sg[q], sm[q], blk - q);
+  if (seg > 0 && lane_ok) Sg.fin[size_t(seg - 1) * bc + size_t(b) * C + cg * 64 + lane] = gm;
+}
+
+// Repair pass of the split backward: one wave per (batch, 64 channels), one
+// lane per channel, boundaries from the last to the first.  Boundary j lies
+// between segments j and j + 1: the exact carry there is what segment j + 1
+// handed on (G.fin[j], exact when segment j + 1 is), the speculated one
+// G.start[j].  A rerun recomputes each block's membranes from its record and
+// runs the exact and the speculated carries side by side, rewriting dL/dx
+// where they differ, until the carries coincide.
+template <typename E, typename G>
+__global__ __launch_bounds__(64) void lif_bwd_fixup_kernel(const typename E::raw* __restrict__ x,
+                                                           const typename G::raw* __restrict__ gs,
+                                                           const float* __restrict__ ck,
+                                                           typename E::raw* __restrict__ gx,
+                                                           int B, int T, int C, LifParams P,
+                                                           LifSeg Sg) {
+  const int n_cg = (C + 63) / 64;
+  const int b = int(blockIdx.x) / n_cg;
+  const int cg = int(blockIdx.x) - b * n_cg;
+  const int c = cg * 64 + int(threadIdx.x);
+  const bool ok = c < C;
+  const int nblk = (T + kLifBlock - 1) / kLifBlock;
+  const size_t bc = size_t(B) * C;
+  const size_t at = size_t(b) * C + size_t(ok ? c : 0);
+  __shared__ float lst[kLifMaxSeg - 1][64], lfi[kLifMaxSeg - 1][64];
+  const int lane = int(threadIdx.x);
+  // Fast path: every speculated carry equals the one handed on (all loads
+  // issued together; past the last boundary a slot re-reads the last one).
+  unsigned differ = 0;
+#pragma unroll
+  for (int k = 0; k < kLifMaxSeg - 1; ++k) {
+    const int kk = min(k, Sg.nseg - 2);
+    const float s0 = Sg.start[size_t(kk) * bc + at];
+    const float f0 = Sg.fin[size_t(kk) * bc + at];
+    differ |= __float_as_uint(s0) ^ __float_as_uint(f0);
+    lst[k][lane] = s0;
+    lfi[k][lane] = f0;
+  }
+  if (!__any(ok && differ != 0)) return;
+  // General path (one wave per workgroup: the LDS values are its own).
+  float carry = lfi[Sg.nseg - 2][lane];  // the last segment starts from the exact zero
+  for (int j = Sg.nseg - 2; j >= 0; --j) {
+    const float spec = lst[j][lane];
+    bool todo = ok && __float_as_uint(carry) != __float_as_uint(spec);
+    float gm = carry, gms = spec;
+    const int lo = j * Sg.bps;
+    const int hi = min(nblk, lo + Sg.bps);
+    for (int blk = hi - 1; blk >= lo && __any(todo); --blk) {
+      const int t0 = blk * kLifBlock;
+      float xv[kLifBlock], gv[kLifBlock];
+#pragma unroll
+      for (int s = 0; s < kLifBlock; ++s) {
+        const int t = t0 + s;
+        const size_t i = (size_t(b) * T + size_t(t)) * C + size_t(c);
+        xv[s] = todo && t < T ? load_scalar<E>(x + i) : 0.f;
+        gv[s] = todo && t < T ? load_scalar<G>(gs + i) : 0.f;
+      }
+      float m = todo ? ck[(size_t(b) * nblk + blk) * C + c] : 0.f;
+      float h[kLifBlock];
+#pragma unroll
+      for (int s = 0; s < kLifBlock; ++s) {
+        const float hh = m * P.decay + xv[s];
+        const float sp = P.slope * (hh - P.threshold) >= 0.f ? 1.f : 0.f;
+        m = hh * (1.f - sp) + P.reset * sp;
+        h[s] = hh;
+      }
+#pragma unroll
+      for (int s = kLifBlock - 1; s >= 0; --s) {
+        const int t = t0 + s;
+        const bool live = todo && t < T;
+        const float cc = P.slope * (h[s] - P.threshold);
+        const float sp = cc >= 0.f ? 1.f : 0.f;
+        const float dsdh = lif_surrogate(cc, P.slope);
+        const float a = (1.f - sp) + (P.reset - h[s]) * dsdh;
+        const float gh = gv[s] * dsdh + gm * a;
+        const float ghs = gv[s] * dsdh + gms * a;
+        if (live && __float_as_uint(gh) != __float_as_uint(ghs))
+          store_scalar<E>(gx + (size_t(b) * T + size_t(t)) * C + size_t(c), gh);
+        if (t < T) {
+          gm = P.decay * gh;
+          gms = P.decay * ghs;
+        }
+        if (live && __float_as_uint(gm) == __float_as_uint(gms)) todo = false;
+      }
+    }
+    // Into boundary j - 1: the carry segment j hands on is exact unless this
+    // lane never coincided with the speculated run.
+    if (j > 0) carry = todo ? gm : lfi[j - 1][lane];
+  }
 }
 
 }  // namespace wkv
@@ -745,52 +859,90 @@ static bool lif_staged_ok(int T, int C) {
   return C % (16 / int(sizeof(typename E::raw))) == 0 && span < (size_t(1) << 31);
 }
 
-// Split forward: time segments for these sizes (1: no split).  Enough
-// segments for ~4096 waves (four per SIMD) while every segment keeps at
-// least 4 blocks (128 steps); WKV_LIF_SEGS overrides (measurement).
-// Measured at B=64 T=1024 C=512 bf16 (forward, warm-up 2 blocks): one pass
-// 56.6 us; 2 segments 40.1, 4 segments 33.5, 8 segments 31.8 us.
-static int lif_fwd_nseg(int64_t B, int64_t T, int64_t C) {
+// Time segments of the split passes for these sizes (1: no split): doubled
+// while the waves stay below `waves` and every segment keeps at least
+// `min_blocks` blocks; `env` overrides (measurement).
+static int lif_nseg(int64_t B, int64_t T, int64_t C, const char* env, int64_t waves,
+                    int64_t min_blocks) {
   const int64_t nblk = (T + wkv::kLifBlock - 1) / wkv::kLifBlock;
   const int64_t rows = B * ((C + 63) / 64);
   if (nblk <= 1 || rows <= 0) return 1;  // empty or one block: nothing to split
   int64_t n = 1;
-  if (const char* e = getenv("WKV_LIF_SEGS")) {
+  if (const char* e = getenv(env)) {
     n = std::min<int64_t>(std::max(atoi(e), 1), wkv::kLifMaxSeg);
   } else {
-    while (n < wkv::kLifMaxSeg && rows * n < 4096 && 2 * n * 4 <= nblk) n *= 2;
+    while (n < wkv::kLifMaxSeg && rows * n < waves && 2 * n * min_blocks <= nblk) n *= 2;
   }
   n = std::min<int64_t>(n, nblk);
   const int64_t bps = (nblk + n - 1) / n;  // >= 1
   return int((nblk + bps - 1) / bps);
 }
 
-// Warm-up blocks of a segment after the first (WKV_LIF_WARMUP overrides).
-// Two (64 steps): with one, enough channels still differ at the boundary
-// that the repair costs more than the second block (B=64 T=1024 C=512, 4
+// The four passes and their rules, from measurements on MI355X (bf16, T =
+// 1024, two-block warm-up; one pass -> split, microseconds):
+//  * forward (4 B per element): ~4096 waves, segments >= 4 blocks.  B=64
+//    C=512: 56.6 -> 40.1 / 33.5 / 31.8 at 2 / 4 / 8 segments.
+//  * backward (6 B): ~2048 waves, segments >= 8 blocks (its blocks cost
+//    more, so the warm-up weighs more on short segments).  B=64 C=512: 90.1
+//    -> 54.4 / 65.2 / 78.0 at 4 / 8 / 16 segments.
+//  * forward with the residual add (10 B): one pass from 384 rows of 64
+//    channels on (the one pass already moves ~5.8 TB/s: B=64 C=512 57.7,
+//    split 65-67), else ~2048 waves (B=16 C=768: 53.1 -> 26.9 at 8).
+//  * backward with the fp32 residual gradient (8 B): ~1024 waves, >= 8
+//    blocks (B=64 C=512: 79.0 -> 56.2 at 2, 61.8 at 4; B=16 C=768: 74.7 ->
+//    34.4 at 4).
+enum class LifPass { kForward, kBackward, kResidualForward, kResidualBackward };
+
+static int lif_nseg(int64_t B, int64_t T, int64_t C, LifPass pass) {
+  switch (pass) {
+    case LifPass::kForward: return lif_nseg(B, T, C, "WKV_LIF_SEGS", 4096, 4);
+    case LifPass::kBackward: return lif_nseg(B, T, C, "WKV_LIF_BWD_SEGS", 2048, 8);
+    case LifPass::kResidualForward:
+      if (B * ((C + 63) / 64) >= 384 && getenv("WKV_LIF_SEGS") == nullptr) return 1;
+      return lif_nseg(B, T, C, "WKV_LIF_SEGS", 2048, 4);
+    case LifPass::kResidualBackward: return lif_nseg(B, T, C, "WKV_LIF_BWD_SEGS", 1024, 8);
+  }
+  return 1;
+}
+
+// Warm-up blocks of a speculated segment (`env` overrides).  Two (64
+// steps): with one, enough channels still differ at the boundary that the
+// forward's repair costs more than the second block (B=64 T=1024 C=512, 4
 // segments: repair 10.8 us after one block, 4.6 us after two or three).
-static int lif_fwd_warmup() {
-  if (const char* e = getenv("WKV_LIF_WARMUP")) return std::min(std::max(atoi(e), 0), 8);
+static int lif_warmup(const char* env) {
+  if (const char* e = getenv(env)) return std::min(std::max(atoi(e), 0), 8);
   return 2;
 }
 
-size_t lif_fwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
-  const int n = lif_fwd_nseg(B, T, C);
+static size_t lif_seg_bytes(int64_t B, int64_t T, int64_t C, LifPass pass) {
+  const int n = lif_nseg(B, T, C, pass);
   if (n <= 1) return 0;
   return size_t(2) * size_t(n - 1) * size_t(B) * size_t(C) * sizeof(float);
 }
 
-// The split's layout for these sizes when `ws` holds enough bytes, else one
-// segment (the sequential pass).
-static wkv::LifSeg lif_fwd_seg(void* ws, size_t ws_bytes, int B, int T, int C) {
+// One workspace query per direction serves both variants (the larger need).
+size_t lif_fwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
+  return std::max(lif_seg_bytes(B, T, C, LifPass::kForward),
+                  lif_seg_bytes(B, T, C, LifPass::kResidualForward));
+}
+
+size_t lif_bwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C) {
+  return std::max(lif_seg_bytes(B, T, C, LifPass::kBackward),
+                  lif_seg_bytes(B, T, C, LifPass::kResidualBackward));
+}
+
+// The split's layout for this pass and these sizes when `ws` holds enough
+// bytes, else one segment (the one-pass kernel).
+static wkv::LifSeg lif_seg(void* ws, size_t ws_bytes, int B, int T, int C, LifPass pass) {
   const int nblk = (T + wkv::kLifBlock - 1) / wkv::kLifBlock;
   wkv::LifSeg G{1, nblk, 0, nullptr, nullptr};
-  const size_t need = lif_fwd_workspace_bytes_impl(B, T, C);
+  const size_t need = lif_seg_bytes(B, T, C, pass);
   if (need == 0 || ws == nullptr || ws_bytes < need) return G;
-  const int n = lif_fwd_nseg(B, T, C);
+  const int n = lif_nseg(B, T, C, pass);
+  const bool backward = pass == LifPass::kBackward || pass == LifPass::kResidualBackward;
   G.nseg = n;
   G.bps = (nblk + n - 1) / n;
-  G.wb = lif_fwd_warmup();
+  G.wb = lif_warmup(backward ? "WKV_LIF_BWD_WARMUP" : "WKV_LIF_WARMUP");
   G.start = static_cast<float*>(ws);
   G.fin = G.start + size_t(n - 1) * size_t(B) * size_t(C);
   return G;
@@ -801,7 +953,7 @@ static int lif_fwd_dispatch(const void* x, void* spk, float* ck, void* ws, size_
                             int T, int C, const wkv::LifParams& P, hipStream_t stream) {
   using raw = typename E::raw;
   if (lif_staged_ok<E>(T, C)) {
-    const wkv::LifSeg G = lif_fwd_seg(ws, ws_bytes, B, T, C);
+    const wkv::LifSeg G = lif_seg(ws, ws_bytes, B, T, C, LifPass::kForward);
     const unsigned rows = unsigned(B) * unsigned((C + 63) / 64);
     const dim3 grid(rows * unsigned(G.nseg));
     const bool last = G.nseg == 1;
@@ -831,16 +983,35 @@ static int lif_fwd_dispatch(const void* x, void* spk, float* ck, void* ws, size_
                             : lif_fwd_launch<E, 1>(x, spk, ck, B, T, C, P, stream);
 }
 
-template <typename E>
-static int lif_bwd_dispatch(const void* x, const void* gs, const float* ck, void* gx, int B,
-                            int T, int C, const wkv::LifParams& P, hipStream_t stream) {
+// Split backward: the segmented kernel, then the repair pass.
+template <typename E, typename G>
+static int lif_bwd_staged(const void* x, const void* gs, const float* ck, void* gx, void* ws,
+                          size_t ws_bytes, int B, int T, int C, const wkv::LifParams& P,
+                          LifPass pass, hipStream_t stream) {
   using raw = typename E::raw;
-  if (lif_staged_ok<E>(T, C)) {
-    launch(wkv::lif_bwd_staged_kernel<E, E>, dim3(unsigned(B) * unsigned((C + 63) / 64)),
-           dim3(64), stream, true, static_cast<const raw*>(x), static_cast<const raw*>(gs), ck,
-           static_cast<raw*>(gx), T, C, P);
-    return check_launch("lif_bwd_staged_kernel");
+  using graw = typename G::raw;
+  const wkv::LifSeg S = lif_seg(ws, ws_bytes, B, T, C, pass);
+  const unsigned rows = unsigned(B) * unsigned((C + 63) / 64);
+  launch(wkv::lif_bwd_staged_kernel<E, G>, dim3(rows * unsigned(S.nseg)), dim3(64), stream,
+         S.nseg == 1, static_cast<const raw*>(x), static_cast<const graw*>(gs), ck,
+         static_cast<raw*>(gx), T, C, P, S);
+  if (const int rc = check_launch("lif_bwd_staged_kernel")) return rc;
+  if (S.nseg > 1) {
+    launch(wkv::lif_bwd_fixup_kernel<E, G>, dim3(rows), dim3(64), stream, true,
+           static_cast<const raw*>(x), static_cast<const graw*>(gs), ck, static_cast<raw*>(gx), B,
+           T, C, P, S);
+    return check_launch("lif_bwd_fixup_kernel");
   }
+  return 0;
+}
+
+template <typename E>
+static int lif_bwd_dispatch(const void* x, const void* gs, const float* ck, void* gx, void* ws,
+                            size_t ws_bytes, int B, int T, int C, const wkv::LifParams& P,
+                            hipStream_t stream) {
+  if (lif_staged_ok<E>(T, C))
+    return lif_bwd_staged<E, E>(x, gs, ck, gx, ws, ws_bytes, B, T, C, P, LifPass::kBackward,
+                                stream);
   return lif_vec(B, C, int(sizeof(typename E::raw))) == 2 ? lif_bwd_launch<E, 2>(x, gs, ck, gx, B, T, C, P, stream)
                             : lif_bwd_launch<E, 1>(x, gs, ck, gx, B, T, C, P, stream);
 }
@@ -854,8 +1025,8 @@ static int lif_residual_fwd(const void* x, const float* res, float* out, float* 
   using raw = typename E::raw;
   const size_t n = size_t(B) * size_t(T) * size_t(C);
   const bool disjoint = out + n <= res || res + n <= out;
-  const wkv::LifSeg G = disjoint ? lif_fwd_seg(ws, ws_bytes, B, T, C)
-                                 : lif_fwd_seg(nullptr, 0, B, T, C);
+  const wkv::LifSeg G =
+      lif_seg(disjoint ? ws : nullptr, ws_bytes, B, T, C, LifPass::kResidualForward);
   const unsigned rows = unsigned(B) * unsigned((C + 63) / 64);
   launch(wkv::lif_fwd_residual_kernel<E>, dim3(rows * unsigned(G.nseg)), dim3(64), stream,
          G.nseg == 1, static_cast<const raw*>(x), res, out, ck, T, C, P, G);
@@ -869,13 +1040,11 @@ static int lif_residual_fwd(const void* x, const float* res, float* out, float* 
 }
 
 template <typename E>
-static int lif_residual_bwd(const void* x, const float* g, const float* ck, void* gx, int B,
-                            int T, int C, const wkv::LifParams& P, hipStream_t stream) {
-  using raw = typename E::raw;
-  launch(wkv::lif_bwd_staged_kernel<E, wkv::F32>, dim3(unsigned(B) * unsigned((C + 63) / 64)),
-         dim3(64), stream, true, static_cast<const raw*>(x), g, ck, static_cast<raw*>(gx), T, C,
-         P);
-  return check_launch("lif_bwd_staged_kernel");
+static int lif_residual_bwd(const void* x, const float* g, const float* ck, void* gx, void* ws,
+                            size_t ws_bytes, int B, int T, int C, const wkv::LifParams& P,
+                            hipStream_t stream) {
+  return lif_bwd_staged<E, wkv::F32>(x, g, ck, gx, ws, ws_bytes, B, T, C, P,
+                                     LifPass::kResidualBackward, stream);
 }
 
 bool lif_residual_ok(int64_t T, int64_t C, int dtype) {
@@ -897,14 +1066,15 @@ int lif_residual_forward_impl(const void* x, const float* res, float* out, float
   }
 }
 
-int lif_residual_backward_impl(const void* x, const float* g, const float* ck, void* gx, int B,
-                               int T, int C, float decay, float threshold, float reset,
-                               float slope, int dtype, hipStream_t stream) {
+int lif_residual_backward_impl(const void* x, const float* g, const float* ck, void* gx,
+                               void* ws, size_t ws_bytes, int B, int T, int C, float decay,
+                               float threshold, float reset, float slope, int dtype,
+                               hipStream_t stream) {
   const wkv::LifParams P{decay, threshold, reset, slope};
   switch (dtype) {
-    case 0: return lif_residual_bwd<wkv::F32>(x, g, ck, gx, B, T, C, P, stream);
-    case 1: return lif_residual_bwd<wkv::BF16>(x, g, ck, gx, B, T, C, P, stream);
-    case 2: return lif_residual_bwd<wkv::F16>(x, g, ck, gx, B, T, C, P, stream);
+    case 0: return lif_residual_bwd<wkv::F32>(x, g, ck, gx, ws, ws_bytes, B, T, C, P, stream);
+    case 1: return lif_residual_bwd<wkv::BF16>(x, g, ck, gx, ws, ws_bytes, B, T, C, P, stream);
+    case 2: return lif_residual_bwd<wkv::F16>(x, g, ck, gx, ws, ws_bytes, B, T, C, P, stream);
     default: return fail(1, "lif_residual_backward: unknown dtype");
   }
 }
@@ -921,14 +1091,14 @@ int lif_forward_impl(const void* x, void* spk, float* ck, void* ws, size_t ws_by
   }
 }
 
-int lif_backward_impl(const void* x, const void* gs, const float* ck, void* gx, int B, int T,
-                      int C, float decay, float threshold, float reset, float slope, int dtype,
-                      hipStream_t stream) {
+int lif_backward_impl(const void* x, const void* gs, const float* ck, void* gx, void* ws,
+                      size_t ws_bytes, int B, int T, int C, float decay, float threshold,
+                      float reset, float slope, int dtype, hipStream_t stream) {
   const wkv::LifParams P{decay, threshold, reset, slope};
   switch (dtype) {
-    case 0: return lif_bwd_dispatch<wkv::F32>(x, gs, ck, gx, B, T, C, P, stream);
-    case 1: return lif_bwd_dispatch<wkv::BF16>(x, gs, ck, gx, B, T, C, P, stream);
-    case 2: return lif_bwd_dispatch<wkv::F16>(x, gs, ck, gx, B, T, C, P, stream);
+    case 0: return lif_bwd_dispatch<wkv::F32>(x, gs, ck, gx, ws, ws_bytes, B, T, C, P, stream);
+    case 1: return lif_bwd_dispatch<wkv::BF16>(x, gs, ck, gx, ws, ws_bytes, B, T, C, P, stream);
+    case 2: return lif_bwd_dispatch<wkv::F16>(x, gs, ck, gx, ws, ws_bytes, B, T, C, P, stream);
     default: return fail(1, "lif_backward: unknown dtype");
   }
 }

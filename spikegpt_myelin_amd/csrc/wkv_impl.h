@@ -91,13 +91,17 @@ int lif_forward_impl(const void* x, void* spk, float* ck, void* ws, size_t ws_by
                      int C, float decay, float threshold, float reset, float slope, int dtype,
                      hipStream_t stream);
 size_t lif_fwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C);
-int lif_backward_impl(const void*, const void*, const float*, void*, int, int, int, float, float,
-                      float, float, int, hipStream_t);
+int lif_backward_impl(const void* x, const void* gs, const float* ck, void* gx, void* ws,
+                      size_t ws_bytes, int B, int T, int C, float decay, float threshold,
+                      float reset, float slope, int dtype, hipStream_t stream);
+size_t lif_bwd_workspace_bytes_impl(int64_t B, int64_t T, int64_t C);
 int lif_residual_forward_impl(const void* x, const float* res, float* out, float* ck, void* ws,
                               size_t ws_bytes, int B, int T, int C, float decay, float threshold,
                               float reset, float slope, int dtype, hipStream_t stream);
-int lif_residual_backward_impl(const void*, const float*, const float*, void*, int, int, int,
-                               float, float, float, float, int, hipStream_t);
+int lif_residual_backward_impl(const void* x, const float* g, const float* ck, void* gx,
+                               void* ws, size_t ws_bytes, int B, int T, int C, float decay,
+                               float threshold, float reset, float slope, int dtype,
+                               hipStream_t stream);
 bool lif_residual_ok(int64_t, int64_t, int);
 int relu_square_forward_impl(const void*, void*, int64_t, int, hipStream_t);
 int relu_square_backward_impl(const void*, const void*, void*, int64_t, int, hipStream_t);

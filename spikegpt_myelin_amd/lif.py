@@ -48,6 +48,15 @@ def _forward_workspace(lib, b: int, t: int, c: int, device) -> tuple[Tensor | No
     return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
 
 
+def _backward_workspace(lib, b: int, t: int, c: int, device) -> tuple[Tensor | None, int]:
+    """Workspace of the backward's split over time (boundary carries), or
+    (None, 0) for sizes that run as one pass."""
+    nbytes = int(lib.lif_backward_workspace_bytes(b, t, c))
+    if nbytes == 0:
+        return None, 0
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
 def _native(x: Tensor) -> Tensor:
     return _lib.aligned(x if x.dtype in _NATIVE else x.float())
 
@@ -95,9 +104,10 @@ def _lif_backward(
     ck = _lib.aligned(checkpoint)
     gx = torch.empty_like(xs)
     lib = _lib.load()
+    ws, nbytes = _backward_workspace(lib, b, t, c, x.device)
     rc = _lib.timed("lif_backward", x.device, lambda: lib.lif_backward(
-        xs.data_ptr(), gs.data_ptr(), ck.data_ptr(), gx.data_ptr(), b, t, c, decay, threshold,
-        reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs),
+        xs.data_ptr(), gs.data_ptr(), ck.data_ptr(), gx.data_ptr(), _lib.ptr(ws), nbytes, b, t, c,
+        decay, threshold, reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs),
     ))
     _lib.check(rc, "lif_backward")
     return gx
@@ -194,9 +204,10 @@ def _lif_res_backward(grad_out: Tensor, x: Tensor, checkpoint: Tensor, decay: fl
     g = _lib.aligned(grad_out.float())
     gx = torch.empty_like(xs)
     lib = _lib.load()
+    ws, nbytes = _backward_workspace(lib, b, t, c, x.device)
     rc = _lib.timed("lif_residual_backward", x.device, lambda: lib.lif_residual_backward(
-        xs.data_ptr(), g.data_ptr(), checkpoint.data_ptr(), gx.data_ptr(), b, t, c, decay,
-        threshold, reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs)))
+        xs.data_ptr(), g.data_ptr(), checkpoint.data_ptr(), gx.data_ptr(), _lib.ptr(ws), nbytes,
+        b, t, c, decay, threshold, reset, slope, _lib.dtype_code(xs.dtype), _lib.stream_of(xs)))
     _lib.check(rc, "lif_residual_backward")
     return gx
 

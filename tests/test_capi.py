@@ -93,6 +93,16 @@ def test_lif_forward_workspace_sizes(lib, monkeypatch):
     assert lib.lif_forward_workspace_bytes(2, 0, 70) == 0
     monkeypatch.setenv("WKV_LIF_SEGS", "1")
     assert lib.lif_forward_workspace_bytes(64, 1024, 512) == 0
+    monkeypatch.delenv("WKV_LIF_SEGS")
+    # the residual forward splits only below 384 rows (eight segments at
+    # B=16, C=768, as the plain one), so the query's maximum is the plain one
+    assert lib.lif_forward_workspace_bytes(16, 1024, 768) == 2 * 7 * 16 * 768 * 4
+    # the backward: segments of at least eight blocks, ~2048 waves (plain) or
+    # ~1024 (residual); the query covers the larger
+    assert lib.lif_backward_workspace_bytes(64, 1024, 512) == 2 * 3 * 64 * 512 * 4
+    assert lib.lif_backward_workspace_bytes(16, 1024, 768) == 2 * 3 * 16 * 768 * 4
+    assert lib.lif_backward_workspace_bytes(2, 200, 64) == 0  # 7 blocks
+    assert lib.lif_backward_workspace_bytes(2, 0, 64) == 0
 
 
 def test_step_row_args_layout_matches_header(tmp_path):

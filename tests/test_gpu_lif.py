@@ -265,3 +265,59 @@ def test_default_split_at_the_benchmark_shape():
     from spikegpt_myelin_amd import _lib
 
     assert int(_lib.load().lif_forward_workspace_bytes(64, 1024, 512)) == 2 * 7 * 64 * 512 * 4
+
+
+@pytest.mark.parametrize("kind", list(LIF_PARAMS))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 100, 70), (3, 257, 256), (1, 1000, 128), (2, 300, 136)])
+def test_split_backward_equals_one_pass(kind, dtype, shape, monkeypatch):
+    # The backward's split mirrors the forward's (segments run last to
+    # first from a zero gradient carry after a warm-up, then a repair pass):
+    # dL/dx bit-identical to the one-pass kernel, and to the oracle's bar.
+    ops = _ops()
+    b, t, c = shape
+    x, p = _lif_case(b, t, c, dtype, kind, seed=t + c + 1)
+    gs = torch.randn(b, t, c, generator=torch.Generator().manual_seed(c)).to(dtype)
+    decay = 1.0 - 1.0 / p["tau"]
+    args = (decay, p["threshold"], p["reset"], p["slope"])
+    print(f"lif backward split {kind} {dtype} {shape}", flush=True)
+    monkeypatch.setenv("WKV_LIF_SEGS", "1")
+    _, ck = ops.lif_sequence_forward(x.to(DEV), *args)
+    monkeypatch.setenv("WKV_LIF_BWD_SEGS", "1")
+    g1 = ops.lif_sequence_backward(gs.to(DEV), x.to(DEV), ck, *args).cpu()
+    ref = L.lif_reverse(x.float(), gs.float(), p["tau"], p["threshold"], p["reset"], p["slope"],
+                        forward_dtype=torch.float32)
+    _check_grad(g1, ref, dtype, f"one pass {kind}")
+    for segs in ("2", "3", "5", "16"):
+        for warm in ("0", "1", "2"):
+            monkeypatch.setenv("WKV_LIF_BWD_SEGS", segs)
+            monkeypatch.setenv("WKV_LIF_BWD_WARMUP", warm)
+            g2 = ops.lif_sequence_backward(gs.to(DEV), x.to(DEV), ck, *args).cpu()
+            assert torch.equal(g2.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                               g1.view(torch.int16 if dtype != torch.float32 else torch.int32)), \
+                f"grad_x: {segs} segments, warm-up {warm}"
+
+
+@pytest.mark.parametrize("kind", list(LIF_PARAMS))
+def test_split_residual_backward_equals_one_pass(kind, monkeypatch):
+    ops = _ops()
+    b, t, c = 2, 1000, 136
+    x, p = _lif_case(b, t, c, torch.bfloat16, kind, seed=7)
+    g = torch.randn(b, t, c, generator=torch.Generator().manual_seed(8))
+    residual = torch.zeros(b, t, c)
+    args = (1.0 - 1.0 / p["tau"], p["threshold"], p["reset"], p["slope"])
+    print(f"lif residual backward split {kind}", flush=True)
+    _, ck = ops.lif_residual_forward(x.to(DEV), residual.to(DEV), *args)
+    monkeypatch.setenv("WKV_LIF_BWD_SEGS", "1")
+    g1 = ops.lif_residual_backward(g.to(DEV), x.to(DEV), ck, *args).cpu()
+    for segs in ("2", "5", "16"):
+        monkeypatch.setenv("WKV_LIF_BWD_SEGS", segs)
+        g2 = ops.lif_residual_backward(g.to(DEV), x.to(DEV), ck, *args).cpu()
+        assert torch.equal(g2.view(torch.int16), g1.view(torch.int16)), f"{segs} segments"
+
+
+def test_default_backward_split_at_the_benchmark_shape():
+    from spikegpt_myelin_amd import _lib
+
+    # four segments of eight blocks
+    assert int(_lib.load().lif_backward_workspace_bytes(64, 1024, 512)) == 2 * 3 * 64 * 512 * 4
