@@ -197,11 +197,14 @@ struct Lane {
   }
 };
 
-// One forward step on the lane's 4x4 block: returns sa (S_{t-1} a) per row
-// and advances S.  The same code runs in the forward kernel and in the
-// backward's recomputation, so both produce the same state bits.
-__device__ __forceinline__ void fwd_step(float (&S)[4][4], const float* stage, int s,
-                                         const Lane& L, float (&sa)[4]) {
+// One forward step on the lane's 4x4 block: sa (S_{t-1} a) per row and the
+// next state So from Si (separate arrays, so that an unrolled sequence of
+// steps keeps every state in its own registers without copies).  The row
+// layout of the forward kernel does the same operations in the same order,
+// so both produce the same state bits.
+__device__ __forceinline__ void fwd_step(const float (&Si)[4][4], float (&So)[4][4],
+                                         const float* stage, int s, const Lane& L,
+                                         float (&sa)[4]) {
   const float4 a4 = lds4(stage, QA, s, L.j0);
   const float4 w4 = lds4(stage, QW, s, L.j0);
   const float4 b4 = lds4(stage, QB, s, L.j0);
@@ -214,9 +217,9 @@ __device__ __forceinline__ void fwd_step(float (&S)[4][4], const float* stage, i
   const float v[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float x = S[r][0] * a[0];
+    float x = Si[r][0] * a[0];
 #pragma unroll
-    for (int c = 1; c < 4; ++c) x = fmaf(S[r][c], a[c], x);
+    for (int c = 1; c < 4; ++c) x = fmaf(Si[r][c], a[c], x);
     sa[r] = x;
   }
 #pragma unroll
@@ -224,7 +227,7 @@ __device__ __forceinline__ void fwd_step(float (&S)[4][4], const float* stage, i
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) S[r][c] = fmaf(S[r][c], w[c], fmaf(sa[r], b[c], v[r] * k[c]));
+    for (int c = 0; c < 4; ++c) So[r][c] = fmaf(Si[r][c], w[c], fmaf(sa[r], b[c], v[r] * k[c]));
 }
 
 __device__ __forceinline__ size_t state_off(int bh, int i, int j) {
@@ -532,32 +535,22 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
   const bool dv_lane = L.cg < 4;
   float* const dv_base = dv_lane ? &sm.dvb[rbuf][0][L.i0 + L.cg] : &sm.dv_sink[threadIdx.x];
   const int dv_stride = dv_lane ? kN + kRedPad : 0;
-  float S[4][4];
+  // Recompute the sub-chunk: Sp[s] = S_{t-1} of step s, Sp[s+1] = S_t; sa_t
+  // kept.
+  float Sp[KS + 1][4][4], sas[KS][4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) S[r][c] = S0[r][c];
-  // Recompute the sub-chunk keeping S_{t-1} and sa_t.
-  float Sp[KS][4][4], sas[KS][4];
+    for (int c = 0; c < 4; ++c) Sp[0][r][c] = S0[r][c];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    if (FULL || s < cnt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) Sp[s][r][c] = S[r][c];
-      fwd_step(S, sg, sl + s, L, sas[s]);
-    }
+    if (FULL || s < cnt) fwd_step(Sp[s], Sp[s + 1], sg, sl + s, L, sas[s]);
   }
-  // Reverse; St holds the post-update state of step s (S_t).
-  float St[4][4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) St[r][c] = S[r][c];
+  // Reverse; the post-update state of step s (S_t) is Sp[s + 1].
 #pragma unroll
   for (int s = KS - 1; s >= 0; --s) {
     if (FULL || s < cnt) {
+      const float (&St)[4][4] = Sp[s + 1];
       const int ss = sl + s;
       const float4 r4 = lds4(sg, QR, ss, L.j0);
       const float4 w4 = lds4(sg, QW, ss, L.j0);
@@ -629,10 +622,6 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
         const float d23 = (L.cg & 1) ? dvr[3] : dvr[2];
         dv_base[s * dv_stride] = (L.cg & 2) ? d23 : d01;
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) St[r][c] = Sp[s][r][c];
     }
   }
 }
