@@ -3,10 +3,11 @@
 Bars: forward of ``relu_square`` bit-exact against ``relu(x).square()`` in
 fp32 rounded once (the autocast values); ``sigmoid_gate`` forward within one
 unit in the last place of the element type of torch's own two-kernel result
-(the kernels evaluate the same fp32 expression; the exponential's last bit
-may differ) and equal on at least 99.9 % of elements; backward against
-float64 autograd with ``rtol=1e-5`` (fp32) or ``rtol=2e-2, atol=1e-2``
-(16-bit).
+and equal on at least 99.9 % of elements (the kernels evaluate torch's fp32
+expression; the exponential's last bit may differ), also over every 16-bit
+input;
+backward against float64 autograd with ``rtol=1e-5`` (fp32) or
+``rtol=2e-2, atol=1e-2`` (16-bit).
 """
 
 from __future__ import annotations
@@ -65,6 +66,25 @@ def test_sigmoid_gate(dt, shape):
     grr, gxr = torch.autograd.grad(torch.sigmoid(rr) * xr, [rr, xr], gy.double())
     assert torch.allclose(gr.double().cpu(), grr, **_tol(dt))
     assert torch.allclose(gx.double().cpu(), gxr, **_tol(dt))
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_sigmoid_gate_every_16bit_input(dt):
+    # Every finite value of the type as r, x = 1: the gate is then the
+    # rounded sigmoid itself.  Against torch's sigmoid of the same inputs:
+    # within one unit in the last place everywhere, equal on >= 99.9 %.
+    bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16)
+    r = bits.view(dt)
+    r = r[torch.isfinite(r.float())].to(DEV)
+    y = _ops().sigmoid_gate(r, torch.ones_like(r))
+    ref = torch.sigmoid(r)
+    diff = (y.float() - ref.float()).abs()
+    ulp = torch.finfo(dt).eps * ref.float().abs().clamp_min(torch.finfo(dt).tiny)
+    equal = float((y == ref).float().mean())
+    print(f"{dt}: {r.numel()} inputs, equal {equal:.6f}, max diff / ulp "
+          f"{float((diff / ulp).max()):.3f}")
+    assert bool((diff <= ulp).all()), float((diff / ulp).max())
+    assert equal >= 0.999
 
 
 def test_module_functions_route_and_differentiate():
