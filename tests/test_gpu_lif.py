@@ -321,3 +321,30 @@ def test_default_backward_split_at_the_benchmark_shape():
 
     # four segments of eight blocks
     assert int(_lib.load().lif_backward_workspace_bytes(64, 1024, 512)) == 2 * 3 * 64 * 512 * 4
+
+
+def test_216m_activation_shape_with_the_default_split():
+    # B=16, T=1024, C=768 bf16 (the 216M class): the sizes alone pick the
+    # split (forward 8 segments, backward 4; the residual forward also 8 at
+    # these 192 rows).  Spikes exact, gradients to the 16-bit bar, and the
+    # residual form equal to residual + spikes.
+    from spikegpt_myelin_amd import _lib
+    from spikegpt_myelin_amd.lif import lif_residual
+
+    b, t, c = 16, 1024, 768
+    lib = _lib.load()
+    assert int(lib.lif_forward_workspace_bytes(b, t, c)) == 2 * 7 * b * c * 4
+    assert int(lib.lif_backward_workspace_bytes(b, t, c)) == 2 * 3 * b * c * 4
+    x, gs = _inputs(b, t, c, torch.bfloat16, seed=21, scale=1.0)
+    spikes, gx = _run(x, gs)
+    assert torch.equal(spikes, L.lif_loop(x.float()).to(torch.bfloat16))
+    _check_grad(gx, L.lif_reverse(x.float(), gs.float(), forward_dtype=torch.float32),
+                torch.bfloat16, "grad_x 216M shape")
+    residual = torch.randn(b, t, c, generator=torch.Generator().manual_seed(22))
+    gout = torch.randn(b, t, c, generator=torch.Generator().manual_seed(23))
+    xd = x.to(DEV).requires_grad_(True)
+    out = lif_residual(residual.to(DEV), xd)
+    assert torch.equal(out.detach().cpu(), residual + L.lif_loop(x.float()))
+    (gxr,) = torch.autograd.grad(out, xd, gout.to(DEV))
+    _check_grad(gxr, L.lif_reverse(x.float(), gout, forward_dtype=torch.float32),
+                torch.bfloat16, "residual grad_x 216M shape")
