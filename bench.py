@@ -735,6 +735,8 @@ def bench_timemix(args) -> dict:
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "token_shift_mix_fwd_bwd", "B": B, "T": T, "C": C, "n": n},
         "hbm_gbps_algorithmic": (fwd_bytes + bwd_bytes) / step_s / 1e9,
+        "fwd_launch_us": fwd_t * 1e6, "bwd_launch_us": bwd_t * 1e6,
+        "fwd_gbps_algorithmic": fwd_bytes / fwd_t / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "kernel": "shift_mix_bwd_kernel + column_sum_kernel",

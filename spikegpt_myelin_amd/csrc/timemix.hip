@@ -18,16 +18,19 @@
 // out), and the backward reads x and the N gradients once and writes gx.
 //
 // Decomposition: a wave owns 64*VEC consecutive channels of one batch row
-// over a chunk of kTmChunk steps (it re-reads the one row before its chunk);
-// four waves per workgroup take consecutive chunks.  The mixing-vector
+// over a chunk of `chunk` steps (it re-reads the one row before its chunk);
+// four waves per workgroup take consecutive chunks.  The host picks the
+// chunk length (a power of two, 8 to 64 steps) so that the grid holds
+// enough waves to keep loads in flight on every SIMD.  The mixing-vector
 // gradient is reduced per wave in registers, written as per-(batch, chunk)
 // partial sums and summed over them in fixed order by a second kernel
 // (deterministic).
+#include <type_traits>
+
 #include "wkv_common.h"
 
 namespace wkv {
 
-constexpr int kTmChunk = 64;  // steps per wave
 constexpr int kTmMaxN = 3;
 
 template <typename RAW>
@@ -61,11 +64,11 @@ template <typename EI, typename EO, int N, int VEC>
 __global__ __launch_bounds__(256) void shift_mix_fwd_kernel(const typename EI::raw* __restrict__ x,
                                                             const float* __restrict__ mix,
                                                             Ptrs3<typename EO::raw> out, int B,
-                                                            int T, int C) {
+                                                            int T, int C, int chunk) {
   constexpr int U = 8;  // steps loaded ahead
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
-  const int n_tc = (T + kTmChunk - 1) / kTmChunk;
-  const int wave = threadIdx.x >> 6;
+  const int n_tc = (T + chunk - 1) / chunk;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + wave;  // (b, cg, tc), tc fastest
   const int tc = item % n_tc;
@@ -75,8 +78,8 @@ __global__ __launch_bounds__(256) void shift_mix_fwd_kernel(const typename EI::r
   if (b >= B) return;  // the last workgroup may hold fewer than four items
   const int c0 = cg * 64 * VEC + lane * VEC;
   if (c0 >= C) return;
-  const int t0 = tc * kTmChunk;
-  const int t1 = min(T, t0 + kTmChunk);
+  const int t0 = tc * chunk;
+  const int t1 = min(T, t0 + chunk);
   const size_t base = size_t(b) * T * C + c0;
 
   float mu[N][VEC], om[N][VEC];
@@ -128,13 +131,11 @@ __global__ __launch_bounds__(256) void shift_mix_bwd_kernel(const typename EI::r
                                                             Ptrs3<const typename EG::raw> g,
                                                             typename EI::raw* __restrict__ gx,
                                                             float* __restrict__ partial, int B,
-                                                            int T, int C) {
-  // Steps loaded ahead: fewer for several gradients at four channels per
-  // lane, where eight would leave one or two waves per SIMD.
-  constexpr int U = (N >= 2 && VEC == 4) ? 4 : 8;
+                                                            int T, int C, int chunk) {
+  constexpr int U = 8;  // steps per block (measured: 2 and 4 no faster)
   const int n_cg = (C + 64 * VEC - 1) / (64 * VEC);
-  const int n_tc = (T + kTmChunk - 1) / kTmChunk;
-  const int wave = threadIdx.x >> 6;
+  const int n_tc = (T + chunk - 1) / chunk;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);  // wave-uniform
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * 4 + wave;
   const int tc = item % n_tc;
@@ -144,8 +145,8 @@ __global__ __launch_bounds__(256) void shift_mix_bwd_kernel(const typename EI::r
   if (b >= B) return;
   const int c0 = cg * 64 * VEC + lane * VEC;
   if (c0 >= C) return;
-  const int t0 = tc * kTmChunk;
-  const int t1 = min(T, t0 + kTmChunk);
+  const int t0 = tc * chunk;
+  const int t1 = min(T, t0 + chunk);
   const size_t base = size_t(b) * T * C + c0;
 
   float mu[N][VEC], om[N][VEC], acc[N][VEC];
@@ -169,45 +170,48 @@ __global__ __launch_bounds__(256) void shift_mix_bwd_kernel(const typename EI::r
   float gn[N][VEC];
 #pragma unroll
   for (int j = 0; j < N; ++j) tm_load<EG, VEC>(gn[j], g.p[j] + base + size_t(t0) * C);
-  for (int t = t0; t < t1; t += U) {
-    float xc[U][VEC], gg[U][N][VEC];
+  // A block of K steps (K = U, or 1 for the steps after the last whole
+  // block): the loads of all K steps are issued first (16-bit gradients held
+  // packed and converted where used), then the steps are computed and stored
+  // in order.  No load sits under a branch (a load under a branch that joins
+  // a constant gets a wait of its own): the gradient row after step T-1 is
+  // read from row T-1 and replaced by zero.
+  auto block = [&](int t, auto k_tag) {
+    constexpr int K = decltype(k_tag)::value;
+    Pack<EI, VEC> xs[K];
+    Pack<EG, VEC> gs[K][N];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      if (t + i < t1) {
-        tm_load<EI, VEC>(xc[i], x + base + size_t(t + i) * C);
+    for (int i = 0; i < K; ++i) {
+      const int tg = min(t + i + 1, T - 1);
+      xs[i].load(x + base + size_t(t + i) * C);
 #pragma unroll
-        for (int j = 0; j < N; ++j) {
-          if (t + i + 1 < T) {
-            tm_load<EG, VEC>(gg[i][j], g.p[j] + base + size_t(t + i + 1) * C);
-          } else {
-#pragma unroll
-            for (int c = 0; c < VEC; ++c) gg[i][j][c] = 0.f;
-          }
-        }
-      }
+      for (int j = 0; j < N; ++j) gs[i][j].load(g.p[j] + base + size_t(tg) * C);
     }
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      if (t + i < t1) {
-        float o[VEC];
+    for (int i = 0; i < K; ++i) {
+      const bool past_end = t + i + 1 >= T;
+      float o[VEC];
 #pragma unroll
-        for (int c = 0; c < VEC; ++c) o[c] = 0.f;
+      for (int c = 0; c < VEC; ++c) o[c] = 0.f;
 #pragma unroll
-        for (int j = 0; j < N; ++j) {
+      for (int j = 0; j < N; ++j) {
 #pragma unroll
-          for (int c = 0; c < VEC; ++c) {
-            const float gc = gn[j][c];
-            o[c] = fmaf(gg[i][j][c], om[j][c], fmaf(gc, mu[j][c], o[c]));
-            acc[j][c] = fmaf(gc, xc[i][c] - prev[c], acc[j][c]);
-            gn[j][c] = gg[i][j][c];
-          }
+        for (int c = 0; c < VEC; ++c) {
+          const float gc = gn[j][c];
+          const float gnext = past_end ? 0.f : gs[i][j].get(c);
+          o[c] = fmaf(gnext, om[j][c], fmaf(gc, mu[j][c], o[c]));
+          acc[j][c] = fmaf(gc, xs[i].get(c) - prev[c], acc[j][c]);
+          gn[j][c] = gnext;
         }
-        tm_store<EI, VEC>(gx + base + size_t(t + i) * C, o);
-#pragma unroll
-        for (int c = 0; c < VEC; ++c) prev[c] = xc[i][c];
       }
+      tm_store<EI, VEC>(gx + base + size_t(t + i) * C, o);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) prev[c] = xs[i].get(c);
     }
-  }
+  };
+  int t = t0;
+  for (; t + U <= t1; t += U) block(t, std::integral_constant<int, U>{});
+  for (; t < t1; ++t) block(t, std::integral_constant<int, 1>{});
   const size_t prow = size_t(b) * n_tc + tc;
 #pragma unroll
   for (int j = 0; j < N; ++j) {
@@ -224,15 +228,35 @@ namespace wkv_host {
 
 static int tm_vec(int C) { return C % 4 == 0 ? 4 : 1; }
 
+// Steps per wave: the longest power-of-two chunk (64 down to 8) that still
+// gives kTmMinWaves waves, two per SIMD.  Shorter chunks (more waves) were
+// measured no faster at B=64, T=1024, C=512 and cost more partial sums.
+// WKV_TM_CHUNK=8|16|32|64 in the environment overrides it (measurement).
+constexpr int64_t kTmMinWaves = 2048;
+
+static int tm_chunk(int64_t B, int64_t T, int64_t C) {
+  static const int env = [] {
+    const char* s = getenv("WKV_TM_CHUNK");
+    const int v = s ? atoi(s) : 0;
+    return (v == 8 || v == 16 || v == 32 || v == 64) ? v : 0;
+  }();
+  if (env) return env;
+  const int64_t n_cg = (C + 64 * tm_vec(int(C)) - 1) / (64 * tm_vec(int(C)));
+  int chunk = 64;
+  while (chunk > 8 && B * n_cg * ((T + chunk - 1) / chunk) < kTmMinWaves) chunk /= 2;
+  return chunk;
+}
+
 // Four waves per workgroup; wave items (b, cg, tc) enumerate tc fastest.
-static dim3 tm_grid(int B, int T, int C, int vec) {
+static dim3 tm_grid(int B, int T, int C, int vec, int chunk) {
   const int64_t n_cg = (C + 64 * vec - 1) / (64 * vec);
-  const int64_t n_tc = (T + wkv::kTmChunk - 1) / wkv::kTmChunk;
+  const int64_t n_tc = (T + chunk - 1) / chunk;
   return dim3(unsigned((int64_t(B) * n_cg * n_tc + 3) / 4));
 }
 
 size_t shift_mix_partial_floats(int64_t N, int64_t B, int64_t T, int64_t C) {
-  return size_t(N) * size_t(B) * size_t((T + wkv::kTmChunk - 1) / wkv::kTmChunk) * size_t(C);
+  const int64_t chunk = tm_chunk(B, T, C);
+  return size_t(N) * size_t(B) * size_t((T + chunk - 1) / chunk) * size_t(C);
 }
 
 template <typename EI, typename EO, int N, int VEC>
@@ -240,8 +264,9 @@ static int fwd_launch(const void* x, const float* mix, void* const* out, int B, 
                       hipStream_t stream) {
   wkv::Ptrs3<typename EO::raw> o{};
   for (int j = 0; j < N; ++j) o.p[j] = static_cast<typename EO::raw*>(out[j]);
-  launch(wkv::shift_mix_fwd_kernel<EI, EO, N, VEC>, tm_grid(B, T, C, VEC), dim3(256), stream, true,
-         static_cast<const typename EI::raw*>(x), mix, o, B, T, C);
+  const int chunk = tm_chunk(B, T, C);
+  launch(wkv::shift_mix_fwd_kernel<EI, EO, N, VEC>, tm_grid(B, T, C, VEC, chunk), dim3(256), stream,
+         true, static_cast<const typename EI::raw*>(x), mix, o, B, T, C, chunk);
   return check_launch("shift_mix_fwd_kernel");
 }
 
@@ -279,12 +304,13 @@ static int bwd_launch(const void* x, const float* mix, const void* const* g, voi
                       float* partial, float* gmix, int B, int T, int C, hipStream_t stream) {
   wkv::Ptrs3<const typename EG::raw> gp{};
   for (int j = 0; j < N; ++j) gp.p[j] = static_cast<const typename EG::raw*>(g[j]);
-  launch(wkv::shift_mix_bwd_kernel<EI, EG, N, VEC>, tm_grid(B, T, C, VEC), dim3(256), stream,
-         false, static_cast<const typename EI::raw*>(x), mix, gp,
-         static_cast<typename EI::raw*>(gx), partial, B, T, C);
+  const int chunk = tm_chunk(B, T, C);
+  launch(wkv::shift_mix_bwd_kernel<EI, EG, N, VEC>, tm_grid(B, T, C, VEC, chunk), dim3(256),
+         stream, false, static_cast<const typename EI::raw*>(x), mix, gp,
+         static_cast<typename EI::raw*>(gx), partial, B, T, C, chunk);
   int rc = check_launch("shift_mix_bwd_kernel");
   if (rc) return rc;
-  const int P = B * ((T + wkv::kTmChunk - 1) / wkv::kTmChunk);
+  const int P = B * ((T + chunk - 1) / chunk);
   launch(wkv::column_sum_kernel<16>, dim3(unsigned((C + 63) / 64), unsigned(N)), dim3(1024), stream,
          true, static_cast<const float*>(partial), gmix, P, C);
   return check_launch("column_sum_kernel");

@@ -407,8 +407,9 @@ __device__ __forceinline__ void store_buf(const OutPack<E, VEC>& o, rsrc_t r, un
 
 // out[r][c] = sum_p partial[r][p][c] over P partial rows in a fixed order:
 // G threads per channel (G x 64 = the workgroup) each sum every G-th row,
-// then a fixed LDS tree.  A template so that each translation unit that
-// launches it holds its own copy.
+// then a fixed LDS tree (the loop is unrolled so that a thread's loads are
+// in flight together; the sums keep their order).  A template so that each
+// translation unit that launches it holds its own copy.
 template <int G>
 __global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restrict__ partial,
                                                           float* __restrict__ out, int P, int C) {
@@ -420,6 +421,7 @@ __global__ __launch_bounds__(1024) void column_sum_kernel(const float* __restric
   float a = 0.f;
   if (c < C) {
     const float* src = partial + size_t(r) * P * C + c;
+#pragma unroll 8
     for (int p = grp; p < P; p += G) a += src[size_t(p) * C];
   }
   sh[grp][lane] = a;

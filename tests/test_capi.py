@@ -105,6 +105,18 @@ def test_lif_forward_workspace_sizes(lib, monkeypatch):
     assert lib.lif_backward_workspace_bytes(2, 0, 64) == 0
 
 
+def test_token_shift_mix_workspace_sizes(lib):
+    # One fp32 partial row of grad_mu per (mixing vector, batch row, chunk of
+    # steps); chunks are the longest power of two (64 down to 8) that still
+    # gives 2048 waves of 256 channels.
+    assert lib.token_shift_mix_workspace_bytes(3, 64, 1024, 512) == 3 * 64 * 16 * 512 * 4  # 64
+    assert lib.token_shift_mix_workspace_bytes(3, 128, 1024, 8) == 3 * 128 * 16 * 8 * 4  # 64
+    assert lib.token_shift_mix_workspace_bytes(2, 64, 1003, 16) == 2 * 64 * 32 * 16 * 4  # 32
+    assert lib.token_shift_mix_workspace_bytes(2, 4, 257, 512) == 2 * 4 * 33 * 512 * 4  # 8
+    assert lib.token_shift_mix_workspace_bytes(3, 0, 5, 8) == 0
+    assert lib.token_shift_mix_workspace_bytes(3, 2, 0, 8) == 0
+
+
 def test_step_row_args_layout_matches_header(tmp_path):
     # The ctypes mirror of wkv_step_row_args has the C struct's size and field
     # offsets (compiled with the host C compiler from the header).

@@ -44,6 +44,11 @@ CASES = [  # (B, T, C, n, x dtype, out dtype)
     (2, 130, 256, 2, torch.bfloat16, torch.bfloat16),
     (2, 65, 64, 3, torch.float16, torch.float16),
     (4, 257, 512, 2, torch.float32, torch.bfloat16),
+    # Enough (batch, channel-group) rows that the host picks 64-step chunks
+    # (128 x 16 = 2048 waves), then 32-step chunks with a 3-step tail after the
+    # last 8-step block (T = 1003).
+    (128, 1024, 8, 3, torch.float32, torch.bfloat16),
+    (64, 1003, 16, 2, torch.float32, torch.float32),
 ]
 
 
