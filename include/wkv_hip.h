@@ -269,7 +269,8 @@ int lif_backward(const void* x, const void* grad_spikes, const float* membrane_c
                  void* stream);
 
 /* Bytes of device workspace token_shift_mix_backward needs for n mixing
- * vectors (per-(batch, 64-step chunk) partial sums, fp32). */
+ * vectors (per-(batch, chunk of steps) partial sums, fp32; the chunk length,
+ * 8 to 64 steps, follows from B, T and C). */
 size_t token_shift_mix_workspace_bytes(int64_t n, int64_t B, int64_t T, int64_t C);
 
 /* Fused token-shift mixing (the time-mix and channel-mix prologue).
