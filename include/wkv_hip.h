@@ -185,8 +185,9 @@ int wkv7_forward(const void* r, const void* w, const void* k, const void* v, con
                  const void* b, const float* s0, void* y, float* s_out, int64_t B, int64_t T,
                  int64_t H, int64_t N, int dtype, void* stream);
 
-/* Bytes of the RWKV-7 state checkpoints: the 64x64 fp32 state at the start of
- * every 8-step block, [B*H][ceil(T/8)][64][64]. */
+/* Bytes of the RWKV-7 checkpoint records: one per 8-step block,
+ * [B*H][ceil(T/8)][72][64] fp32; rows 0-63 hold the 64x64 state at the
+ * block's first step, row 64 + s holds S_{t-1} a_t of its step s. */
 size_t wkv7_checkpoint_bytes(int64_t B, int64_t T, int64_t H, int64_t N);
 
 /* wkv7_forward that also writes the state checkpoints (y and s_out may be

@@ -31,12 +31,13 @@
 // registers while the current one is computed).  Arithmetic is fp32 on the
 // vector ALUs; no matrix cores.
 //
-// Checkpoints.  The forward can write the state at the start of every
-// KS-step sub-chunk ([B*H][ceil(T/KS)][64][64] fp32; record 0 holds the
-// initial state).  The backward walks the blocks last to first and, inside
-// each, the sub-chunks last to first; each sub-chunk's forward is recomputed
-// from its own record (no replay), holding S_{t-1} and sa_t in registers,
-// then the reverse recurrence runs over it.
+// Checkpoints.  The forward can write a record per KS-step sub-chunk
+// ([B*H][ceil(T/KS)][64 + KS][64] fp32): rows 0-63 hold the state at the
+// sub-chunk's start (record 0: the initial state), row 64 + s holds sa_t of
+// its step s.  The backward walks the blocks last to first and, inside each,
+// the sub-chunks last to first; each sub-chunk's forward is recomputed from
+// its own record (no replay; sa_t read, not recomputed), holding S_{t-1} and
+// sa_t in registers, then the reverse recurrence runs over it.
 //
 // The reference's RWKV-7 code was deleted
 // (benchmarks/results/optimizer_wkv_experiments_5090.md:3); the output
@@ -52,6 +53,10 @@ constexpr int kThreads = 256;   // threads per workgroup
 constexpr int kKC = 16;         // steps per staged block
 constexpr int kKS = 8;          // steps per checkpoint / backward sub-chunk (registers)
 constexpr int kNSub = kKC / kKS;
+// A checkpoint record: the state at the start of its kKS steps (rows 0-63)
+// and, for each of those steps, sa_t = S_{t-1} a_t (rows 64 ..).
+constexpr int kRecRows = kN + kKS;
+constexpr int kRecFloats = kRecRows * kN;
 
 __device__ __forceinline__ float as_f(unsigned u) { return __uint_as_float(u); }
 
@@ -179,7 +184,8 @@ struct Stager {
 };
 
 // Index of each step vector in the staged block.
-enum { QR = 0, QW = 1, QK = 2, QV = 3, QA = 4, QB = 5, QDY = 6 };
+enum { QR = 0, QW = 1, QK = 2, QV = 3, QA = 4, QB = 5, QDY = 6, QSA = 7 };
+constexpr int kStageVecs = 8;  // the seven inputs, then sa_t from the records
 
 __device__ __forceinline__ float4 lds4(const float* stage, int q, int s, int j) {
   return *reinterpret_cast<const float4*>(stage + (q * kKC + s) * kN + j);
@@ -197,33 +203,24 @@ struct Lane {
   }
 };
 
-// One forward step on the lane's 4x4 block: sa (S_{t-1} a) per row and the
-// next state So from Si (separate arrays, so that an unrolled sequence of
-// steps keeps every state in its own registers without copies).  The row
-// layout of the forward kernel does the same operations in the same order,
-// so both produce the same state bits.
+// One forward step on the lane's 4x4 block: the next state So from Si
+// (separate arrays, so that an unrolled sequence of steps keeps every state
+// in its own registers without copies), with sa (S_{t-1} a) per row taken
+// from the records, where the forward kernel stored the value it used.  The
+// update is the forward's expression, so both produce the same state bits.
 __device__ __forceinline__ void fwd_step(const float (&Si)[4][4], float (&So)[4][4],
                                          const float* stage, int s, const Lane& L,
                                          float (&sa)[4]) {
-  const float4 a4 = lds4(stage, QA, s, L.j0);
   const float4 w4 = lds4(stage, QW, s, L.j0);
   const float4 b4 = lds4(stage, QB, s, L.j0);
   const float4 k4 = lds4(stage, QK, s, L.j0);
   const float4 v4 = lds4(stage, QV, s, L.i0);
-  const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+  const float4 s4 = lds4(stage, QSA, s, L.i0);
   const float w[4] = {w4.x, w4.y, w4.z, w4.w};
   const float b[4] = {b4.x, b4.y, b4.z, b4.w};
   const float k[4] = {k4.x, k4.y, k4.z, k4.w};
   const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float x = Si[r][0] * a[0];
-#pragma unroll
-    for (int c = 1; c < 4; ++c) x = fmaf(Si[r][c], a[c], x);
-    sa[r] = x;
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) sa[r] = row16_sum(sa[r]);
+  sa[0] = s4.x; sa[1] = s4.y; sa[2] = s4.z; sa[3] = s4.w;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -353,8 +350,9 @@ struct RowStager {
 // arithmetic waits on LDS, and the wait for the next block's staging loads
 // finds only old stores ahead of it).
 template <bool FULL, bool CK>
-__device__ __forceinline__ void fwd_rows_block(float (&S)[4], const float* sg, float* yb, int n,
-                                               float (&rec)[kNSub][4], int lr, int j0) {
+__device__ __forceinline__ void fwd_rows_block(float (&S)[4], const float* sg, float* yb,
+                                               float& my_sa, int n, float (&rec)[kNSub][4],
+                                               int lr, int j0) {
 #pragma unroll
   for (int s = 0; s < kKC; ++s) {
     if (FULL || s < n) {
@@ -375,6 +373,8 @@ __device__ __forceinline__ void fwd_rows_block(float (&S)[4], const float* sg, f
 #pragma unroll
       for (int c = 1; c < 4; ++c) x = fmaf(S[c], a[c], x);
       const float sa = row16_sum(x);
+      // Every lane of the DPP row holds the row's sa; lane cg keeps step cg's.
+      if (CK) my_sa = (j0 == 4 * s) ? sa : my_sa;
 #pragma unroll
       for (int c = 0; c < 4; ++c) S[c] = fmaf(S[c], w[c], fmaf(sa, b[c], v * k[c]));
       const float4 r4 = lds4(sg, KR, s, j0);
@@ -448,19 +448,26 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
     const float* sg = stage[blk & 1];
     float* yb = ybuf[blk & 1];
     float rec[kNSub][4];
+    float my_sa = 0.f;  // sa of step cg of the block (row `row`)
+    static_assert(kKC == 16, "one step of sa per lane of a 16-lane DPP row");
     if (n == kKC) {
-      fwd_rows_block<true, CK>(S, sg, yb, n, rec, lr, j0);
+      fwd_rows_block<true, CK>(S, sg, yb, my_sa, n, rec, lr, j0);
     } else {
-      fwd_rows_block<false, CK>(S, sg, yb, n, rec, lr, j0);
+      fwd_rows_block<false, CK>(S, sg, yb, my_sa, n, rec, lr, j0);
     }
     if (blk + 1 < nblk) st.store(stage[(blk + 1) & 1]);
     if (CK) {
-      float* ckr = ck + (size_t(bh) * nrec + blk * kNSub) * kN * kN + row * kN + j0;
+      float* ckr = ck + (size_t(bh) * nrec + blk * kNSub) * kRecFloats + row * kN + j0;
 #pragma unroll
       for (int m = 0; m < kNSub; ++m)
         if (m * kKS < n)
-          *reinterpret_cast<float4*>(ckr + m * kN * kN) =
+          *reinterpret_cast<float4*>(ckr + m * kRecFloats) =
               make_float4(rec[m][0], rec[m][1], rec[m][2], rec[m][3]);
+      // sa of step s = cg of the block into row kN + s mod kKS of its record.
+      const int s = j0 / 4;
+      if (s < n)
+        ck[(size_t(bh) * nrec + blk * kNSub + s / kKS) * kRecFloats + (kN + s % kKS) * kN + row] =
+            my_sa;
     }
     __syncthreads();
     if (y) {
@@ -505,7 +512,7 @@ namespace w7 {
 constexpr int kRedPad = 4;
 
 struct BwdSmem {
-  float stage[2][7 * kKC * kN];
+  float stage[2][kStageVecs * kKC * kN];
   // Per sub-chunk step: per-wave partial sums over the wave's 16 rows of the
   // five key-indexed gradients (dr, dk, dw, da, db) at [(wave * 5 + q) * kN
   // + column], and dv.
@@ -694,6 +701,30 @@ struct GradStores {
   }
 };
 
+// Stages sa_t of one block's kKC steps (rows kN .. of its kNSub records)
+// into LDS as step vector QSA: kKC * kN / 4 pieces of 16 bytes, one per
+// thread.  Steps past T read the last record (never used).
+struct SaStager {
+  static_assert(kKC * kN / 4 == kThreads, "one sa piece per thread");
+  float4 buf;
+
+  __device__ __forceinline__ void load(const float* ckh, int blk, int nrec) {
+    const int p = int(threadIdx.x);
+    const int s = p / (kN / 4);
+    const int pc = p - s * (kN / 4);
+    const int rec = min(blk * kNSub + s / kKS, nrec - 1);
+    buf = *reinterpret_cast<const float4*>(ckh + size_t(rec) * kRecFloats +
+                                           (kN + s % kKS) * kN + pc * 4);
+  }
+
+  __device__ __forceinline__ void store(float* stage) const {
+    const int p = int(threadIdx.x);
+    const int s = p / (kN / 4);
+    const int pc = p - s * (kN / 4);
+    *reinterpret_cast<float4*>(stage + (QSA * kKC + s) * kN + pc * 4) = buf;
+  }
+};
+
 }  // namespace w7
 
 // One workgroup per (batch, head); blocks of kKC steps last to first, each
@@ -726,8 +757,9 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
   wait_vmem_all();
   const int nblk = (T + kKC - 1) / kKC;
   const int nrec = (T + kKS - 1) / kKS;
-  const float* ckh = ck + size_t(bh) * nrec * kN * kN;
+  const float* ckh = ck + size_t(bh) * nrec * kRecFloats;
   Stager<E, 7> st;
+  SaStager sst;
   // Sub-chunks run last to first as one loop.  Loads and stores are ordered
   // so that no fresh store is in flight when a load is waited for (the
   // vector-memory counter counts both, so such a wait would also wait for
@@ -738,8 +770,10 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
   float Sn[4][4];
   if (nblk > 0) {
     st.load(in, bi, h, (nblk - 1) * kKC, T, H);
-    load_state(Sn, ckh + size_t(nrec - 1) * kN * kN, L);
+    sst.load(ckh, nblk - 1, nrec);
+    load_state(Sn, ckh + size_t(nrec - 1) * kRecFloats, L);
     st.store(sm.stage[(nblk - 1) & 1]);
+    sst.store(sm.stage[(nblk - 1) & 1]);
     __syncthreads();
   }
   GradStores<E> out;
@@ -755,10 +789,13 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
     for (int r = 0; r < 4; ++r)
 #pragma unroll
       for (int c = 0; c < 4; ++c) S0[r][c] = Sn[r][c];
-    if (sc > 0) load_state(Sn, ckh + size_t(sc - 1) * kN * kN, L);
+    if (sc > 0) load_state(Sn, ckh + size_t(sc - 1) * kRecFloats, L);
     out.flush();
     // First sub-chunk of this block to run: fetch the previous block.
-    if (blk > 0 && (m == kNSub - 1 || sc == nrec - 1)) st.load(in, bi, h, t0 - kKC, T, H);
+    if (blk > 0 && (m == kNSub - 1 || sc == nrec - 1)) {
+      st.load(in, bi, h, t0 - kKC, T, H);
+      sst.load(ckh, blk - 1, nrec);
+    }
     const float* sg = sm.stage[blk & 1];
     if (cnt == kKS) {
       bwd_subchunk<true>(sm, sc & 1, sg, S0, sl, cnt, L, G);
@@ -771,6 +808,7 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
     // and the barrier after it orders this collect before the one after.
     if (m == 0 && blk > 0) {
       st.store(sm.stage[(blk - 1) & 1]);
+      sst.store(sm.stage[(blk - 1) & 1]);
       __syncthreads();
     }
   }
@@ -783,7 +821,8 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
 namespace wkv_host {
 
 size_t wkv7_checkpoint_floats(int64_t B, int64_t T, int64_t H) {
-  return size_t(B) * size_t(H) * size_t((T + wkv::w7::kKS - 1) / wkv::w7::kKS) * 64 * 64;
+  return size_t(B) * size_t(H) * size_t((T + wkv::w7::kKS - 1) / wkv::w7::kKS) *
+         wkv::w7::kRecFloats;
 }
 
 template <typename E>

@@ -58,7 +58,10 @@ def _check_shapes(r: Tensor, others, state: Tensor | None) -> None:
 
 
 def checkpoint_shape(b: int, t: int, h: int) -> tuple[int, int, int, int, int]:
-    return (b, h, (t + CKPT_STEPS - 1) // CKPT_STEPS, HEAD_SIZE, HEAD_SIZE)
+    """Records of the training forward, one per CKPT_STEPS steps: rows
+    0..HEAD_SIZE-1 hold the state at the record's first step, row
+    HEAD_SIZE + s holds S_{t-1} a_t of its step s (read by the backward)."""
+    return (b, h, (t + CKPT_STEPS - 1) // CKPT_STEPS, HEAD_SIZE + CKPT_STEPS, HEAD_SIZE)
 
 
 def _launch_forward(r, w, k, v, a, b, state, *, with_checkpoint: bool):

@@ -171,11 +171,26 @@ def test_forward_without_checkpoints_equals_training_forward():
     y1, s1 = wkv7_forward_no_checkpoint(*xd, s0.to(DEV))
     y2, s2, ck = ops.wkv7_forward_train(*xd, s0.to(DEV))
     assert torch.equal(y1, y2) and torch.equal(s1, s2)
-    # checkpoint 0 is the initial state, checkpoint j the state after 8 j steps
-    assert torch.equal(ck[:, :, 0], s0.to(DEV))
+    # record 0 starts with the initial state, record j with the state after
+    # 8 j steps
+    assert ck.shape == (2, 2, 5, 72, 64)
+    assert torch.equal(ck[:, :, 0, :64], s0.to(DEV))
     for j in (1, 2, 4):
         _, sj = wkv7_forward_no_checkpoint(*(x[:, :8 * j] for x in xd), s0.to(DEV))
-        assert torch.equal(ck[:, :, j], sj), f"checkpoint {j}"
+        assert torch.equal(ck[:, :, j, :64], sj), f"checkpoint {j}"
+    # row 64 + s of record j holds S_{t-1} a_t for t = 8 j + s (the backward
+    # reads it instead of recomputing it); steps 0 .. 36 of 37, so record 4
+    # holds five.  Summation order differs from the kernel's: fp32 bar.
+    a = xd[4].float()
+    for t in (0, 1, 7, 8, 13, 31, 32, 36):
+        if t == 0:
+            s_prev = s0.to(DEV)
+        else:
+            _, s_prev = wkv7_forward_no_checkpoint(*(x[:, :t] for x in xd), s0.to(DEV))
+        want = torch.matmul(s_prev, a[:, t].unsqueeze(-1).contiguous()).squeeze(-1)
+        got = ck[:, :, t // 8, 64 + t % 8]
+        err = (got - want).abs().max().item()
+        assert err <= 1e-5 * max(want.abs().max().item(), 1.0), f"sa at step {t}: {err:.3e}"
 
 
 def test_deterministic():
