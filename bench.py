@@ -399,7 +399,7 @@ def bench_decode(args) -> dict:
     per_layer = elapsed / args.steps / layers
     alg = 36 * B * C  # k, v read (8 B); state read and written (24 B); y written (4 B)
     achieved = alg / per_layer / 1e9
-    return {
+    out = {
         "metric": "WKV decode state update tokens/sec, B=256 C=768 x18 layers fp32 state",
         "value": B * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True,
@@ -413,6 +413,34 @@ def bench_decode(args) -> dict:
                      "kernel": "wkv4_decode_kernel (per-layer graph time, dispatch gaps included)",
                      "algorithmic_bytes_per_launch": alg},
     }
+    if not args.no_cpu_baseline:
+        # The reference's decode is this eager step (language.py:989-1012),
+        # restated by the oracle: one token through the 18 layers on the host.
+        torch.set_num_threads(os.cpu_count() or 1)
+        kc = [k.cpu() for k in ks]
+        vc = [v.cpu() for v in vs]
+        tdc = [t.cpu() for t in tds]
+        tfc = [t.cpu() for t in tfs]
+        cst = [O.initial_decode_state(B, C) for _ in range(layers)]
+
+        def cpu_token():
+            for layer in range(layers):
+                _, *cst[layer] = O.decode_step(kc[layer], vc[layer], tdc[layer], tfc[layer],
+                                               *cst[layer])
+
+        cpu_token()
+        n = 50
+        t0 = time.perf_counter()
+        for _ in range(n):
+            cpu_token()
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {
+            "value": B * n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{n} tokens at B={B}, C={C} through the {layers} layers' WKV state "
+                      f"updates, the oracle's eager fp32 step (language.py:989-1012 restated); "
+                      f"host {_cpu_model()}"}
+    return out
 
 
 def bench_block_decode(args) -> dict:
@@ -544,7 +572,7 @@ def bench_wkv7(args) -> dict:
     fwd_bytes = 14 * N * units      # r, w, k, v, a, b read, y written (bf16)
     bwd_bytes = 26 * N * units      # 6 inputs + dy read, 6 grads written (bf16)
     achieved = bwd_flops / bwd_t / 1e12
-    return {
+    out = {
         "metric": "RWKV-7 DPLR fwd+bwd tokens/sec, B=16 T=1024 H=12 N=64 bf16 I/O fp32 state",
         "value": B * T / step_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True,
@@ -560,6 +588,25 @@ def bench_wkv7(args) -> dict:
                      "kernel": "wkv7_bwd_kernel", "algorithmic_flops_per_launch": bwd_flops,
                      "avg_launch_us": bwd_t * 1e6},
     }
+    if not args.no_cpu_baseline:
+        # No CPU path survives in the reference for RWKV-7 (its code was
+        # deleted); the oracle's fp32 loops are the host counterpart: the
+        # forward recurrence, then the explicit reverse recurrence.
+        torch.set_num_threads(os.cpu_count() or 1)
+        bs = 1
+        xc = [x[:bs].float().cpu() for x in xs]
+        gyc = gy[:bs].float().cpu()
+        t0 = time.perf_counter()
+        O7.wkv7_loop(*xc)
+        O7.wkv7_backward_loop(*xc, None, gyc)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {
+            "value": bs * T / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"B={bs} of {B}, T={T}, H={H}: the oracle's fp32 forward loop and explicit "
+                      f"reverse loop (the reference's RWKV-7 code was deleted), one run; host "
+                      f"{_cpu_model()}"}
+    return out
 
 
 def bench_lif(args) -> dict:
