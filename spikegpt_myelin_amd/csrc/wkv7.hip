@@ -403,8 +403,9 @@ __device__ __forceinline__ int xcd_local_block() {
 
 // ------------------------------------------------------------- forward ----
 // kSplit workgroups per (batch, head), kRows state rows each.  ck (optional):
-// state at the start of every kKS-step sub-chunk, [B*H][ceil(T/kKS)][64][64]
-// (each workgroup writes its rows).  y may be null (records only).
+// one record per kKS-step sub-chunk, [B*H][ceil(T/kKS)][kRecRows][64]: the
+// state at its start and sa_t of its steps (each workgroup writes its rows).
+// y may be null (records only).
 template <typename E, bool CK>
 __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
     w7::Vecs<E, 6> in, const float* __restrict__ s0, typename E::raw* __restrict__ y,
