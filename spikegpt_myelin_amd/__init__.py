@@ -26,6 +26,7 @@ from .decode import initial_wkv_state, wkv_decode_step
 from .language import validate_wkv_inputs, weighted_key_value
 from .gates import relu_square, sigmoid_gate
 from .lif import lif_sequence
+from .splitk import split_k_sum
 from .timemix import token_shift_mix
 from .wkv import (
     weighted_key_value_gated,
@@ -41,6 +42,7 @@ __all__ = [
     "lif_sequence",
     "relu_square",
     "sigmoid_gate",
+    "split_k_sum",
     "token_shift_mix",
     "validate_wkv_inputs",
     "weighted_key_value",

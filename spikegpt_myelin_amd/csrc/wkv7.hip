@@ -464,11 +464,13 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_fwd_kernel(
         if (m * kKS < n)
           *reinterpret_cast<float4*>(ckr + m * kRecFloats) =
               make_float4(rec[m][0], rec[m][1], rec[m][2], rec[m][3]);
-      // sa of step s = cg of the block into row kN + s mod kKS of its record.
+      // sa of step s = cg of the block into row kN + s mod kKS of its record;
+      // the rows of steps past T in the last record hold zeros (so that the
+      // records are fully written).
       const int s = j0 / 4;
-      if (s < n)
+      if (blk * kNSub + s / kKS < nrec)
         ck[(size_t(bh) * nrec + blk * kNSub + s / kKS) * kRecFloats + (kN + s % kKS) * kN + row] =
-            my_sa;
+            s < n ? my_sa : 0.f;
     }
     __syncthreads();
     if (y) {

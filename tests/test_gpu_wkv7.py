@@ -191,6 +191,8 @@ def test_forward_without_checkpoints_equals_training_forward():
         got = ck[:, :, t // 8, 64 + t % 8]
         err = (got - want).abs().max().item()
         assert err <= 1e-5 * max(want.abs().max().item(), 1.0), f"sa at step {t}: {err:.3e}"
+    # the rows of steps 37 .. 39 (past T) in the last record are zeros
+    assert torch.all(ck[:, :, 4, 64 + 5:] == 0)
 
 
 def test_deterministic():
