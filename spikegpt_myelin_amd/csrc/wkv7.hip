@@ -203,24 +203,31 @@ struct Lane {
   }
 };
 
+// Staged vectors of one recomputed forward step (w, b, k on the lane's
+// columns; v and sa on its rows).
+struct FwdVecs {
+  float4 w, b, k, v, sa;
+  __device__ __forceinline__ void load(const float* stage, int s, int i0, int j0) {
+    w = lds4(stage, QW, s, j0);
+    b = lds4(stage, QB, s, j0);
+    k = lds4(stage, QK, s, j0);
+    v = lds4(stage, QV, s, i0);
+    sa = lds4(stage, QSA, s, i0);
+  }
+};
+
 // One forward step on the lane's 4x4 block: the next state So from Si
 // (separate arrays, so that an unrolled sequence of steps keeps every state
 // in its own registers without copies), with sa (S_{t-1} a) per row taken
 // from the records, where the forward kernel stored the value it used.  The
 // update is the forward's expression, so both produce the same state bits.
 __device__ __forceinline__ void fwd_step(const float (&Si)[4][4], float (&So)[4][4],
-                                         const float* stage, int s, const Lane& L,
-                                         float (&sa)[4]) {
-  const float4 w4 = lds4(stage, QW, s, L.j0);
-  const float4 b4 = lds4(stage, QB, s, L.j0);
-  const float4 k4 = lds4(stage, QK, s, L.j0);
-  const float4 v4 = lds4(stage, QV, s, L.i0);
-  const float4 s4 = lds4(stage, QSA, s, L.i0);
-  const float w[4] = {w4.x, w4.y, w4.z, w4.w};
-  const float b[4] = {b4.x, b4.y, b4.z, b4.w};
-  const float k[4] = {k4.x, k4.y, k4.z, k4.w};
-  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-  sa[0] = s4.x; sa[1] = s4.y; sa[2] = s4.z; sa[3] = s4.w;
+                                         const FwdVecs& x, float (&sa)[4]) {
+  const float w[4] = {x.w.x, x.w.y, x.w.z, x.w.w};
+  const float b[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
+  const float k[4] = {x.k.x, x.k.y, x.k.z, x.k.w};
+  const float v[4] = {x.v.x, x.v.y, x.v.z, x.v.w};
+  sa[0] = x.sa.x; sa[1] = x.sa.y; sa[2] = x.sa.z; sa[3] = x.sa.w;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -514,6 +521,21 @@ namespace w7 {
 // step spread them (and keep 16-byte alignment).
 constexpr int kRedPad = 4;
 
+// Staged vectors of one reverse step (r, w, k, a, b on the lane's columns;
+// v and dy on its rows).
+struct RevVecs {
+  float4 r, w, k, a, b, v, g;
+  __device__ __forceinline__ void load(const float* stage, int s, int i0, int j0) {
+    r = lds4(stage, QR, s, j0);
+    w = lds4(stage, QW, s, j0);
+    k = lds4(stage, QK, s, j0);
+    a = lds4(stage, QA, s, j0);
+    b = lds4(stage, QB, s, j0);
+    v = lds4(stage, QV, s, i0);
+    g = lds4(stage, QDY, s, i0);
+  }
+};
+
 struct BwdSmem {
   float stage[2][kStageVecs * kKC * kN];
   // Per sub-chunk step: per-wave partial sums over the wave's 16 rows of the
@@ -546,36 +568,52 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
   float* const dv_base = dv_lane ? &sm.dvb[rbuf][0][L.i0 + L.cg] : &sm.dv_sink[threadIdx.x];
   const int dv_stride = dv_lane ? kN + kRedPad : 0;
   // Recompute the sub-chunk: Sp[s] = S_{t-1} of step s, Sp[s+1] = S_t; sa_t
-  // kept.
+  // kept.  In a full sub-chunk every step's LDS vectors are read one step
+  // ahead (the last recomputed step reads the first reverse step's), so no
+  // step waits for its own reads.
   float Sp[KS + 1][4][4], sas[KS][4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int c = 0; c < 4; ++c) Sp[0][r][c] = S0[r][c];
+  FwdVecs fx;
+  RevVecs rx;
+  if (FULL) fx.load(sg, sl, L.i0, L.j0);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    if (FULL || s < cnt) fwd_step(Sp[s], Sp[s + 1], sg, sl + s, L, sas[s]);
+    if (FULL) {
+      const FwdVecs cur = fx;
+      if (s + 1 < KS) {
+        fx.load(sg, sl + s + 1, L.i0, L.j0);
+      } else {
+        rx.load(sg, sl + KS - 1, L.i0, L.j0);
+      }
+      fwd_step(Sp[s], Sp[s + 1], cur, sas[s]);
+    } else if (s < cnt) {
+      FwdVecs cur;
+      cur.load(sg, sl + s, L.i0, L.j0);
+      fwd_step(Sp[s], Sp[s + 1], cur, sas[s]);
+    }
   }
   // Reverse; the post-update state of step s (S_t) is Sp[s + 1].
 #pragma unroll
   for (int s = KS - 1; s >= 0; --s) {
     if (FULL || s < cnt) {
       const float (&St)[4][4] = Sp[s + 1];
-      const int ss = sl + s;
-      const float4 r4 = lds4(sg, QR, ss, L.j0);
-      const float4 w4 = lds4(sg, QW, ss, L.j0);
-      const float4 k4 = lds4(sg, QK, ss, L.j0);
-      const float4 a4 = lds4(sg, QA, ss, L.j0);
-      const float4 b4 = lds4(sg, QB, ss, L.j0);
-      const float4 v4 = lds4(sg, QV, ss, L.i0);
-      const float4 g4 = lds4(sg, QDY, ss, L.i0);
-      const float rr[4] = {r4.x, r4.y, r4.z, r4.w};
-      const float ww[4] = {w4.x, w4.y, w4.z, w4.w};
-      const float kk[4] = {k4.x, k4.y, k4.z, k4.w};
-      const float aa[4] = {a4.x, a4.y, a4.z, a4.w};
-      const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
-      const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-      const float gy[4] = {g4.x, g4.y, g4.z, g4.w};
+      RevVecs x;
+      if (FULL) {
+        x = rx;
+        if (s > 0) rx.load(sg, sl + s - 1, L.i0, L.j0);
+      } else {
+        x.load(sg, sl + s, L.i0, L.j0);
+      }
+      const float rr[4] = {x.r.x, x.r.y, x.r.z, x.r.w};
+      const float ww[4] = {x.w.x, x.w.y, x.w.z, x.w.w};
+      const float kk[4] = {x.k.x, x.k.y, x.k.z, x.k.w};
+      const float aa[4] = {x.a.x, x.a.y, x.a.z, x.a.w};
+      const float bb[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
+      const float vv[4] = {x.v.x, x.v.y, x.v.z, x.v.w};
+      const float gy[4] = {x.g.x, x.g.y, x.g.z, x.g.w};
       float pr[4], pk[4], pw[4], pa[4], pb[4], dvr[4], cc[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
