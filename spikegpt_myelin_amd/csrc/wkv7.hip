@@ -22,11 +22,12 @@
 //
 // Backward layout.  One 256-thread workgroup (4 waves) owns one (batch,
 // head): lane (rg, cg) of wave wv holds the 4x4 block of the state (and of
-// its gradient) at rows 16 wv + 4 rg .. +3 and columns 4 cg .. +3.  Sums over j (S a, S r, G k, G b) are in-thread
-// over 4 columns, then a DPP butterfly across the 16 lanes of a DPP row (no
+// its gradient) at rows 16 wv + 4 rg .. +3 and columns 4 cg .. +3.  Sums
+// over j (S a, S r, G k, G b) are in-thread over 4 columns, then a DPP butterfly across the 16 lanes of a DPP row (no
 // LDS).  Sums over i (the key-indexed gradients) are in-thread over 4 rows,
 // then two gfx950 permlane swaps across the 4 DPP rows of the wave, then LDS
-// across the 4 waves once per sub-chunk.  The step vectors of KC = 16 steps
+// across the 4 waves once per sub-chunk (collected while the next sub-chunk
+// is recomputed).  The step vectors of KC = 16 steps
 // are staged in LDS as fp32 (double-buffered; the next block is loaded into
 // registers while the current one is computed).  Arithmetic is fp32 on the
 // vector ALUs; no matrix cores.
@@ -548,17 +549,25 @@ struct BwdSmem {
   float dvb[2][kKS][kN + kRedPad];
   // Store target of the lanes that hold no dv value (one word per thread).
   float dv_sink[kThreads];
+  // -0.0 x 4: the three missing partials of a dv output in GradStores
+  // (adding -0.0 leaves every value, -0.0 included, unchanged).
+  float neg_zero[4];
 };
 
 // Recompute + reverse over one sub-chunk of cnt steps starting at staged
 // step sl, from the sub-chunk's state record S0 (FULL: cnt == kKS, no
 // per-step guards).  Leaves the per-step partial sums in sm.red / sm.dvb and
 // advances G to before the sub-chunk.
-template <bool FULL>
+template <bool FULL, typename Pre>
 __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float* sg,
                                              const float (&S0)[4][4],
-                                             int sl, int cnt, const Lane& L, float (&G)[4][4]) {
+                                             int sl, int cnt, const Lane& L, float (&G)[4][4],
+                                             Pre&& pre) {
   constexpr int KS = kKS;
+  // Work of the previous sub-chunk (its gradients' collection) issued in the
+  // same basic block as this one's, so its LDS reads and sums interleave
+  // with the recomputation below.
+  pre();
   const int col = L.j0 + L.rg;  // column this lane holds after rows4_sum
   // dv of row i0 + cg is stored by lane cg < 4 of each DPP row (every lane of
   // the row holds the four rows' sums); the other lanes store to their own
@@ -674,71 +683,79 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
   }
 }
 
-// The six gradients of one sub-chunk (dr, dk, dw, da, db from the four
-// waves' partial sums in sm.red, dv from sm.dvb), packed to the element
-// type in registers by collect() and written by flush(), which the caller
-// issues after its next wait on a load.
+// The six gradients of one sub-chunk of kKS steps: 5 x kKS x 16 outputs of
+// four columns summed over the four waves' partials in sm.red (dr, dk, dw,
+// da, db), then kKS x 16 of dv from sm.dvb; 768 outputs, three per thread.
+// collect() has no branch (the gradient an output belongs to is the same in
+// every lane of a wave, and a dv output adds three -0.0 partials, which leave
+// every value unchanged), so the caller can place it in the basic block of
+// the next sub-chunk's work; the sums run in the order ((w0 + w1) + w2) + w3
+// over the waves.  flush() writes the outputs of steps < cnt; the caller
+// issues it after its next wait on a load.
 template <typename E>
 struct GradStores {
   using raw = typename E::raw;
-  static constexpr int EPP = 16 / int(sizeof(raw));
-  static constexpr int PPV = kN / EPP;
-  static constexpr int NS = (6 * kKS * PPV + kThreads - 1) / kThreads;
-  uint4 data[NS];
-  raw* dst[NS];
+  static constexpr int NO = 3;
+  static_assert(6 * kKS * (kN / 4) == NO * kThreads, "three outputs per thread");
+  static_assert(kKS * (kN / 4) % 64 == 0, "one gradient per wave and output slot");
+  OutPack<E, 4> data[NO];
 
-  __device__ __forceinline__ GradStores() {
-#pragma unroll
-    for (int k = 0; k < NS; ++k) dst[k] = nullptr;
+  // Gradient (0-4: dr, dk, dw, da, db; 5: dv), step and column group of
+  // output slot k of this thread.
+  __device__ static __forceinline__ int grad_of(int k) {
+    return __builtin_amdgcn_readfirstlane((int(threadIdx.x) + k * kThreads) / (kKS * (kN / 4)));
+  }
+  __device__ static __forceinline__ int step_of(int k) {
+    return ((int(threadIdx.x) + k * kThreads) / (kN / 4)) % kKS;
+  }
+  __device__ static __forceinline__ int col_of(int k) {
+    return 4 * ((int(threadIdx.x) + k * kThreads) % (kN / 4));
   }
 
-  __device__ __forceinline__ void collect(const BwdSmem& sm, int rbuf, raw* dr, raw* dk, raw* dw,
-                                          raw* da,
-                                          raw* db, raw* dv, int bi, int h, int t, int cnt, int T,
-                                          int H) {
+  __device__ __forceinline__ void collect(const BwdSmem& sm, int rbuf) {
 #pragma unroll
-    for (int k = 0; k < NS; ++k) {
-      const int p = int(threadIdx.x) + k * kThreads;
-      dst[k] = nullptr;
-      if (p < 6 * cnt * PPV) {
-        const int q = p / (cnt * PPV);
-        const int rem = p - q * (cnt * PPV);
-        const int s = rem / PPV;
-        const int pc = rem - s * PPV;
-        float f[EPP];
-#pragma unroll
-        for (int e = 0; e < EPP; e += 4) {
-          float4 x;
-          if (q < 5) {
-            x = *reinterpret_cast<const float4*>(&sm.red[rbuf][s][q * kN + pc * EPP + e]);
-#pragma unroll
-            for (int wv = 1; wv < 4; ++wv) {
-              const float4 z = *reinterpret_cast<const float4*>(
-                  &sm.red[rbuf][s][(wv * 5 + q) * kN + pc * EPP + e]);
-              x.x += z.x; x.y += z.y; x.z += z.z; x.w += z.w;
-            }
-          } else {
-            x = *reinterpret_cast<const float4*>(&sm.dvb[rbuf][s][pc * EPP + e]);
-          }
-          f[e] = x.x; f[e + 1] = x.y; f[e + 2] = x.z; f[e + 3] = x.w;
-        }
-        raw* o = q == 0 ? dr : q == 1 ? dk : q == 2 ? dw : q == 3 ? da : q == 4 ? db : dv;
-        dst[k] = o + ((size_t(bi) * T + t + s) * H + h) * kN + pc * EPP;
-        if constexpr (EPP == 4) {
-          data[k] = make_uint4(as_u(f[0]), as_u(f[1]), as_u(f[2]), as_u(f[3]));
-        } else {
-          OutPack<E, 8> o8;
-          o8.set(f);
-          data[k] = make_uint4(o8.u[0], o8.u[1], o8.u[2], o8.u[3]);
-        }
-      }
+    for (int k = 0; k < NO; ++k) {
+      const int q = grad_of(k);
+      const int s = step_of(k);
+      const int c = col_of(k);
+      const float* red = &sm.red[rbuf][s][(q < 5 ? q : 0) * kN + c];
+      const bool sum = q < 5;
+      const float* p0 = sum ? red : &sm.dvb[rbuf][s][c];
+      const float* p1 = sum ? red + 5 * kN : sm.neg_zero;
+      const float* p2 = sum ? red + 10 * kN : sm.neg_zero;
+      const float* p3 = sum ? red + 15 * kN : sm.neg_zero;
+      float4 x = *reinterpret_cast<const float4*>(p0);
+      const float4 x1 = *reinterpret_cast<const float4*>(p1);
+      const float4 x2 = *reinterpret_cast<const float4*>(p2);
+      const float4 x3 = *reinterpret_cast<const float4*>(p3);
+      x.x += x1.x; x.y += x1.y; x.z += x1.z; x.w += x1.w;
+      x.x += x2.x; x.y += x2.y; x.z += x2.z; x.w += x2.w;
+      x.x += x3.x; x.y += x3.y; x.z += x3.z; x.w += x3.w;
+      const float f[4] = {x.x, x.y, x.z, x.w};
+      data[k].set(f);
     }
   }
 
-  __device__ __forceinline__ void flush() {
+  // outs: dr, dk, dw, da, db, dv; t: first step of the sub-chunk.
+  __device__ __forceinline__ void flush(raw* const (&outs)[6], int bi, int h, int t, int cnt,
+                                        int T, int H) const {
 #pragma unroll
-    for (int k = 0; k < NS; ++k)
-      if (dst[k]) *reinterpret_cast<uint4*>(dst[k]) = data[k];
+    for (int k = 0; k < NO; ++k) {
+      const int q = grad_of(k);
+      const int s = step_of(k);
+      raw* o = outs[0];
+#pragma unroll
+      for (int i = 1; i < 6; ++i) o = (q == i) ? outs[i] : o;
+      raw* dst = o + ((size_t(bi) * T + t + s) * H + h) * kN + col_of(k);
+      if (s < cnt) {
+        if constexpr (sizeof(raw) == 4) {
+          *reinterpret_cast<uint4*>(dst) =
+              make_uint4(data[k].u[0], data[k].u[1], data[k].u[2], data[k].u[3]);
+        } else {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(data[k].u[0], data[k].u[1]);
+        }
+      }
+    }
   }
 };
 
@@ -817,6 +834,12 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
     sst.store(sm.stage[(nblk - 1) & 1]);
     __syncthreads();
   }
+  using raw = typename E::raw;
+  if (threadIdx.x < 4) sm.neg_zero[threadIdx.x] = -0.f;
+  raw* const outs[6] = {dr, dk, dw, da, db, dv};
+  // The gradients of sub-chunk sc + 1 are collected during sub-chunk sc (in
+  // its basic block, overlapping its recomputation) and stored at the start
+  // of sub-chunk sc - 1.
   GradStores<E> out;
   for (int sc = nrec - 1; sc >= 0; --sc) {
     const int blk = sc / kNSub;
@@ -831,29 +854,36 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c) S0[r][c] = Sn[r][c];
     if (sc > 0) load_state(Sn, ckh + size_t(sc - 1) * kRecFloats, L);
-    out.flush();
+    // Gradients of sub-chunk sc + 2 (none before the third sub-chunk).
+    if (sc + 2 < nrec) out.flush(outs, bi, h, (sc + 2) * kKS, min(kKS, T - (sc + 2) * kKS), T, H);
     // First sub-chunk of this block to run: fetch the previous block.
     if (blk > 0 && (m == kNSub - 1 || sc == nrec - 1)) {
       st.load(in, bi, h, t0 - kKC, T, H);
       sst.load(ckh, blk - 1, nrec);
     }
     const float* sg = sm.stage[blk & 1];
+    // Sub-chunk sc + 1's sums are in sm.red / sm.dvb [(sc + 1) & 1] since the
+    // last barrier; in the first sub-chunk those buffers hold nothing yet
+    // and the collected values are never stored.  Only the last sub-chunk of
+    // the sequence (the first to run) can be partial.
     if (cnt == kKS) {
-      bwd_subchunk<true>(sm, sc & 1, sg, S0, sl, cnt, L, G);
+      bwd_subchunk<true>(sm, sc & 1, sg, S0, sl, cnt, L, G,
+                         [&] { out.collect(sm, (sc + 1) & 1); });
     } else {
-      bwd_subchunk<false>(sm, sc & 1, sg, S0, sl, cnt, L, G);
+      bwd_subchunk<false>(sm, sc & 1, sg, S0, sl, cnt, L, G, [] {});
     }
     __syncthreads();
-    out.collect(sm, sc & 1, dr, dk, dw, da, db, dv, bi, h, t0 + sl, cnt, T, H);
-    // No barrier here: the next sub-chunk writes the other reduction buffer,
-    // and the barrier after it orders this collect before the one after.
     if (m == 0 && blk > 0) {
       st.store(sm.stage[(blk - 1) & 1]);
       sst.store(sm.stage[(blk - 1) & 1]);
       __syncthreads();
     }
   }
-  out.flush();
+  if (nrec > 1) out.flush(outs, bi, h, kKS, min(kKS, T - kKS), T, H);
+  if (nrec > 0) {
+    out.collect(sm, 0);
+    out.flush(outs, bi, h, 0, min(kKS, T), T, H);
+  }
   if (ds0) store_state(ds0 + state_off(bh, 0, 0), G, L);
 }
 
