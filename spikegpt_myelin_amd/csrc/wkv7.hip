@@ -23,14 +23,14 @@
 // Backward layout.  One 256-thread workgroup (4 waves) owns one (batch,
 // head): lane (rg, cg) of wave wv holds the 4x4 block of the state (and of
 // its gradient) at rows 16 wv + 4 rg .. +3 and columns 4 cg .. +3.  Sums
-// over j (S a, S r, G k, G b) are in-thread over 4 columns, then a DPP butterfly across the 16 lanes of a DPP row (no
-// LDS).  Sums over i (the key-indexed gradients) are in-thread over 4 rows,
-// then two gfx950 permlane swaps across the 4 DPP rows of the wave, then LDS
-// across the 4 waves once per sub-chunk (collected while the next sub-chunk
-// is recomputed).  The step vectors of KC = 16 steps
-// are staged in LDS as fp32 (double-buffered; the next block is loaded into
-// registers while the current one is computed).  Arithmetic is fp32 on the
-// vector ALUs; no matrix cores.
+// over j (S a, S r, G k, G b) are in-thread over 4 columns, then a DPP
+// butterfly across the 16 lanes of a DPP row (no LDS).  Sums over i (the
+// key-indexed gradients) are in-thread over 4 rows, then two gfx950 permlane
+// swaps across the 4 DPP rows of the wave, then LDS across the 4 waves once
+// per sub-chunk (collected while the next sub-chunk is recomputed).  The
+// step vectors of KC = 16 steps are staged in LDS as fp32 (double-buffered;
+// the next block is loaded into registers while the current one is
+// computed).  Arithmetic is fp32 on the vector ALUs; no matrix cores.
 //
 // Checkpoints.  The forward can write a record per KS-step sub-chunk
 // ([B*H][ceil(T/KS)][64 + KS][64] fp32): rows 0-63 hold the state at the
