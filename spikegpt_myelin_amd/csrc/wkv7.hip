@@ -37,8 +37,8 @@
 // sub-chunk's start (record 0: the initial state), row 64 + s holds sa_t of
 // its step s.  The backward walks the blocks last to first and, inside each,
 // the sub-chunks last to first; each sub-chunk's forward is recomputed from
-// its own record (no replay; sa_t read, not recomputed), holding S_{t-1} and
-// sa_t in registers, then the reverse recurrence runs over it.
+// its own record (no replay; sa_t read, not recomputed), holding the states
+// in registers, then the reverse recurrence runs over it.
 //
 // The reference's RWKV-7 code was deleted
 // (benchmarks/results/optimizer_wkv_experiments_5090.md:3); the output
@@ -223,12 +223,12 @@ struct FwdVecs {
 // from the records, where the forward kernel stored the value it used.  The
 // update is the forward's expression, so both produce the same state bits.
 __device__ __forceinline__ void fwd_step(const float (&Si)[4][4], float (&So)[4][4],
-                                         const FwdVecs& x, float (&sa)[4]) {
+                                         const FwdVecs& x) {
   const float w[4] = {x.w.x, x.w.y, x.w.z, x.w.w};
   const float b[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
   const float k[4] = {x.k.x, x.k.y, x.k.z, x.k.w};
   const float v[4] = {x.v.x, x.v.y, x.v.z, x.v.w};
-  sa[0] = x.sa.x; sa[1] = x.sa.y; sa[2] = x.sa.z; sa[3] = x.sa.w;
+  const float sa[4] = {x.sa.x, x.sa.y, x.sa.z, x.sa.w};
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -523,9 +523,10 @@ namespace w7 {
 constexpr int kRedPad = 4;
 
 // Staged vectors of one reverse step (r, w, k, a, b on the lane's columns;
-// v and dy on its rows).
+// v, dy and sa on its rows; sa is read again rather than kept in registers
+// from the recomputation).
 struct RevVecs {
-  float4 r, w, k, a, b, v, g;
+  float4 r, w, k, a, b, v, g, sa;
   __device__ __forceinline__ void load(const float* stage, int s, int i0, int j0) {
     r = lds4(stage, QR, s, j0);
     w = lds4(stage, QW, s, j0);
@@ -534,6 +535,7 @@ struct RevVecs {
     b = lds4(stage, QB, s, j0);
     v = lds4(stage, QV, s, i0);
     g = lds4(stage, QDY, s, i0);
+    sa = lds4(stage, QSA, s, i0);
   }
 };
 
@@ -576,11 +578,11 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
   const bool dv_lane = L.cg < 4;
   float* const dv_base = dv_lane ? &sm.dvb[rbuf][0][L.i0 + L.cg] : &sm.dv_sink[threadIdx.x];
   const int dv_stride = dv_lane ? kN + kRedPad : 0;
-  // Recompute the sub-chunk: Sp[s] = S_{t-1} of step s, Sp[s+1] = S_t; sa_t
-  // kept.  In a full sub-chunk every step's LDS vectors are read one step
-  // ahead (the last recomputed step reads the first reverse step's), so no
-  // step waits for its own reads.
-  float Sp[KS + 1][4][4], sas[KS][4];
+  // Recompute the sub-chunk: Sp[s] = S_{t-1} of step s, Sp[s+1] = S_t.  In a
+  // full sub-chunk every step's LDS vectors are read one step ahead (the
+  // last recomputed step reads the first reverse step's), so no step waits
+  // for its own reads.
+  float Sp[KS + 1][4][4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -597,11 +599,11 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
       } else {
         rx.load(sg, sl + KS - 1, L.i0, L.j0);
       }
-      fwd_step(Sp[s], Sp[s + 1], cur, sas[s]);
+      fwd_step(Sp[s], Sp[s + 1], cur);
     } else if (s < cnt) {
       FwdVecs cur;
       cur.load(sg, sl + s, L.i0, L.j0);
-      fwd_step(Sp[s], Sp[s + 1], cur, sas[s]);
+      fwd_step(Sp[s], Sp[s + 1], cur);
     }
   }
   // Reverse; the post-update state of step s (S_t) is Sp[s + 1].
@@ -623,6 +625,7 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
       const float bb[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
       const float vv[4] = {x.v.x, x.v.y, x.v.z, x.v.w};
       const float gy[4] = {x.g.x, x.g.y, x.g.z, x.g.w};
+      const float sa[4] = {x.sa.x, x.sa.y, x.sa.z, x.sa.w};
       float pr[4], pk[4], pw[4], pa[4], pb[4], dvr[4], cc[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -654,13 +657,13 @@ __device__ __forceinline__ void bwd_subchunk(BwdSmem& sm, int rbuf, const float*
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         float xk = G[0][c] * vv[0], xw = G[0][c] * Sp[s][0][c];
-        float xa = Sp[s][0][c] * cc[0], xb = G[0][c] * sas[s][0];
+        float xa = Sp[s][0][c] * cc[0], xb = G[0][c] * sa[0];
 #pragma unroll
         for (int r = 1; r < 4; ++r) {
           xk = fmaf(G[r][c], vv[r], xk);
           xw = fmaf(G[r][c], Sp[s][r][c], xw);
           xa = fmaf(Sp[s][r][c], cc[r], xa);
-          xb = fmaf(G[r][c], sas[s][r], xb);
+          xb = fmaf(G[r][c], sa[r], xb);
         }
         pk[c] = xk; pw[c] = xw; pa[c] = xa; pb[c] = xb;
       }
