@@ -827,7 +827,7 @@ __global__ __launch_bounds__(w7::kThreads) void wkv7_bwd_kernel(
   // the store): the record of the next sub-chunk is fetched one sub-chunk
   // ahead, a block's staging loads are issued after its first record has
   // arrived, and each sub-chunk's gradients are held in registers and
-  // stored after the next record has arrived.
+  // stored two sub-chunks later, once that sub-chunk's record has arrived.
   float Sn[4][4];
   if (nblk > 0) {
     st.load(in, bi, h, (nblk - 1) * kKC, T, H);
