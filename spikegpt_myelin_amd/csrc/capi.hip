@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <initializer_list>
@@ -71,6 +72,12 @@ bool env_cfg(const char* name, int& vec, int& L, int& W) {
   const char* s = getenv(name);
   if (!s) return false;
   return sscanf(s, "%d,%d,%d", &vec, &L, &W) == 3;
+}
+
+int lb_poll_limit() {
+  const char* s = getenv("WKV_LB_MAX_POLLS");
+  if (!s) return wkv::kLbMaxPolls;
+  return std::min(std::max(atoi(s), -1), wkv::kLbMaxPolls);
 }
 
 static bool dtype_ok(int dtype) { return dtype >= 0 && dtype <= 2; }

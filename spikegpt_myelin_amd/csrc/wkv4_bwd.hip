@@ -604,7 +604,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_split_kernel(
     const float* __restrict__ ck, typename E::raw* __restrict__ gk,
     typename E::raw* __restrict__ gv, typename E::raw* __restrict__ gr,
     float* __restrict__ gw_part, float* __restrict__ gu_part, uint64_t* __restrict__ lb,
-    uint32_t* __restrict__ status, int rows, int T, int C) {
+    uint32_t* __restrict__ status, int rows, int T, int C, int max_polls) {
   using F = Bwd<E, VEC, L, W, GATE>;
   using PackT = typename F::PackT;
   __shared__ typename F::Smem sm;
@@ -726,7 +726,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_split_kernel(
     float rg[VEC], rh[VEC];
     const uint64_t* base = lb + size_t(row) * F::CPW + lane * VEC;
     const bool gave_up = !lb_window_carry<VEC>(base, base + plane, size_t(rows) * F::CPW, seg,
-                                               nseg, -1, DS, rg, rh);
+                                               nseg, -1, DS, rg, rh, max_polls);
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       lb_store(mine + plane + c, lb_pack(fmaf(DS[c], rg[c], ag[c]), fmaf(DS[c], rh[c], ah[c])));
@@ -1010,11 +1010,12 @@ static int launch_bwd_split(const void* gy, const float* decay, int decay_is_w, 
   const dim3 grid(unsigned(nseg) * unsigned(rows)), block(W * 64);
   if (r != nullptr) {
     launch(wkv::wkv4_bwd_split_kernel<E, VEC, L, W, true>, grid, block, stream, false, g_, decay,
-           decay_is_w, u, k_, v_, r_, ck, gk_, gv_, gr_, gw_part, gu_part, lb, status, rows, T, C);
+           decay_is_w, u, k_, v_, r_, ck, gk_, gv_, gr_, gw_part, gu_part, lb, status, rows, T, C,
+           lb_poll_limit());
   } else {
     launch(wkv::wkv4_bwd_split_kernel<E, VEC, L, W, false>, grid, block, stream, false, g_, decay,
            decay_is_w, u, k_, v_, r_, ck, gk_, gv_, static_cast<raw*>(nullptr), gw_part, gu_part,
-           lb, status, rows, T, C);
+           lb, status, rows, T, C, lb_poll_limit());
   }
   if (int rc = check_launch("wkv4_bwd_split_kernel")) return rc;
   if (r != nullptr) {

@@ -390,7 +390,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_split_kernel(
     const float* __restrict__ decay, int decay_is_w, const float* __restrict__ time_first,
     const typename E::raw* __restrict__ r, typename E::raw* __restrict__ y,
     float* __restrict__ ck, uint64_t* __restrict__ lb, uint32_t* __restrict__ status, int rows,
-    int T, int C) {
+    int T, int C, int max_polls) {
   using F = Fwd<E, VEC, L, W, WY, GATE>;
   using PackT = typename F::PackT;
   __shared__ typename F::Smem sm;
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_split_kernel(
       float cp[VEC], cq[VEC];
       const uint64_t* base = lb + size_t(row) * F::CPW + lane * VEC;
       const bool gave_up = !lb_window_carry<VEC>(base, base + plane, size_t(rows) * F::CPW, seg,
-                                                 nseg, +1, DS, cp, cq);
+                                                 nseg, +1, DS, cp, cq, max_polls);
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
         lb_store(mine + plane + c, lb_pack(fmaf(cp[c], DS[c], ap[c]), fmaf(cq[c], DS[c], aq[c])));
@@ -631,13 +631,13 @@ static int launch_fwd_split(const void* k, const void* v, const float* decay, in
   const dim3 grid(unsigned(nseg) * unsigned(rows)), block(W * 64);
   if (r != nullptr) {
     launch(wkv::wkv4_fwd_split_kernel<E, VEC, L, W, true, true>, grid, block, stream, false, kk,
-           vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C);
+           vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C, lb_poll_limit());
   } else if (y != nullptr) {
     launch(wkv::wkv4_fwd_split_kernel<E, VEC, L, W, true, false>, grid, block, stream, false, kk,
-           vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C);
+           vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C, lb_poll_limit());
   } else {
     launch(wkv::wkv4_fwd_split_kernel<E, VEC, L, W, false, false>, grid, block, stream, false,
-           kk, vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C);
+           kk, vv, decay, decay_is_w, tf, rr, yy, ck, lb, status, rows, T, C, lb_poll_limit());
   }
   if (int rc = check_launch("wkv4_fwd_split_kernel")) return rc;
   if (r != nullptr) {

@@ -448,7 +448,8 @@ constexpr uint64_t kLbEmpty = ~uint64_t(0);
 constexpr uint64_t kLbNaN = (uint64_t(0x7fc00000u) << 32) | 0x7fc00000u;
 // Polls of one word before a workgroup gives up waiting (the row is then
 // recomputed by the exact path).  A published word arrives within
-// microseconds; the bound only guarantees that every wave ends.
+// microseconds; the bound only guarantees that every wave ends.  The kernels
+// take the bound as an argument (at most this).
 constexpr int kLbMaxPolls = 1 << 16;
 // Marker values of the per-row status words (filled with all ones).
 constexpr uint32_t kRowOk = ~uint32_t(0);
@@ -481,16 +482,18 @@ constexpr int kLbWindow = WKV_LB_WINDOW;
 // depend on when they were published, so the carry (and the kernel's result)
 // is the same on every run.  agg, incl: this lane's words of segment 0;
 // segment j's are seg_stride words further.  Returns false when a word did
-// not arrive within kLbMaxPolls polls.
+// not arrive within max_polls polls (at once, without reading, for
+// max_polls < 0).
 template <int VEC>
 __device__ __forceinline__ bool lb_window_carry(const uint64_t* agg, const uint64_t* incl,
                                                 size_t seg_stride, int s, int nseg, int dir,
                                                 const float (&DS)[VEC], float (&ca)[VEC],
-                                                float (&cb)[VEC]) {
+                                                float (&cb)[VEC], int max_polls) {
   constexpr int K = kLbWindow;
   uint64_t wa[K][VEC], wi[VEC];
   const int jo = s - dir * (K + 1);  // the inclusive word's segment
   const bool has_incl = jo >= 0 && jo < nseg;
+  if (max_polls < 0) return false;
   for (int polls = 0;; ++polls) {
     bool ready = true;
 #pragma unroll
@@ -511,7 +514,7 @@ __device__ __forceinline__ bool lb_window_carry(const uint64_t* agg, const uint6
       }
     }
     if (ready) break;
-    if (polls >= kLbMaxPolls) return false;
+    if (polls >= max_polls) return false;
     __builtin_amdgcn_s_sleep(1);
   }
 #pragma unroll

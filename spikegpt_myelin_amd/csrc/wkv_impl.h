@@ -31,6 +31,11 @@ constexpr int64_t kSplitRows = 256;
 constexpr int64_t kSplitMinSegs = 32;
 constexpr int64_t kSplitMinElems = int64_t(1) << 23;
 int split_mode();
+// Polls of one look-back word before a split workgroup gives up and leaves
+// its row to the fix-up kernel: kLbMaxPolls, or WKV_LB_MAX_POLLS from the
+// environment (-1 .. kLbMaxPolls; -1 gives up at once, so that a test can
+// send every row through the fix-up path).
+int lb_poll_limit();
 // Fills `bytes` (a multiple of 16) of look-back workspace with all ones.
 int lb_fill(void* ws, size_t bytes, hipStream_t stream);
 

@@ -433,6 +433,59 @@ def test_split_tile_configurations(fcfg, bcfg, monkeypatch):
         _close(g, r, rtol=2e-2, atol=1e-2, what=f"split {fcfg}/{bcfg} fix-up {name}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_split_look_back_give_up_takes_the_fix_up_path(dtype, monkeypatch):
+    # The split kernels' look-back waits are bounded; a workgroup that gives
+    # up marks its row, and the fix-up kernels recompute such rows with the
+    # exact running-max path.  WKV_LB_MAX_POLLS=-1 makes every workgroup give
+    # up at once (forced from the host; no wait is skipped), so every row
+    # goes through the fix-up: the results must still meet the bar against
+    # the fp64 oracle, and differ in bits from the fixed-frame results, which
+    # shows that the recomputation ran.
+    from spikegpt_myelin_amd import weighted_key_value_hip, weighted_key_value_hip_bf16io
+
+    fn = weighted_key_value_hip_bf16io if dtype != torch.float32 else weighted_key_value_hip
+    monkeypatch.setenv("WKV_SPLIT", "1")
+    print(f"split give-up {dtype}", flush=True)
+    k, v, td, tf, gy = O.make_inputs(3, 700, 192, seed=38, dtype=dtype)
+    xs = [x.to(DEV) for x in (k, v, td, tf, gy)]
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    normal = _grads(fn, *xs)
+    monkeypatch.setenv("WKV_LB_MAX_POLLS", "-1")
+    forced = _grads(fn, *xs)
+    names = ("y", "gk", "gv", "gtd", "gtf")
+    for got, r, name in zip(forced, ref, names):
+        tol = FP32_TOL if dtype == torch.float32 else _bf16_tol(name)
+        _close(got, r, what=f"split give-up {name}", **tol)
+    assert not all(torch.equal(a, b) for a, b in zip(forced, normal))
+
+
+def test_split_look_back_give_up_gated(monkeypatch):
+    # The same forced give-up through the gated pair (the model's time mix):
+    # its fix-up kernels also write grad_r.
+    from spikegpt_myelin_amd import weighted_key_value_gated
+
+    monkeypatch.setenv("WKV_SPLIT", "1")
+    k, v, td, tf, gy = O.make_inputs(2, 640, 128, seed=39, dtype=torch.float32)
+    r = torch.randn(2, 640, 128, generator=torch.Generator().manual_seed(40)) * 2
+    xs = [x.to(torch.bfloat16) for x in (k, v)] + [td, tf, r.to(torch.bfloat16)]
+
+    def run():
+        leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+        y = weighted_key_value_gated(*leaves)
+        return (y, *torch.autograd.grad(y, leaves, gy.to(torch.bfloat16).to(DEV)))
+
+    normal = run()
+    monkeypatch.setenv("WKV_LB_MAX_POLLS", "-1")
+    forced = run()
+    leaves = [x.double().requires_grad_(True) for x in xs]
+    y = torch.sigmoid(leaves[4]) * O.wkv_loop(*leaves[:4])
+    ref = (y, *torch.autograd.grad(y, leaves, gy.to(torch.bfloat16).double()))
+    for name, a, e in zip(("y", "gk", "gv", "gtd", "gtf", "gr"), forced, ref):
+        assert torch.allclose(a.detach().double().cpu(), e.detach(), rtol=2e-2, atol=1e-2), name
+    assert not all(torch.equal(a, b) for a, b in zip(forced, normal))
+
+
 def test_split_and_one_row_kernels_agree(monkeypatch):
     # The two decompositions of the long-context shape (4 of its 24 rows)
     # compute the same function: equal to fp32 rounding before the bf16
