@@ -9,7 +9,11 @@ The timed region issues that step through the C ABI on buffers allocated
 once (``wkv4_forward_checkpointed`` then ``wkv4_backward_checkpointed``, the
 two launches the autograd path makes), so the number is the kernels' own
 throughput; the same work through the torch.library op path (dispatch,
-allocation and autograd on every call) is reported as ``op_ms_per_step``.
+allocation and autograd on every call) is reported as ``op_ms_per_step``,
+and as ``op_ms_per_step_backward_on_calling_thread`` with the autograd
+engine's per-device worker threads switched off
+(``torch.autograd.set_multithreading_enabled(False)``), which removes the
+engine's hand-off of every backward to its device thread.
 
 Reported beside the throughput:
 * ``roofline`` -- the dominant kernel (the backward's reverse sweep,
@@ -232,14 +236,21 @@ def bench_wkv4(args, cfg) -> dict:
             else:
                 torch.autograd.grad(fwd_op(*leaves), leaves, dy)
 
-    for _ in range(args.warmup):
-        op_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        op_step()
-    torch.cuda.synchronize()
-    op_step_s = (time.perf_counter() - t0) / args.steps
+    def time_op_path():
+        for _ in range(args.warmup):
+            op_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            op_step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps
+
+    op_step_s = time_op_path()
+    # The same with the autograd engine running the backward on the calling
+    # thread (no hand-off to its per-device worker thread).
+    with torch.autograd.set_multithreading_enabled(False):
+        op_step_1t_s = time_op_path()
 
     dom_name = "fwd" if fwd_only else "bwd"
     # The dominant kernel: the reverse sweep of the backward (the forward for
@@ -319,6 +330,7 @@ def bench_wkv4(args, cfg) -> dict:
         "hbm_frac_of_peak": alg_step / step_s / 1e9 / HBM_PEAK_GBS,
         "op_ms_per_step": op_step_s * 1e3,
         "op_tokens_per_s": B * T / op_step_s,
+        "op_ms_per_step_backward_on_calling_thread": op_step_1t_s * 1e3,
         "fwd_launch_us": fwd_s * 1e6,
     }
     dom_t = statistics.mean(per[dom_name])
