@@ -481,9 +481,9 @@ constexpr int kLbWindow = WKV_LB_WINDOW;
 // agg_near, where DS is the decay over one segment.  The words read never
 // depend on when they were published, so the carry (and the kernel's result)
 // is the same on every run.  agg, incl: this lane's words of segment 0;
-// segment j's are seg_stride words further.  Returns false when a word did
-// not arrive within max_polls polls (at once, without reading, for
-// max_polls < 0).
+// segment j's are seg_stride words further.  Returns false, with a zero
+// carry, when a word did not arrive within max_polls polls (at once,
+// without reading, for max_polls < 0).
 template <int VEC>
 __device__ __forceinline__ bool lb_window_carry(const uint64_t* agg, const uint64_t* incl,
                                                 size_t seg_stride, int s, int nseg, int dir,
@@ -493,6 +493,8 @@ __device__ __forceinline__ bool lb_window_carry(const uint64_t* agg, const uint6
   uint64_t wa[K][VEC], wi[VEC];
   const int jo = s - dir * (K + 1);  // the inclusive word's segment
   const bool has_incl = jo >= 0 && jo < nseg;
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) { ca[c] = 0.f; cb[c] = 0.f; }
   if (max_polls < 0) return false;
   for (int polls = 0;; ++polls) {
     bool ready = true;
