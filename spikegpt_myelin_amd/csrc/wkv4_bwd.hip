@@ -168,6 +168,9 @@ struct Bwd {
   static constexpr int CPW = 64 * VEC;
   static constexpr int SEG = W * L;
   static constexpr int BPS = SEG / kCkptBlock;  // checkpoint blocks per segment
+  // The one-row kernel's (1, 8, 16) tile loads each segment when it starts
+  // instead of one segment ahead (see wkv4_bwd_kernel).
+  static constexpr bool kNoPrefetch = VEC == 1 && L == 8 && W == 16;
   static_assert(SEG % kCkptBlock == 0, "segment/block layout");
 
   struct Smem {
@@ -511,6 +514,24 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
     PackT xA[L], xB[L];  // receptance chunks (loaded and used only with GATE)
     typename F::Recs rA, rB;
     const int last = nseg - 1;
+    if constexpr (F::kNoPrefetch) {
+      // Sixteen waves of one channel per lane: no segment is fetched ahead
+      // (the second register buffer would not fit the 128 VGPRs that four
+      // waves per SIMD leave); the other waves on each SIMD cover the wait.
+      for (int seg = last; seg >= 0; --seg) {
+        F::load(k, v, gy, r, ck, ck_row, ck_boff, ck_field, seg, row_base, row_tail, lane_boff,
+                seg * F::SEG + wave * L, C, kA, vA, gA, xA, rA);
+        if (seg < nfull) {
+          F::template segment<true>(sm, seg, nseg, T, C, wave, lane, active, row_base, row_tail,
+                                    lane_boff, kA, vA, gA, xA, rA, D, DL, U, Wt, gk, gv, gr, gw,
+                                    gu);
+        } else {
+          F::template segment<false>(sm, seg, nseg, T, C, wave, lane, active, row_base, row_tail,
+                                     lane_boff, kA, vA, gA, xA, rA, D, DL, U, Wt, gk, gv, gr, gw,
+                                     gu);
+        }
+      }
+    } else {
     F::load(k, v, gy, r, ck, ck_row, ck_boff, ck_field, last, row_base, row_tail, lane_boff,
             last * F::SEG + wave * L, C, kA, vA, gA, xA, rA);
     // The next segment is prefetched on every path (segment 0 prefetches
@@ -538,6 +559,7 @@ __global__ __launch_bounds__(W * 64) void wkv4_bwd_kernel(
         F::template segment<false>(sm, seg - 1, nseg, T, C, wave, lane, active, row_base,
                                    row_tail, lane_boff, kB, vB, gB, xB, rB, D, DL, U, Wt, gk, gv, gr, gw, gu);
       }
+    }
     }
   }
 
@@ -883,9 +905,12 @@ namespace wkv_host {
 // Tile configurations compiled into the library (selectable with
 // WKV_BWD_CFG="vec,L,W" for measurement).  SEG = W*L must be a multiple of
 // the 64-step checkpoint block.  Defaults: (2,8,8) for 16-bit tensors with
-// enough rows of 128 channels to fill the chip, else (1,8,8) (fastest measured
-// for the few-row shapes, no spills); the W=16
-// configurations are capped at 128 VGPRs and spill.
+// enough rows of 128 channels to fill the chip; for one channel per lane,
+// (1,8,16) when at most one workgroup per CU exists (256 rows of 64
+// channels or fewer: four waves per SIMD without the segment prefetch,
+// 4-9 % faster than (1,8,8) at B=16 C=768 and B=24 T=3072), else (1,8,8)
+// (1 % faster at 512 rows).  The other W=16 configurations are capped at
+// 128 VGPRs and spill.
 static constexpr TileCfg kBwdCfgs[] = {{2, 8, 8}, {1, 8, 16}, {2, 4, 16}, {1, 16, 8}, {1, 8, 8},
                                         {1, 16, 4}, {2, 16, 4}};
 // Tile configurations of the split kernel (WKV_BWD_SPLIT_CFG).
@@ -899,7 +924,7 @@ static TileCfg pick_bwd_cfg(int64_t B, int64_t C, int elem_bytes) {
       if (c.vec == vec && c.L == L && c.W == W && (vec == 1 || C % 2 == 0)) return c;
   }
   if (elem_bytes == 2 && pick_vec(B, C) == 2) return TileCfg{2, 8, 8};
-  return TileCfg{1, 8, 8};
+  return B * ((C + 63) / 64) <= 256 ? TileCfg{1, 8, 16} : TileCfg{1, 8, 8};
 }
 
 // The split kernel runs on the same condition as the forward's (few rows,

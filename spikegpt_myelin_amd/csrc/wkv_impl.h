@@ -21,13 +21,16 @@ int pick_vec(int64_t B, int64_t C);
 bool env_cfg(const char* name, int& vec, int& L, int& W);
 
 // The split-over-time RWKV-4 kernels run for fewer than kSplitRows rows of 64
-// channels, at least kSplitMinSegs segments and kSplitMinElems elements: the
-// split kernels beat the one-row kernels, but their fill, fix-up and
-// batch-sum launches cost ~8-10 us per call, which only a long sequence
-// repays (measured: B=24 T=3072 C=512 157.8 against 163.6 us per fwd+bwd;
-// B=16 T=1024 C=768 61.3 against 60.7 us).  split_mode() is WKV_SPLIT from
-// the environment (0 off, 1 on, -1 unset: by these sizes).
-constexpr int64_t kSplitRows = 256;
+// channels, at least kSplitMinSegs segments and kSplitMinElems elements.
+// Measured fwd+bwd (MI355X, bf16, one-row backward on its 16-wave tile):
+// 96 rows or fewer the split wins by far (B=12 T=4096 C=512: 109 against
+// 193 us; B=4 T=8192: 98 against 376 us), at 192 rows the two are within
+// 2 % (B=24 T=3072 C=512: 149-154 against 151 us; B=16 T=1024 C=768 and
+// T=2048: one-row 3 % and 1 % faster) and at 256 rows the one-row kernels
+// win (116 against 135 us).  The split's fill, fix-up and batch-sum
+// launches cost ~8-10 us per call.  split_mode() is WKV_SPLIT from the
+// environment (0 off, 1 on, -1 unset: by these sizes).
+constexpr int64_t kSplitRows = 192;
 constexpr int64_t kSplitMinSegs = 32;
 constexpr int64_t kSplitMinElems = int64_t(1) << 23;
 int split_mode();
