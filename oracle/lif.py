@@ -32,6 +32,11 @@ Functions and what pins each one (``tests/test_oracle_lif.py``):
   inputs (two formulations; dropping the reset-path term or the decay carry
   fails it), and the surrogate derivative matches central differences of the
   smooth surrogate ``atan(pi/2 c)/pi + 1/2``.
+* :func:`lif_membranes` -- the forward replay in a chosen dtype.  Pinned at a
+  constructed exact float32 threshold tie (``h == fp32(theta)``): its float32
+  spikes equal :func:`lif_loop`'s, and :func:`lif_reverse` built on it equals
+  autograd through the float32 :func:`lif_loop`; a float64 replay of the same
+  float32 inputs misses that spike, which the test also asserts.
 """
 
 from __future__ import annotations
@@ -91,14 +96,18 @@ def lif_membranes(x: Tensor, tau: float = 2.0, threshold: float = 1.0, reset: fl
                   slope: float = 2.0, dtype: torch.dtype = torch.float64) -> tuple[Tensor, Tensor]:
     """Pre-spike membranes ``h`` and spikes ``s`` of the loop evaluated in
     ``dtype`` (float64 by default; float32 replays the kernels' arithmetic),
-    no autograd."""
+    no autograd.
+
+    Every step stays in ``dtype``: the spike is cast to ``dtype`` before the
+    reset line, so a float32 replay fires at exactly the steps where
+    :func:`lif_loop` fires in float32, exact threshold ties included."""
     x = x.to(dtype)
     decay = 1.0 - 1.0 / tau
     m = torch.zeros(x.shape[0], x.shape[2], dtype=x.dtype)
     hs, ss = [], []
     for t in range(x.shape[1]):
         h = m * decay + x[:, t]
-        s = (slope * (h - threshold) >= 0).double()
+        s = (slope * (h - threshold) >= 0).to(dtype)
         m = h * (1.0 - s) + reset * s
         hs.append(h)
         ss.append(s)

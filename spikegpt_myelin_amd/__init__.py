@@ -25,7 +25,7 @@ block-step kernels, optionally captured in a HIP graph) and
 from .decode import initial_wkv_state, wkv_decode_step
 from .language import validate_wkv_inputs, weighted_key_value
 from .gates import relu_square, sigmoid_gate
-from .lif import lif_sequence
+from .lif import atan_surrogate, lif_sequence
 from .splitk import split_k_sum
 from .timemix import token_shift_mix
 from .wkv import (
@@ -38,6 +38,7 @@ from .wkv import (
 from .wkv7 import wkv7_backward, wkv7_forward
 
 __all__ = [
+    "atan_surrogate",
     "initial_wkv_state",
     "lif_sequence",
     "relu_square",

@@ -146,13 +146,25 @@ def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def _need(t: Tensor | None, shape: tuple, name: str, dtype: torch.dtype = torch.float32) -> None:
-    """Raise unless ``t`` (if given) is a contiguous ``dtype`` tensor of ``shape``."""
+def _need(t: Tensor | None, shape: tuple, name: str, dtype: torch.dtype = torch.float32,
+          device: torch.device | None = None) -> None:
+    """Raise unless ``t`` (if given) is a contiguous ``dtype`` tensor of ``shape``
+    on ``device`` (when given).  The kernels receive raw addresses, so a host
+    tensor must be refused here rather than handed to the GPU."""
     if t is None:
         return
     if tuple(t.shape) != tuple(shape) or t.dtype != dtype or not t.is_contiguous():
         raise ValueError(f"{name}: expected a contiguous {dtype} tensor of shape "
                          f"{tuple(shape)}; got {t.dtype} {tuple(t.shape)}")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name}: expected a tensor on {device}; got one on {t.device}")
+
+
+def _gpu_device(t: Tensor, name: str) -> torch.device:
+    """The HIP device of ``t``; a host (or meta) tensor raises ValueError."""
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: the step kernels run on a HIP GPU; got a tensor on {t.device}")
+    return t.device
 
 
 def _row(pre: int, *, residual: Tensor, stream: int, ln: torch.nn.LayerNorm | None = None,
@@ -164,25 +176,30 @@ def _row(pre: int, *, residual: Tensor, stream: int, ln: torch.nn.LayerNorm | No
          mem_out: Tensor | None = None, lif=None) -> None:
     a = _lib.StepRowArgs()
     B, C = residual.shape
+    dev = residual.device
     # Every tensor is handed to the kernel as a raw pointer: check that each
-    # one has the [B, C] row shape (or [C] / [vocab, C]) the kernel indexes.
+    # one has the [B, C] row shape (or [C] / [vocab, C]) the kernel indexes,
+    # on the residual's device, and (below) that this device is a GPU.
     for name, t in (("prev_in", prev_in), ("prev_out", prev_out), ("add", add), ("gate", gate),
                     ("mem_in", mem_in), ("mem_out", mem_out)):
-        _need(t, (B, C), name)
+        _need(t, (B, C), name, device=dev)
     for j, o in enumerate(outs):
-        _need(o, (B, C), f"out[{j}]")
+        _need(o, (B, C), f"out[{j}]", device=dev)
     for mod, name in ((ln, "ln"), (ln0, "ln0")):
         if mod is not None:
-            _need(mod.weight, (C,), f"{name}.weight")
-            _need(mod.bias, (C,), f"{name}.bias")
+            _need(mod.weight, (C,), f"{name}.weight", device=dev)
+            _need(mod.bias, (C,), f"{name}.bias", device=dev)
     for j, m in enumerate(mix):
         if m.numel() != C or m.dtype != torch.float32:
             raise ValueError(f"mixing vector {j} has {m.numel()} elements; the row has {C}")
+        if m.device != dev:
+            raise ValueError(f"mixing vector {j}: expected a tensor on {dev}; got one on {m.device}")
     if ids is not None:
-        _need(ids, (B,), "ids", torch.int64)
+        _need(ids, (B,), "ids", torch.int64, device=dev)
         if embedding is None or embedding.ndim != 2 or embedding.shape[1] != C:
             raise ValueError(f"embedding must be [vocab, {C}]")
-        _need(embedding, tuple(embedding.shape), "embedding")
+        _need(embedding, tuple(embedding.shape), "embedding", device=dev)
+    _gpu_device(residual, "residual")
     a.batch, a.channels = B, C
     a.residual = residual.data_ptr()
     if ids is not None:
@@ -317,9 +334,11 @@ def model_step(model: "SpikeLanguageModel", ids: Tensor, src: Tensor, dst: Tenso
                ws: StepWorkspace) -> Tensor:
     """Advance every layer by one token: reads state ``src``, writes ``dst``
     (may be the same tensor), returns ``ws.logits`` [B, vocab]."""
-    stream = torch.cuda.current_stream(ids.device).cuda_stream
     cfg = model.config
     _check_workspace(model, ws, ids.shape[0], src, dst)
+    dev = _gpu_device(model.embedding.weight, "model parameters")
+    _need(ids, (ids.shape[0],), "ids", torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
     blocks = list(model.blocks)
     L = len(blocks)
     first = blocks[0]
@@ -349,13 +368,16 @@ def block_step(block: "SpikeGPTBlock", inputs: Tensor, src: Tensor, dst: Tensor,
                ws: StepWorkspace) -> Tensor:
     """One block's step on its input ``inputs`` [B, C]; state slot rows
     ``src``/``dst`` [7, B, C]; returns the new residual (``ws.residual``)."""
-    stream = torch.cuda.current_stream(inputs.device).cuda_stream
     B, C = inputs.shape
     if ws.dims[:3] != (B, C, block.ffn.key.out_features):
         raise ValueError(f"step workspace sized for (B, C, hidden) = {ws.dims[:3]}; the block "
                          f"and batch need {(B, C, block.ffn.key.out_features)}")
-    _need(src, (len(SLOTS), B, C), "state src")
-    _need(dst, (len(SLOTS), B, C), "state dst")
+    dev = _gpu_device(block.att.time_decay, "block parameters")
+    _need(inputs, (B, C), "inputs", device=dev)
+    _need(src, (len(SLOTS), B, C), "state src", device=dev)
+    _need(dst, (len(SLOTS), B, C), "state dst", device=dev)
+    _need(ws.residual, (B, C), "workspace", device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
     ws.residual.copy_(inputs)
     _row(PRE_NONE, residual=ws.residual, stream=stream, ln0=block.ln0, ln=block.ln1,
          mix=_mixes(block.att), prev_in=src[_TPREV], prev_out=dst[_TPREV],
@@ -381,8 +403,10 @@ def _check_workspace(model: "SpikeLanguageModel", ws: StepWorkspace, batch: int,
         raise ValueError(f"step workspace sized for (B, C, hidden, vocab) = {ws.dims}; "
                          f"the model and batch need {dims}")
     want = (model.config.n_layer, len(SLOTS), batch, model.config.n_embd)
+    dev = model.embedding.weight.device
     for name, t in (("src", src), ("dst", dst)):
-        _need(t, want, f"state {name}")
+        _need(t, want, f"state {name}", device=dev)
+    _need(ws.residual, (batch, model.config.n_embd), "step workspace", device=dev)
 
 
 # Step workspaces per live model (weak keys: a workspace never outlives its

@@ -26,6 +26,8 @@ depend on it; input gradients do.
 
 from __future__ import annotations
 
+import math
+
 import torch
 from torch import Tensor
 
@@ -137,6 +139,32 @@ def _backward(ctx, grad_spikes, _grad_ck):
 
 
 _lif_forward.register_autograd(_backward, setup_context=_setup_context)
+
+
+def atan_surrogate(x: Tensor) -> Tensor:
+    """The smooth arctan spike ``atan(pi/2 * x) / pi + 1/2`` (``x`` already
+    scaled by the slope).  Its derivative ``0.5 / (1 + (pi/2 * x)^2)`` is the
+    surrogate gradient the LIF kernels apply.  It stands in for the default
+    ``surrogate`` of ``SpikingSequenceLIF`` (``language.py:775``), which the
+    external ``myelin`` package defines under the same name."""
+    return torch.atan((math.pi / 2.0) * x) / math.pi + 0.5
+
+
+def serves_surrogate(surrogate, hard_forward: bool = True) -> bool:
+    """True when the LIF kernels compute what ``SpikingSequenceLIF`` with this
+    ``surrogate`` and ``hard_forward`` computes: a Heaviside forward
+    (``hard_forward=True``, ``language.py:835-836``) with the arctan
+    surrogate's derivative.  The arctan surrogate is this module's
+    :func:`atan_surrogate` or ``myelin``'s function of that name (recognised
+    by module and name; ``myelin`` is not imported).  Any other surrogate, or
+    the smooth forward ``spike = surrogate(c)`` (``:838``), is not served."""
+    if not hard_forward:
+        return False
+    if surrogate is atan_surrogate:
+        return True
+    module = getattr(surrogate, "__module__", None) or ""
+    return module.split(".")[0] == "myelin" and getattr(surrogate, "__name__", "") == \
+        "atan_surrogate"
 
 
 def lif_sequence(

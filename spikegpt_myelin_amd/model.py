@@ -34,7 +34,7 @@ from .gates import relu_square, sigmoid_gate
 from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguageModelState,
                          SpikeTimeMixState, SpikingSequenceLIFState, StepWorkspace, block_step,
                          initial_packed, pack_state, state_from_packed)
-from .lif import lif_residual, lif_sequence
+from .lif import atan_surrogate, lif_residual, lif_sequence, serves_surrogate
 from .splitk import split_k_sum
 from .timemix import layer_norm_shift_mix, layer_norm_shift_mix_fork, token_shift_mix
 from .wkv import weighted_key_value_gated
@@ -151,17 +151,39 @@ class SplitKLinear(nn.Linear):
 
 
 class SpikingSequenceLIF(nn.Module):
-    """``language.py:766-918``: LIF over ``[B, T, C]`` in one HIP kernel."""
+    """``language.py:766-918``: LIF over ``[B, T, C]`` in one HIP kernel.
+
+    The constructor takes the reference's arguments (``:769-781``).  What the
+    kernels compute is the reference's fused path for the arctan surrogate
+    with a Heaviside forward; ``fused`` and ``recompute`` are accepted and
+    change nothing in the values: the reference's per-step loop (``fused=False``)
+    performs the same float32 operations in the same order as the kernels,
+    and the kernels always recompute inside 32-step blocks from membrane
+    records (the reference's ``recompute`` trades memory the same way).  A
+    surrogate other than the arctan one, or ``hard_forward=False`` (a smooth
+    forward ``spike = surrogate(c)``), raises ``NotImplementedError`` here,
+    so such a module never reaches the kernels."""
 
     def __init__(self, *, tau: float = 2.0, threshold: float = 1.0, reset: float = 0.0,
-                 surrogate_slope: float = 2.0) -> None:
+                 surrogate=atan_surrogate, surrogate_slope: float = 2.0,
+                 hard_forward: bool = True, fused: bool = True, recompute: bool = False) -> None:
         super().__init__()
         if tau <= 0.0:
             raise ValueError("tau must be positive")
+        if not serves_surrogate(surrogate, hard_forward):
+            what = ("hard_forward=False (smooth forward spikes)" if not hard_forward
+                    else f"surrogate {getattr(surrogate, '__name__', surrogate)!r}")
+            raise NotImplementedError(
+                f"SpikingSequenceLIF: the HIP LIF kernels serve the arctan surrogate with "
+                f"hard_forward=True; {what} is not served")
         self.tau = tau
         self.threshold = threshold
         self.reset = reset
+        self.surrogate = surrogate
         self.surrogate_slope = surrogate_slope
+        self.hard_forward = hard_forward
+        self.fused = fused
+        self.recompute = recompute
 
     @property
     def decay(self) -> float:

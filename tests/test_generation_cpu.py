@@ -79,3 +79,28 @@ def test_gradient_checkpointing_flag():
     assert m.gradient_checkpointing is False
     m.set_gradient_checkpointing()
     assert m.gradient_checkpointing is True
+
+
+def test_tensors_off_the_gpu_are_rejected_before_launch():
+    # The step kernels take raw addresses: a host tensor (or one on another
+    # device than the model) must raise ValueError, never reach a kernel.
+    cuda0 = torch.device("cuda", 0)
+    with pytest.raises(ValueError, match="expected a tensor on cuda:0"):
+        G._need(torch.zeros(2, 3), (2, 3), "state src", device=cuda0)
+    residual = torch.zeros(2, 32)
+    with pytest.raises(ValueError, match="HIP GPU"):
+        G._row(G.PRE_NONE, residual=residual, stream=0, outs=(torch.zeros(2, 32),))
+    with pytest.raises(ValueError, match="prev_in: expected a tensor on"):
+        G._row(G.PRE_NONE, residual=residual, stream=0,
+               prev_in=torch.zeros(2, 32, device="meta"))
+    m = _model(32)
+    ws = G.StepWorkspace(*G._model_dims(m, 2), CPU)
+    src = torch.zeros(2, len(G.SLOTS), 2, 32)
+    with pytest.raises(ValueError, match="state dst: expected a tensor on cpu"):
+        G._check_workspace(m, ws, 2, src, src.to("meta"))
+    ids = torch.zeros(2, dtype=torch.int64)
+    with pytest.raises(ValueError, match="HIP GPU"):
+        G.model_step(m, ids, src, src, ws)
+    with pytest.raises(ValueError, match="HIP GPU"):
+        G.block_step(m.blocks[0], torch.zeros(2, 32), src[0], src[0],
+                     G.StepWorkspace(*G._model_dims(m, 2), CPU))

@@ -348,3 +348,39 @@ def test_216m_activation_shape_with_the_default_split():
     (gxr,) = torch.autograd.grad(out, xd, gout.to(DEV))
     _check_grad(gxr, L.lif_reverse(x.float(), gout, forward_dtype=torch.float32),
                 torch.bfloat16, "residual grad_x 216M shape")
+
+
+# Exact float32 threshold ties: the pre-spike membrane equals fp32(threshold),
+# so h - threshold == 0 and the step fires (language.py:834-836).  The kernels
+# must fire there as the float32 loop does, and their gradients must follow
+# the float32 spike pattern on every step after the tie.
+TIE_CASES = {
+    # B=64 T=1024 C=512 fp32, tau 2, threshold 1.3, slope 1.5, with x = 1.3
+    # planted every seventh step (after a reset, h = x exactly).
+    "fp32_full_size": dict(shape=(64, 1024, 512), dtype=torch.float32, tau=2.0, threshold=1.3,
+                           slope=1.5, scale=1.5, plant=1.3),
+    # B=64 T=33 C=256 bf16, tau 3, threshold 1, slope 1.5: 1.0 is a bf16 value,
+    # so after a reset the membrane hits the threshold exactly wherever x = 1.
+    "bf16_short": dict(shape=(64, 33, 256), dtype=torch.bfloat16, tau=3.0, threshold=1.0,
+                       slope=1.5, scale=1.5, plant=1.0),
+}
+
+
+@pytest.mark.parametrize("case", list(TIE_CASES))
+def test_exact_threshold_ties(case):
+    p = TIE_CASES[case]
+    b, t, c = p["shape"]
+    dtype = p["dtype"]
+    print(f"lif ties {case}", flush=True)
+    x, gs = _inputs(b, t, c, dtype, seed=31, scale=p["scale"])
+    x[:, 3::7] = p["plant"]
+    h, s_ref = L.lif_membranes(x.float(), p["tau"], p["threshold"], 0.0, p["slope"],
+                               dtype=torch.float32)
+    thr32 = float(torch.tensor(p["threshold"], dtype=torch.float32))
+    ties = int((h == thr32).sum())
+    assert ties > 0, "the inputs must hold exact ties"
+    spikes, gx = _run(x, gs, tau=p["tau"], threshold=p["threshold"], reset=0.0, slope=p["slope"])
+    assert torch.equal(spikes.float(), s_ref), f"spikes differ ({ties} ties)"
+    ref = L.lif_reverse(x.float(), gs.float(), p["tau"], p["threshold"], 0.0, p["slope"],
+                        forward_dtype=torch.float32)
+    _check_grad(gx, ref, dtype, f"grad_x at {ties} exact ties")

@@ -62,3 +62,43 @@ def test_ops_refuse_cpu_tensors():
 def test_reference_api_names_are_exported():
     assert m.weighted_key_value_triton is m.weighted_key_value_hip
     assert m.weighted_key_value_triton_bf16io is m.weighted_key_value_hip_bf16io
+
+
+def test_lif_module_takes_the_reference_options_and_refuses_what_it_cannot_serve():
+    # SpikingSequenceLIF(tau, threshold, reset, surrogate, surrogate_slope,
+    # hard_forward, fused, recompute) -- language.py:769-781.  The kernels
+    # serve the arctan surrogate with a Heaviside forward; fused/recompute do
+    # not change the values.  Anything else is refused at construction, so it
+    # can never reach the kernels.
+    import math
+    import types
+
+    from spikegpt_myelin_amd import atan_surrogate
+    from spikegpt_myelin_amd.model import SpikingSequenceLIF
+
+    for kw in (dict(), dict(fused=False), dict(recompute=True), dict(surrogate=atan_surrogate)):
+        m = SpikingSequenceLIF(**kw)
+        assert m.hard_forward is True and m.surrogate is atan_surrogate
+    with pytest.raises(NotImplementedError, match="surrogate"):
+        SpikingSequenceLIF(surrogate=lambda c: torch.sigmoid(4.0 * c))
+    with pytest.raises(NotImplementedError, match="hard_forward=False"):
+        SpikingSequenceLIF(hard_forward=False)
+    # myelin's own arctan surrogate is recognised by module and name.
+    fake = types.FunctionType(atan_surrogate.__code__, atan_surrogate.__globals__,
+                              "atan_surrogate")
+    fake.__module__ = "myelin.surrogates"
+    assert SpikingSequenceLIF(surrogate=fake).surrogate is fake
+    other = types.FunctionType(atan_surrogate.__code__, atan_surrogate.__globals__,
+                               "sigmoid_surrogate")
+    other.__module__ = "myelin.surrogates"
+    with pytest.raises(NotImplementedError):
+        SpikingSequenceLIF(surrogate=other)
+    # The surrogate's derivative is the one the kernels apply (the oracle's).
+    from oracle import lif as L
+
+    c = torch.linspace(-3, 3, 61, dtype=torch.float64).requires_grad_(True)
+    (d,) = torch.autograd.grad(atan_surrogate(c).sum(), c)
+    assert torch.allclose(d, L.surrogate_grad(c.detach()), rtol=1e-12, atol=1e-14)
+    assert float(atan_surrogate(torch.tensor(0.0))) == 0.5
+    assert math.isclose(float(atan_surrogate(torch.tensor(1e9, dtype=torch.float64))), 1.0,
+                        abs_tol=1e-9)

@@ -85,3 +85,51 @@ def test_dropping_the_reset_term_is_detected():
         wrong[:, t] = dh
         gm = 0.5 * dh
     assert not torch.allclose(gx, wrong, rtol=1e-6, atol=1e-6)
+
+
+def _tie_inputs():
+    # x = [0, fp32(1.3), 0, 0] with tau 2, threshold 1.3: at t = 1 the float32
+    # membrane is exactly fp32(1.3), so h - threshold == 0 in float32 and the
+    # step fires (language.py:833-839 evaluated in float32).
+    x = torch.tensor([0.0, 1.3, 0.0, 0.0], dtype=torch.float32).view(1, 4, 1)
+    return x, dict(tau=2.0, threshold=1.3, reset=0.0, slope=1.5)
+
+
+def test_float32_replay_fires_at_an_exact_threshold_tie():
+    x, kw = _tie_inputs()
+    s_loop = L.lif_loop(x, **kw)
+    assert s_loop[0, :, 0].tolist() == [0.0, 1.0, 0.0, 0.0]
+    h, s = L.lif_membranes(x, **kw, dtype=torch.float32)
+    assert h.dtype == torch.float32 and s.dtype == torch.float32
+    assert torch.equal(s, s_loop)
+    assert float(h[0, 1, 0]) == float(torch.tensor(1.3, dtype=torch.float32))
+    # The same float32 inputs replayed in float64 sit just below 1.3 and miss
+    # the spike: the replay's dtype matters exactly at such ties.
+    _, s64 = L.lif_membranes(x, **kw, dtype=torch.float64)
+    assert s64[0, :, 0].tolist() == [0.0, 0.0, 0.0, 0.0]
+
+
+def test_float32_reverse_equals_autograd_through_the_float32_loop_at_a_tie():
+    x, kw = _tie_inputs()
+    g = torch.Generator().manual_seed(5)
+    gs = torch.randn(1, 4, 1, generator=g, dtype=torch.float32)
+    xr = x.clone().requires_grad_(True)
+    (gx,) = torch.autograd.grad(L.lif_loop(xr, **kw), xr, gs)
+    ref = L.lif_reverse(x, gs, **kw, forward_dtype=torch.float32)
+    assert torch.allclose(gx.double(), ref, rtol=1e-6, atol=1e-6)
+    # A float64 replay (spike missed) gives a different gradient.
+    wrong = L.lif_reverse(x, gs, **kw, forward_dtype=torch.float64)
+    assert not torch.allclose(gx.double(), wrong, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype,tau,thr", [(torch.float32, 2.0, 1.3), (torch.bfloat16, 3.0, 1.0)])
+def test_float32_replay_spikes_equal_the_loop_on_tie_rich_inputs(dtype, tau, thr):
+    # bf16 inputs put exact ties everywhere (after a reset h = x, and 1.0 is a
+    # bf16 value); the float32 replay must reproduce every spike of the loop.
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8, 33, 64, generator=g).to(dtype)
+    if dtype == torch.float32:
+        x[:, ::5] = thr  # plant exact fp32 ties after resets
+    s_loop = L.lif_loop(x, tau=tau, threshold=thr, slope=1.5).float()
+    _, s = L.lif_membranes(x.float(), tau=tau, threshold=thr, slope=1.5, dtype=torch.float32)
+    assert torch.equal(s, s_loop)
