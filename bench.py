@@ -800,6 +800,113 @@ def bench_lif(args) -> dict:
     return out
 
 
+def bench_gated(args) -> dict:
+    """The time mix's WKV with its receptance gate, ``sigmoid(r) * wkv``
+    (src/spikegpt/language.py:1028-1035), forward + backward at B=64,
+    T=1024, C=512 bf16, two ways through the C ABI on preallocated buffers,
+    timed back to back in one process:
+    * fused: ``wkv4_forward_gated_checkpointed`` then
+      ``wkv4_backward_gated_checkpointed`` (the gate inside the WKV kernels);
+    * unfused: ``wkv4_forward_checkpointed``, ``sigmoid_gate_forward``, then
+      ``sigmoid_gate_backward`` and ``wkv4_backward_checkpointed``.
+    Both give the same values bit for bit (tests/test_gpu_wkv4_gated.py).
+    ``value`` is the variant the model uses (``config.model_uses``)."""
+    import spikegpt_myelin_amd  # noqa: F401
+    from spikegpt_myelin_amd import _lib
+    from spikegpt_myelin_amd.wkv import GATED_TIME_MIX, checkpoint_shape
+    from oracle import wkv4 as O
+
+    B, T, C = 64, 1024, 512
+    dt = torch.bfloat16
+    dev = torch.device("cuda", 0)
+    k, v, td, tf, dy = (x.to(dev) for x in O.make_inputs(B, T, C, seed=1, dtype=dt))
+    r = (torch.randn(B, T, C, generator=torch.Generator().manual_seed(9)) * 2).to(dt).to(dev)
+    lib = _lib.load()
+    code = _lib.dtype_code(dt)
+    y, out = torch.empty_like(k), torch.empty_like(k)
+    ck = torch.empty(checkpoint_shape(B, T, C), dtype=torch.float32, device=dev)
+    gk, gv, gr, gy = (torch.empty_like(k) for _ in range(4))
+    gtd = torch.empty(C, dtype=torch.float32, device=dev)
+    gtf = torch.empty_like(gtd)
+    fws_bytes = int(lib.wkv4_forward_workspace_bytes(B, T, C))
+    fws = torch.empty(max(fws_bytes, 16), dtype=torch.uint8, device=dev)
+    bws_bytes = int(lib.wkv4_backward_checkpointed_workspace_bytes(B, T, C))
+    ws = torch.empty(bws_bytes, dtype=torch.uint8, device=dev)
+    fwp = fws.data_ptr() if fws_bytes else None
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    n = B * T * C
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def fused_fwd():
+        _lib.check(lib.wkv4_forward_gated_checkpointed(P(k), P(v), P(td), P(tf), P(r), P(out),
+                                                       P(ck), fwp, fws_bytes, B, T, C, code, sp),
+                   "gated forward")
+
+    def fused_bwd():
+        _lib.check(lib.wkv4_backward_gated_checkpointed(
+            P(dy), P(td), P(tf), P(k), P(v), P(r), P(ck), P(gk), P(gv), P(gr), P(gtd), P(gtf),
+            P(ws), bws_bytes, B, T, C, code, sp), "gated backward")
+
+    def plain_fwd():
+        _lib.check(lib.wkv4_forward_checkpointed(P(k), P(v), P(td), P(tf), P(y), P(ck), fwp,
+                                                 fws_bytes, B, T, C, code, sp), "forward")
+        _lib.check(lib.sigmoid_gate_forward(P(r), P(y), P(out), n, code, sp), "gate forward")
+
+    def plain_bwd():
+        _lib.check(lib.sigmoid_gate_backward(P(dy), P(r), P(y), P(gr), P(gy), n, code, sp),
+                   "gate backward")
+        _lib.check(lib.wkv4_backward_checkpointed(P(gy), P(td), P(tf), P(k), P(v), P(ck), P(gk),
+                                                  P(gv), P(gtd), P(gtf), P(ws), bws_bytes,
+                                                  B, T, C, code, sp), "backward")
+
+    variants = {"fused": (fused_fwd, fused_bwd), "unfused": (plain_fwd, plain_bwd)}
+
+    def region(fwd, bwd) -> float:
+        for _ in range(args.warmup):
+            fwd()
+            bwd()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fwd()
+            bwd()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps
+
+    res = {}
+    for name, (fwd, bwd) in variants.items():
+        res[name] = region(fwd, bwd)
+    # the same again in the opposite order (box drift shows as a difference)
+    for name, (fwd, bwd) in reversed(list(variants.items())):
+        res[name] = min(res[name], region(fwd, bwd))
+    uses = "fused" if GATED_TIME_MIX else "unfused"
+    step_s = res[uses]
+    # Algorithmic bytes per element: fused fwd k, v, r read, out written (8);
+    # fused bwd k, v, r, dy read, dk, dv, dr written (14).  The unfused pair
+    # also writes and reads the WKV output y and its gradient (12 + 20).
+    fused_bytes, unfused_bytes = 22 * n, 32 * n
+    return {
+        "metric": "WKV fwd+bwd with the receptance gate sigmoid(r)*wkv, tokens/sec, "
+                  "B=64 T=1024 C=512 bf16",
+        "value": B * T / step_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": step_s * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "wkv4_gated_fwd_bwd", "B": B, "T": T, "C": C,
+                   "io_dtype": "bfloat16", "model_uses": uses},
+        "fused_ms_per_step": res["fused"] * 1e3,
+        "unfused_ms_per_step": res["unfused"] * 1e3,
+        "fused_hbm_gbps_algorithmic": fused_bytes / res["fused"] / 1e9,
+        "unfused_hbm_gbps_algorithmic": unfused_bytes / res["unfused"] / 1e9,
+        "roofline": {"bound": "hbm", "achieved": (fused_bytes if uses == "fused" else
+                                                  unfused_bytes) / step_s / 1e9,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": (fused_bytes if uses == "fused" else unfused_bytes) / step_s / 1e9
+                     / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": f"{uses} pair, whole step (region time)"},
+    }
+
+
 def bench_timemix(args) -> dict:
     """Fused token-shift mix of the time-mix block (three mixing vectors,
     fp32 input, bf16 outputs) forward + backward through the C ABI on
@@ -959,7 +1066,7 @@ def main() -> int:
     ap.add_argument("--event-every", type=int, default=10,
                     help="time the dominant launch with HIP events on every N-th timed step")
     ap.add_argument("--workload", default="wkv4", choices=[*WORKLOADS, "decode", "block_decode", "wkv7", "lif",
-                             "timemix", "e2e41m", "e2e216m"])
+                             "timemix", "gated", "e2e41m", "e2e216m"])
     ap.add_argument("--cpu-sample-batch", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--e2e-steps", type=int, default=20,
@@ -995,6 +1102,8 @@ def main() -> int:
         out = bench_lif(args)
     elif args.workload == "timemix":
         out = bench_timemix(args)
+    elif args.workload == "gated":
+        out = bench_gated(args)
     elif args.workload in ("e2e41m", "e2e216m"):
         out = bench_e2e(args.steps, args.warmup, args.workload[3:])
     else:

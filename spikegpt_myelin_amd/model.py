@@ -37,7 +37,8 @@ from .generation import (SpikeChannelMixState, SpikeGPTBlockState, SpikeLanguage
 from .lif import atan_surrogate, lif_residual, lif_sequence, serves_surrogate
 from .splitk import split_k_sum
 from .timemix import layer_norm_shift_mix, layer_norm_shift_mix_fork, token_shift_mix
-from .wkv import weighted_key_value_gated
+from .language import weighted_key_value
+from .wkv import GATED_TIME_MIX, weighted_key_value_gated
 
 
 @dataclass
@@ -246,9 +247,14 @@ class SpikeTimeMix(nn.Module):
         """Everything after the token-shift mixes (``language.py:1019-1036``)."""
         key = self.key(k_in)
         value = self.value(v_in)
-        # sigmoid(r) * wkv with the gate folded into the WKV kernels.
-        gated = weighted_key_value_gated(key, value, self.time_decay, self.time_first,
-                                         self.receptance(r_in))
+        receptance = self.receptance(r_in)
+        if GATED_TIME_MIX:
+            # sigmoid(r) * wkv with the gate folded into the WKV kernels.
+            gated = weighted_key_value_gated(key, value, self.time_decay, self.time_first,
+                                             receptance)
+        else:
+            gated = sigmoid_gate(receptance, weighted_key_value(key, value, self.time_decay,
+                                                                self.time_first))
         return self.output(gated)
 
 

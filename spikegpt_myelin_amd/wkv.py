@@ -369,6 +369,14 @@ class _Wkv4GatedTrainFn(torch.autograd.Function):
         return gk, gv, gtd.to(time_decay.dtype), gtf.to(time_first.dtype), gr
 
 
+# Whether the model's time mix runs sigmoid(r) * wkv through the fused gated
+# kernel pair (True) or through the WKV ops followed by the separate
+# sigmoid_gate kernels (False).  Both give the same values bit for bit; the
+# choice is the faster of the two in a same-box measurement at B=64, T=1024,
+# C=512 bf16 (bench.py --workload gated).
+GATED_TIME_MIX = True
+
+
 def weighted_key_value_gated(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor,
                              receptance: Tensor) -> Tensor:
     """``sigmoid(receptance) * weighted_key_value(key, value, ...)`` (the time
