@@ -11,7 +11,8 @@
 // sigmoid(r) to the element type first and then the product, as the two eager
 // bf16 kernels do.  Backward:
 //   squared ReLU: gx = g * 2 max(x, 0);
-//   gate:         gx = g * s,  gr = g * x * s (1 - s),  s = sigmoid(r) (fp32).
+//   gate:         gx = g * s,  gr = g * x * s (1 - s),  s = sigmoid(r) (fp32,
+//                 gate_sigmoid: the short form for the 16-bit types).
 // One pass each, 16-byte loads and stores per lane (8 bf16 or 4 fp32); the
 // eager forms take two to four passes plus fp32 temporaries.
 #include "wkv_common.h"
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void sigmoid_gate_fwd_kernel(const u32x4* __re
   unpack16<E>(__builtin_nontemporal_load(r + i), fr);
   unpack16<E>(__builtin_nontemporal_load(x + i), fx);
 #pragma unroll
-  for (int j = 0; j < N; ++j) fr[j] = round_to<E>(sigmoid_ref(fr[j])) * fx[j];
+  for (int j = 0; j < N; ++j) fr[j] = round_to<E>(gate_sigmoid<E>(fr[j])) * fx[j];
   __builtin_nontemporal_store(pack16<E>(fr), y + i);
 }
 
@@ -113,10 +114,9 @@ __global__ __launch_bounds__(256) void sigmoid_gate_bwd_kernel(const u32x4* __re
   unpack16<E>(__builtin_nontemporal_load(g + i), fg);
 #pragma unroll
   for (int j = 0; j < N; ++j) {
-    const float s = sigmoid_ref(fr[j]);
-    const float a = fg[j] * s;
-    fr[j] = a * fx[j] * (1.f - s);
-    fx[j] = a;
+    float grad_r;
+    fx[j] = gate_backward<E>(fg[j], gate_sigmoid<E>(fr[j]), fx[j], grad_r);
+    fr[j] = grad_r;
   }
   __builtin_nontemporal_store(pack16<E>(fr), gr + i);
   __builtin_nontemporal_store(pack16<E>(fx), gx + i);

@@ -131,10 +131,10 @@ __device__ void wkv4_bwd_channel_serial(const typename E::raw* __restrict__ gy,
           const float vv = load_scalar<E>(v + idx);
           float g = load_scalar<E>(gy + idx);
           if (r != nullptr) {
-            const float sg = sigmoid_ref(load_scalar<E>(r + idx));
-            const float a = g * sg;
-            store_scalar<E>(gr + idx, a * round_to<E>(ys[i]) * (1.f - sg));
-            g = round_to<E>(a);
+            float grad_r;
+            g = gate_backward<E>(g, gate_sigmoid<E>(load_scalar<E>(r + idx)), round_to<E>(ys[i]),
+                                 grad_r);
+            store_scalar<E>(gr + idx, grad_r);
           }
           const float zr = g * rs[i];
           const float ze = zr * fast_exp2(u2 + kk - nfs[i]);
@@ -279,13 +279,10 @@ struct Bwd {
         const float y = fmaf(e1, vv, P[c]) * r;
         float gyv = gb[i].get(c);
         if constexpr (GATE) {
-          // The gate's backward with the separate kernels' roundings: its
-          // input gradient round(g s) feeds the recurrence, and
-          // grad_r = g s y (1 - s) with y rounded as the forward stored it.
-          const float sg = sigmoid_ref(rb[i].get(c));
-          const float a = gyv * sg;
-          grv[c] = a * round_to<E>(y) * (1.f - sg);
-          gyv = round_to<E>(a);
+          // The gate's backward as the separate kernels compute it: its
+          // input gradient round(g s) feeds the recurrence, and grad_r
+          // comes from round(g y) with y rounded as the forward stored it.
+          gyv = gate_backward<E>(gyv, gate_sigmoid<E>(rb[i].get(c)), round_to<E>(y), grv[c]);
         }
         const float z = gyv * r;
         zz[i][c] = FULL || valid ? z : 0.f;

@@ -74,7 +74,8 @@ struct Fwd {
   // Loads the chunk of L steps starting at t0 through buffer descriptors
   // based at the chunk (row_base is wave-uniform, lane_boff the lane's byte
   // offset).  Steps at or past T read as zero.
-  // GATE: the receptance chunk rb as well.
+  // WITH_R: the receptance chunk rb as well (GATE).
+  template <bool WITH_R = GATE>
   __device__ static __forceinline__ void load_chunk(const raw* __restrict__ k,
                                                     const raw* __restrict__ v,
                                                     const raw* __restrict__ r, size_t row_base,
@@ -91,11 +92,18 @@ struct Fwd {
       load_buf(kb[i], rk, lane_boff, unsigned(i) * stride);
       load_buf(vb[i], rv, lane_boff, unsigned(i) * stride);
     }
-    if constexpr (GATE) {
-      const rsrc_t rr = make_rsrc(r + base, bytes);
+    if constexpr (WITH_R) load_r(r, row_base, row_tail, lane_boff, t0, C, rb);
+  }
+
+  // The receptance chunk alone (GATE).
+  __device__ static __forceinline__ void load_r(const raw* __restrict__ r, size_t row_base,
+                                                size_t row_tail, unsigned lane_boff, int t0,
+                                                int C, PackT (&rb)[L]) {
+    const rsrc_t rr = make_rsrc(r + row_base + size_t(t0) * C,
+                                span_bytes(row_tail, t0, C, int(sizeof(raw))));
+    const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
 #pragma unroll
-      for (int i = 0; i < L; ++i) load_buf(rb[i], rr, lane_boff, unsigned(i) * stride);
-    }
+    for (int i = 0; i < L; ++i) load_buf(rb[i], rr, lane_boff, unsigned(i) * stride);
   }
 
   // Phase 1 of a chunk (L steps from t0): e = 2^{k log2e} of every step
@@ -145,7 +153,14 @@ struct Fwd {
       store_vec<F32, VEC>(byte_offset(rec + 2 * ck_field, ck_boff), qin);
     }
     if constexpr (WY) {
-      OutPack<E, VEC> yp[L];
+      // GATE: each step's outputs are stored as soon as they are computed
+      // (the gate's arithmetic leaves no room to hold the chunk's L packs);
+      // otherwise the chunk's stores go out together after the last step.
+      OutPack<E, VEC> yp[GATE ? 1 : L];
+      const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
+      // (unused, hence dropped, without GATE)
+      const rsrc_t ry_gate = make_rsrc(y + row_base + size_t(t0) * C,
+                                       span_bytes(row_tail, t0, C, int(sizeof(raw))));
 #pragma unroll
       for (int i = 0; i < L; ++i) {
         float yv[VEC];
@@ -163,15 +178,19 @@ struct Fwd {
           // and sigmoid(r) each rounded to the element type, then the
           // product), language.py:1035.
           if constexpr (GATE)
-            yv[c] = round_to<E>(sigmoid_ref(rb[i].get(c))) * round_to<E>(yv[c]);
+            yv[c] = round_to<E>(gate_sigmoid<E>(rb[i].get(c))) * round_to<E>(yv[c]);
         }
-        yp[i].set(yv);
+        if constexpr (GATE) {
+          yp[0].set(yv);
+          if (active) store_buf(yp[0], ry_gate, lane_boff, unsigned(i) * stride);
+        } else {
+          yp[i].set(yv);
+        }
       }
-      if (active) {
+      if (!GATE && active) {
         // Steps past T fall outside the descriptor and are dropped.
         const rsrc_t ry = make_rsrc(y + row_base + size_t(t0) * C,
                                     span_bytes(row_tail, t0, C, int(sizeof(raw))));
-        const unsigned stride = unsigned(C) * unsigned(sizeof(raw));
 #pragma unroll
         for (int i = 0; i < L; ++i) store_buf(yp[i], ry, lane_boff, unsigned(i) * stride);
       }
@@ -256,7 +275,7 @@ __device__ void wkv4_fwd_channel_serial(const typename E::raw* __restrict__ k,
       const float bb = fast_exp2(uk - no);
       float yv = (a * p + bb * vv) / (a * q + bb);
       if (r != nullptr)
-        yv = round_to<E>(sigmoid_ref(load_scalar<E>(r + idx))) * round_to<E>(yv);
+        yv = round_to<E>(gate_sigmoid<E>(load_scalar<E>(r + idx))) * round_to<E>(yv);
       store_scalar<E>(y + idx, yv);
     }
     const float wo = w2 + o;
@@ -319,30 +338,40 @@ __global__ __launch_bounds__(W * 64) void wkv4_fwd_kernel(
   const int nseg = (T + F::SEG - 1) / F::SEG;
   const int nfull = T / F::SEG;
   PackT kA[L], vA[L], kB[L], vB[L];
-  PackT rA[L], rB[L];  // receptance chunks (loaded and used only with GATE)
+  // GATE: the receptance of the segment being computed, loaded when that
+  // segment starts (it is read only by the segment's second phase) and
+  // before the next segment's prefetch, so that waiting for it never waits
+  // for the prefetch; one buffer instead of two keeps the 16-wave tile
+  // within its 128 registers.
+  PackT rc[L];
   // The next segment is prefetched on every path (past the end the
   // descriptor is empty and the loads return zeros without touching memory):
   // with the same loads issued on every path, the compiler's wait before a
   // segment's arithmetic only covers the loads it consumes, not the prefetch
   // issued just before it.
-  if (!bad) F::load_chunk(k, v, r, row_base, row_tail, lane_boff, wave * L, C, kA, vA, rA);
+  if (!bad)
+    F::template load_chunk<false>(k, v, r, row_base, row_tail, lane_boff, wave * L, C, kA, vA, rc);
   for (int seg = 0; seg < nseg && !bad; seg += 2) {
-    F::load_chunk(k, v, r, row_base, row_tail, lane_boff, (seg + 1) * F::SEG + wave * L, C, kB, vB,
-                  rB);
+    if constexpr (GATE)
+      F::load_r(r, row_base, row_tail, lane_boff, seg * F::SEG + wave * L, C, rc);
+    F::template load_chunk<false>(k, v, r, row_base, row_tail, lane_boff,
+                                  (seg + 1) * F::SEG + wave * L, C, kB, vB, rc);
     bad = seg < nfull
               ? F::template segment<true>(sm, seg, T, C, wave, lane, active, row_base, row_tail, lane_boff, y,
-                                          ck, ck_row, ck_boff, ck_field, kA, vA, rA, D, DL, U)
+                                          ck, ck_row, ck_boff, ck_field, kA, vA, rc, D, DL, U)
               : F::template segment<false>(sm, seg, T, C, wave, lane, active, row_base, row_tail, lane_boff,
-                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, rA, D, DL, U);
+                                           y, ck, ck_row, ck_boff, ck_field, kA, vA, rc, D, DL, U);
     if (bad || seg + 1 >= nseg) break;
-    F::load_chunk(k, v, r, row_base, row_tail, lane_boff, (seg + 2) * F::SEG + wave * L, C, kA, vA,
-                  rA);
+    if constexpr (GATE)
+      F::load_r(r, row_base, row_tail, lane_boff, (seg + 1) * F::SEG + wave * L, C, rc);
+    F::template load_chunk<false>(k, v, r, row_base, row_tail, lane_boff,
+                                  (seg + 2) * F::SEG + wave * L, C, kA, vA, rc);
     bad = seg + 1 < nfull
               ? F::template segment<true>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                          row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, rB, D,
+                                          row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, rc, D,
                                           DL, U)
               : F::template segment<false>(sm, seg + 1, T, C, wave, lane, active, row_base,
-                                           row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, rB, D,
+                                           row_tail, lane_boff, y, ck, ck_row, ck_boff, ck_field, kB, vB, rc, D,
                                            DL, U);
   }
   if (bad) {
@@ -696,10 +725,7 @@ static int dispatch_fwd(const void* k, const void* v, const float* decay, int de
     WKV_FWD_SPLIT_CASE(2, 4, 16)
 #undef WKV_FWD_SPLIT_CASE
   }
-  TileCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
-  // The gated kernel holds the receptance chunks as well: at 16 waves per
-  // workgroup (128 VGPRs) the two-channel tile spills, so it runs 8 waves.
-  if (r != nullptr && cfg.vec == 2 && cfg.W == 16) cfg = TileCfg{2, cfg.L, 8};
+  const TileCfg cfg = pick_fwd_cfg(B, C, int(sizeof(typename E::raw)));
 #define WKV_FWD_CASE(V, LL, WW)                    \
   if (cfg.vec == V && cfg.L == LL && cfg.W == WW) \
     return launch_fwd<E, V, LL, WW>(k, v, decay, decay_is_w, tf, r, y, ck, B, T, C, stream);

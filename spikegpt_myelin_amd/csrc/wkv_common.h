@@ -105,6 +105,54 @@ __device__ __forceinline__ float round_to(float x) {
 // division), so values rounded from it agree with the eager path.
 __device__ __forceinline__ float sigmoid_ref(float r) { return 1.f / (1.f + expf(-r)); }
 
+// sigmoid(r) of the receptance gate, in fp32, for a gate tensor of element
+// type E: sigmoid_ref for fp32 tensors.  For the 16-bit types the forward
+// only ever uses the value rounded to the type, and the backward uses it at
+// the 16-bit bar, so a short form is enough: e = 2^x with x = -|r| log2e,
+// e in (0, 1], from the hardware exp2; sigmoid(|r|) = rcp(1 + e) and
+// sigmoid(-|r|) = e * sigmoid(|r|).  Its error (a few fp32 ulp) moves the
+// rounded value only where the exact sigmoid lies within that distance of a
+// rounding midpoint.  bf16 keeps fp32's exponent range, so for it the fp32
+// denormal range matters: below x = -126 the exponent is taken 64 higher
+// and the result scaled back by a multiply (the hardware exp2 does not
+// return denormals), and below x = -128, where the eager kernel's expf(-r)
+// overflows and its 1 / (1 + inf) is 0, the value is 0 as there.  No
+// branch: every lane runs the same instructions.
+template <typename E>
+__device__ __forceinline__ float gate_sigmoid(float r) {
+  if constexpr (__is_same(E, F32)) {
+    return sigmoid_ref(r);
+  } else {
+    const float x = -fabsf(r) * kLog2e;
+    float e, sn;
+    if constexpr (__is_same(E, BF16)) {
+      const bool tiny = x < -126.f;
+      e = fast_exp2(tiny ? x + 64.f : x);
+      sn = e * fast_rcp(1.f + e);
+      sn = tiny ? sn * 0x1p-64f : sn;
+      sn = x < -128.f ? 0.f : sn;
+    } else {
+      // fp16: sigmoid(r) is below half the smallest fp16 denormal long
+      // before e nears the fp32 denormal range, so no rescaling is needed.
+      e = fast_exp2(x);
+      sn = e * fast_rcp(1.f + e);
+    }
+    const float sp = fast_rcp(1.f + e);
+    return r >= 0.f ? sp : sn;
+  }
+}
+
+// Backward of out = round_E(s) * x, s = gate_sigmoid<E>(r), x the gated
+// input as stored in E: grad_x = round_E(g s) (returned; it feeds the
+// recurrence in the fused kernels) and grad_r = g s x (1 - s) (rounded at
+// its store), the derivative taken through the unrounded s.
+template <typename E>
+__device__ __forceinline__ float gate_backward(float g, float s, float x, float& grad_r) {
+  const float a = g * s;
+  grad_r = a * x * (1.f - s);
+  return round_to<E>(a);
+}
+
 // Vector of VEC consecutive channels as loaded by one lane in one
 // instruction: raw bits held in 32-bit words.
 template <typename E, int VEC> struct Pack;

@@ -3,9 +3,9 @@
 Bars: forward of ``relu_square`` bit-exact against ``relu(x).square()`` in
 fp32 rounded once (the autocast values); ``sigmoid_gate`` forward within one
 unit in the last place of the element type of torch's own two-kernel result
-and equal on at least 99.9 % of elements (the kernels evaluate torch's fp32
-expression; the exponential's last bit may differ), also over every 16-bit
-input;
+and equal on at least 99.9 % of elements, also over every 16-bit input, where
+bf16 is equal on every input (fp32 gates evaluate torch's expression; 16-bit
+gates a short exp2/reciprocal form whose rounded value is what counts);
 backward against float64 autograd with ``rtol=1e-5`` (fp32) or
 ``rtol=2e-2, atol=1e-2`` (16-bit).
 """
@@ -72,7 +72,10 @@ def test_sigmoid_gate(dt, shape):
 def test_sigmoid_gate_every_16bit_input(dt):
     # Every finite value of the type as r, x = 1: the gate is then the
     # rounded sigmoid itself.  Against torch's sigmoid of the same inputs:
-    # within one unit in the last place everywhere, equal on >= 99.9 %.
+    # bf16 equal everywhere (65,280 inputs, the denormal and overflow ends
+    # included); fp16 within one unit in the last place everywhere and equal
+    # on >= 99.9 % (its 10-bit mantissa puts more values near a rounding
+    # midpoint than the short sigmoid's few-ulp fp32 error can resolve).
     bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16)
     r = bits.view(dt)
     r = r[torch.isfinite(r.float())].to(DEV)
@@ -85,6 +88,8 @@ def test_sigmoid_gate_every_16bit_input(dt):
           f"{float((diff / ulp).max()):.3f}")
     assert bool((diff <= ulp).all()), float((diff / ulp).max())
     assert equal >= 0.999
+    if dt == torch.bfloat16:
+        assert torch.equal(y, ref)
 
 
 def test_module_functions_route_and_differentiate():
