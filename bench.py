@@ -220,6 +220,13 @@ def read_traffic(path: Path, kernel: str) -> int | None:
     return int(m.group(1)) if m else None
 
 
+def event_offset(args) -> int:
+    """Step (mod --event-every) whose launches carry the timing events: the
+    middle of the first block of steps, not the timed region's first step
+    (which follows a synchronisation), as long as the region has it."""
+    return min(args.event_every // 2, max(args.steps - 1, 0))
+
+
 class EventPool:
     """Timing events created and recorded once before the timed region (a
     HIP event is created at its first record, which costs host time that
@@ -345,7 +352,7 @@ def bench_wkv4(args, cfg) -> dict:
         # Every `event_every`-th step carries the events (from the middle of
         # the first block on, not the region's first step, which follows the
         # synchronisation), so the other steps run undisturbed.
-        timed_step = i % args.event_every == args.event_every // 2
+        timed_step = i % args.event_every == event_offset(args)
         step(events if timed_step else None, kernel=dom_index)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -742,7 +749,7 @@ def bench_lif(args) -> dict:
     evs, fevs = [], []
     t0 = time.perf_counter()
     for i in range(args.steps):
-        if i % args.event_every == args.event_every // 2:
+        if i % args.event_every == event_offset(args):
             s_ev, e_ev = pool.take(), pool.take()
             _lib.arm_events(s_ev, e_ev)
             fwd()
@@ -950,7 +957,7 @@ def bench_timemix(args) -> dict:
     evs, fevs = [], []
     t0 = time.perf_counter()
     for i in range(args.steps):
-        if i % args.event_every == args.event_every // 2:
+        if i % args.event_every == event_offset(args):
             s_ev, e_ev = pool.take(), pool.take()
             _lib.arm_events(s_ev, e_ev)
             fwd()
