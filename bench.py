@@ -8,12 +8,16 @@ that is already resident in HBM.
 The timed region issues that step through the C ABI on buffers allocated
 once (``wkv4_forward_checkpointed`` then ``wkv4_backward_checkpointed``, the
 two launches the autograd path makes), so the number is the kernels' own
-throughput; the same work through the torch.library op path (dispatch,
-allocation and autograd on every call) is reported as ``op_ms_per_step``,
-and as ``op_ms_per_step_backward_on_calling_thread`` with the autograd
-engine's per-device worker threads switched off
+throughput; the same work through the Python API the reference's time mix
+calls (``weighted_key_value_triton_bf16io``: dispatch, allocation and
+autograd on every call) is reported as ``op_ms_per_step``, as
+``op_ms_per_step_backward_on_calling_thread`` with the autograd engine's
+per-device worker threads switched off
 (``torch.autograd.set_multithreading_enabled(False)``), which removes the
-engine's hand-off of every backward to its device thread.
+engine's hand-off of every backward to its device thread, and through the
+public op ``myelin::wkv_forward_bf16io`` called directly (its autograd saves
+only the inputs and its backward recomputes the forward's records, as the
+reference's does) as ``public_op_ms_per_step``.
 
 Reported beside the throughput:
 * ``roofline`` -- the dominant kernel (the backward's reverse sweep,
@@ -289,21 +293,32 @@ def bench_wkv4(args, cfg) -> dict:
                                                   gtf.data_ptr(), ws.data_ptr(), bws_bytes,
                                                   B, T, C, code, sp), "backward")
 
-    # The same work through the drop-in op path (torch.library dispatch,
-    # allocation and autograd on every call), for reference; timed first, in
-    # a process with no timing events outstanding.
+    # The same work through the drop-in entry points (dispatch, allocation and
+    # autograd on every call), for reference; timed first, in a process with
+    # no timing events outstanding.  `api`: the Python API the reference's
+    # SpikeTimeMix calls (weighted_key_value_triton{,_bf16io}), whose backward
+    # reads the forward's records; `public_op`: the public torch.library op
+    # called directly, whose autograd saves only the inputs and whose backward
+    # op computes the records again, as the reference's does.
+    from spikegpt_myelin_amd import weighted_key_value_triton, weighted_key_value_triton_bf16io
+
     leaves = [x.detach().requires_grad_(True) for x in (k, v, td, tf)]
-    fwd_op = torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32 else torch.ops.myelin.wkv_forward
+    routes = {
+        "api": weighted_key_value_triton_bf16io if dtype != torch.float32
+        else weighted_key_value_triton,
+        "public_op": torch.ops.myelin.wkv_forward_bf16io if dtype != torch.float32
+        else torch.ops.myelin.wkv_forward,
+    }
 
-    def op_step():
-        for _ in range(layers):
-            if fwd_only:
-                with torch.no_grad():
-                    fwd_op(*leaves)
-            else:
-                torch.autograd.grad(fwd_op(*leaves), leaves, dy)
+    def time_op_path(fwd_op):
+        def op_step():
+            for _ in range(layers):
+                if fwd_only:
+                    with torch.no_grad():
+                        fwd_op(*leaves)
+                else:
+                    torch.autograd.grad(fwd_op(*leaves), leaves, dy)
 
-    def time_op_path():
         for _ in range(args.warmup):
             op_step()
         torch.cuda.synchronize()
@@ -313,11 +328,12 @@ def bench_wkv4(args, cfg) -> dict:
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / args.steps
 
-    op_step_s = time_op_path()
+    op_step_s = time_op_path(routes["api"])
+    public_op_step_s = time_op_path(routes["public_op"])
     # The same with the autograd engine running the backward on the calling
     # thread (no hand-off to its per-device worker thread).
     with torch.autograd.set_multithreading_enabled(False):
-        op_step_1t_s = time_op_path()
+        op_step_1t_s = time_op_path(routes["api"])
 
     dom_name = "fwd" if fwd_only else "bwd"
     # The dominant kernel: the reverse sweep of the backward (the forward for
@@ -411,6 +427,7 @@ def bench_wkv4(args, cfg) -> dict:
         "op_ms_per_step": op_step_s * 1e3,
         "op_tokens_per_s": B * T / op_step_s,
         "op_ms_per_step_backward_on_calling_thread": op_step_1t_s * 1e3,
+        "public_op_ms_per_step": public_op_step_s * 1e3,
         "fwd_launch_us": fwd_s * 1e6,
     }
     dom_t = statistics.mean(per[dom_name])

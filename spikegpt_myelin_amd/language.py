@@ -2,8 +2,9 @@
 
 ``weighted_key_value`` keeps the reference's validation (``language.py:379-396``,
 same ``ValueError`` messages) and the dispatch of ``SpikeTimeMix.forward``
-(``language.py:1028-1032``): bfloat16/float16 inputs go to the 16-bit-I/O op,
-everything else to the fp32 op.  The reference's third branch -- an eager
+(``language.py:1028-1032``): bfloat16/float16 inputs go to the 16-bit-I/O
+entry point (``weighted_key_value_triton_bf16io``), everything else to the
+fp32 one.  The reference's third branch -- an eager
 ``associative_scan`` on CPU (``language.py:1033-1034``) -- has no counterpart
 here: the ops run on the GPU only and raise on CPU tensors.
 """

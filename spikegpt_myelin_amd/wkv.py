@@ -13,15 +13,18 @@ rules and results):
 * ``myelin::wkv_forward_bf16io`` / ``myelin::wkv_backward_bf16io`` --
   ``src/spikegpt/wkv_bf16.py:143-215``: native 16-bit I/O, fp32 state.
 
-Autograd.  The reference saves the four inputs and its backward kernel
-replays the whole forward (``wkv_triton.py:85-115``).  Here the public
-forward ops are composites of the private op ``myelin::wkv4_forward_train``,
-which returns ``y`` together with small forward-state checkpoint records
-(``[3, B, ceil(T/64), C]`` fp32, ~0.19 B per element); its registered backward
-(``myelin::wkv4_backward_train``) reads the sequence once from those records.
-Gradients are the same quantities as the reference's
-(``wkv_triton.py:200-218``).  ``myelin::wkv_backward*`` remain standalone ops
-that recompute the records themselves.
+Autograd.  The public forward ops are registered as the reference registers
+them: opaque custom ops whose autograd saves the four inputs and calls the
+public backward op, which computes the forward-state records from the inputs
+before its reverse sweep (the reference's backward kernel replays the whole
+forward, ``wkv_triton.py:85-115``).  The Python API
+(:func:`weighted_key_value_hip` and the reference's names) runs the private
+op ``myelin::wkv4_forward_train`` instead (or, in eager mode, a plain
+``autograd.Function`` over the same launchers), which returns ``y`` together
+with small forward-state checkpoint records (``[3, B, ceil(T/64), C]`` fp32,
+~0.19 B per element) that autograd saves; its backward
+(``myelin::wkv4_backward_train``) reads the sequence once from them.  Values
+and gradients are the same on both routes.
 
 Python API (``wkv_triton.py:221-228``, ``wkv_bf16.py:218-231``):
 :func:`weighted_key_value_hip` and :func:`weighted_key_value_hip_bf16io`, also
@@ -398,23 +401,67 @@ def weighted_key_value_gated(key: Tensor, value: Tensor, time_decay: Tensor, tim
 
 
 # ------------------------------------------------------------ public ops ----
-_LIB = torch.library.Library("myelin", "FRAGMENT")
-_LIB.define("wkv_forward(Tensor key, Tensor value, Tensor time_decay, Tensor time_first) -> Tensor")
-_LIB.define("wkv_forward_bf16io(Tensor key, Tensor value, Tensor time_decay, Tensor time_first) -> Tensor")
-
-
-def _forward_composite(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
-    # fp32 recurrence on the exactly widened inputs; y in key.dtype
-    # (wkv_triton.py:151-158; bf16io: wkv_bf16.py:147-154).
-    if _eager(key):
-        y = _Wkv4TrainFn.apply(key, value, time_decay, time_first)
-    else:
-        y, _ = torch.ops.myelin.wkv4_forward_train(key, value, time_decay, time_first)
+# myelin::wkv_forward / myelin::wkv_forward_bf16io as the reference registers
+# them (wkv_triton.py:147-162, 200-218; wkv_bf16.py:143-158, 197-215):
+# opaque custom ops with a fake implementation, whose autograd saves the four
+# inputs and calls the public backward op (which computes the forward-state
+# records from the inputs before its reverse sweep, as the reference's
+# backward kernel replays the forward).  The Python API below takes the
+# record-saving route instead; values are identical.
+@torch.library.custom_op("myelin::wkv_forward", mutates_args=())
+def _wkv_forward_op(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
+    # fp32 recurrence on the exactly widened inputs; y in key.dtype.
+    y, _ = _launch_forward(key, value, time_decay, time_first, with_checkpoint=False)
     return y if y.dtype == key.dtype else y.to(key.dtype)
 
 
-_LIB.impl("wkv_forward", _forward_composite, "CompositeImplicitAutograd")
-_LIB.impl("wkv_forward_bf16io", _forward_composite, "CompositeImplicitAutograd")
+@_wkv_forward_op.register_fake
+def _(key, value, time_decay, time_first):
+    return torch.empty_like(key)
+
+
+@torch.library.custom_op("myelin::wkv_forward_bf16io", mutates_args=())
+def _wkv_forward_bf16io_op(
+    key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor
+) -> Tensor:
+    # Native 16-bit I/O, fp32 recurrence in registers.
+    y, _ = _launch_forward(key, value, time_decay, time_first, with_checkpoint=False)
+    return y if y.dtype == key.dtype else y.to(key.dtype)
+
+
+@_wkv_forward_bf16io_op.register_fake
+def _(key, value, time_decay, time_first):
+    return torch.empty_like(key)
+
+
+def _public_setup_context(ctx, inputs, output):
+    key, value, time_decay, time_first = inputs
+    ctx.save_for_backward(key, value, time_decay, time_first)
+
+
+def _public_backward(ctx, grad_y):
+    # wkv_triton.py:204-216: fp32 copies of every input.
+    key, value, time_decay, time_first = ctx.saved_tensors
+    w = (-torch.exp(time_decay.float())).contiguous()
+    u = time_first.float().contiguous()
+    gk, gv, gtd, gtf = torch.ops.myelin.wkv_backward(
+        grad_y.float().contiguous(), w, u, key.float().contiguous(), value.float().contiguous())
+    return gk.to(key.dtype), gv.to(value.dtype), gtd.to(time_decay.dtype), gtf.to(time_first.dtype)
+
+
+def _public_backward_bf16io(ctx, grad_y):
+    # wkv_bf16.py:201-213: k, v and the gradient in their native dtype.
+    key, value, time_decay, time_first = ctx.saved_tensors
+    w = (-torch.exp(time_decay.float())).contiguous()
+    u = time_first.float().contiguous()
+    gk, gv, gtd, gtf = torch.ops.myelin.wkv_backward_bf16io(
+        grad_y.contiguous(), w, u, key.contiguous(), value.contiguous())
+    return gk.to(key.dtype), gv.to(value.dtype), gtd.to(time_decay.dtype), gtf.to(time_first.dtype)
+
+
+_wkv_forward_op.register_autograd(_public_backward, setup_context=_public_setup_context)
+_wkv_forward_bf16io_op.register_autograd(_public_backward_bf16io,
+                                         setup_context=_public_setup_context)
 
 
 @torch.library.custom_op("myelin::wkv_backward", mutates_args=())
@@ -446,21 +493,34 @@ def wkv_forward_no_checkpoint(key: Tensor, value: Tensor, time_decay: Tensor, ti
 
 
 # ------------------------------------------------------------- Python API --
+def _train_forward(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
+    """y in key.dtype with autograd saving the checkpoint records: eager calls
+    on GPU tensors run ``_Wkv4TrainFn``; calls under tracing, fake tensors,
+    functorch transforms or a dispatch mode run the private custom op
+    ``myelin::wkv4_forward_train``.  Tensors off the GPU raise."""
+    if _eager(key):
+        y = _Wkv4TrainFn.apply(key, value, time_decay, time_first)
+    else:
+        y, _ = torch.ops.myelin.wkv4_forward_train(key, value, time_decay, time_first)
+    return y if y.dtype == key.dtype else y.to(key.dtype)
+
+
 def weighted_key_value_hip(key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor) -> Tensor:
-    """RWKV WKV recurrence via the fused HIP custom op (``myelin::wkv_forward``)."""
-    return torch.ops.myelin.wkv_forward(key, value, time_decay, time_first)
+    """RWKV WKV recurrence (``wkv_triton.py:221-228``): the values of
+    ``myelin::wkv_forward`` (fp32 recurrence, y in ``key.dtype``), with the
+    backward reading the forward's checkpoint records instead of replaying
+    the forward."""
+    return _train_forward(key, value, time_decay, time_first)
 
 
 def weighted_key_value_hip_bf16io(
     key: Tensor, value: Tensor, time_decay: Tensor, time_first: Tensor
 ) -> Tensor:
-    """RWKV WKV via the 16-bit-I/O HIP custom op (``myelin::wkv_forward_bf16io``).
-
-    Same values as :func:`weighted_key_value_hip` for bf16/fp16 inputs (the
-    widening to fp32 is exact and the output rounding is the same), without
-    the fp32 copies of k and v.
-    """
-    return torch.ops.myelin.wkv_forward_bf16io(key, value, time_decay, time_first)
+    """RWKV WKV with native 16-bit I/O (``wkv_bf16.py:218-231``): the values of
+    ``myelin::wkv_forward_bf16io``, the same as :func:`weighted_key_value_hip`
+    for bf16/fp16 inputs (the widening to fp32 is exact and the output
+    rounding is the same), without fp32 copies of k and v."""
+    return _train_forward(key, value, time_decay, time_first)
 
 
 # The reference's public names for the same two entry points.

@@ -562,9 +562,8 @@ def test_reduce_overhead_compile_replays_match_eager():
 def test_opcheck_public_ops(fwd, bwd, dtype):
     # torch.library's own checks on the four public ops: schema and mutation,
     # autograd registration, fake-tensor shapes, AOT dispatch (static and
-    # dynamic shapes).  The forwards are CompositeImplicitAutograd bodies
-    # over myelin::wkv4_forward_train (so that autograd saves the checkpoint
-    # records); the backwards are opaque custom ops, as in the reference.
+    # dynamic shapes).  All four are opaque custom ops, as in the reference;
+    # the forwards' autograd saves the inputs and calls the backward ops.
     k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(2, 40, 64, seed=16, dtype=dtype))
     fop, bop = getattr(torch.ops.myelin, fwd).default, getattr(torch.ops.myelin, bwd).default
     torch.library.opcheck(fop, (k, v, td, tf))
@@ -716,3 +715,31 @@ def test_c_abi_launches_replay_in_a_hip_graph(shape, split, monkeypatch):
     ref = _oracle64_fast(*(x.cpu() for x in (k, v, td, tf, gy)))
     for got, r, name in zip((y, *outs), ref, ("y", "gk", "gv", "gtd", "gtf")):
         _close(got, r, what=f"graph {name}", **_bf16_tol(name))
+
+
+@pytest.mark.parametrize("fwd,api,dtype", [
+    ("wkv_forward", "weighted_key_value_triton", torch.float32),
+    ("wkv_forward_bf16io", "weighted_key_value_triton_bf16io", torch.bfloat16),
+    ("wkv_forward", "weighted_key_value_triton", torch.bfloat16)])
+def test_public_ops_are_opaque_and_equal_the_api(fwd, api, dtype):
+    # The public forward ops are opaque custom ops whose autograd saves the
+    # inputs and calls the public backward op (wkv_triton.py:147-218,
+    # wkv_bf16.py:143-215): a trace keeps them as single nodes.  The Python
+    # API saves the forward's records instead; values and gradients are the
+    # same bit for bit.
+    import spikegpt_myelin_amd as P
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    op = getattr(torch.ops.myelin, fwd)
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(3, 200, 192, seed=41, dtype=dtype))
+    traced = make_fx(lambda *a: op(*a))(k, v, td, tf)
+    targets = {str(n.target) for n in traced.graph.nodes if n.op == "call_function"}
+    assert f"myelin.{fwd}.default" in targets, targets
+    assert not any("wkv4_forward_train" in t for t in targets), targets
+    api_traced = make_fx(lambda *a: getattr(P, api)(*a))(k, v, td, tf)
+    api_targets = {str(n.target) for n in api_traced.graph.nodes if n.op == "call_function"}
+    assert "myelin.wkv4_forward_train.default" in api_targets, api_targets
+    via_op = _grads(op, k, v, td, tf, gy)
+    via_api = _grads(getattr(P, api), k, v, td, tf, gy)
+    for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), via_op, via_api):
+        assert a.dtype == b.dtype and torch.equal(a, b), name
