@@ -565,7 +565,8 @@ def test_opcheck_public_ops(fwd, bwd, dtype):
     # dynamic shapes).  All four are opaque custom ops, as in the reference;
     # the forwards' autograd saves the inputs and calls the backward ops.
     k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(2, 40, 64, seed=16, dtype=dtype))
-    fop, bop = getattr(torch.ops.myelin, fwd).default, getattr(torch.ops.myelin, bwd).default
+    ops = _lib_ops()
+    fop, bop = getattr(ops, fwd).default, getattr(ops, bwd).default
     torch.library.opcheck(fop, (k, v, td, tf))
     leaves = tuple(x.clone().requires_grad_(True) for x in (k, v, td, tf))
     torch.library.opcheck(fop, leaves)
@@ -743,3 +744,23 @@ def test_public_ops_are_opaque_and_equal_the_api(fwd, api, dtype):
     via_api = _grads(getattr(P, api), k, v, td, tf, gy)
     for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), via_op, via_api):
         assert a.dtype == b.dtype and torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("fwd,dtype", [("wkv_forward", torch.float32),
+                                       ("wkv_forward_bf16io", torch.bfloat16)])
+def test_public_ops_compile_fullgraph_with_backward(fwd, dtype):
+    # A caller that compiles code calling the public op directly (the
+    # reference's ops are torch.library custom ops, traced opaquely through
+    # their fake implementations): one graph, no breaks, and the compiled
+    # forward and backward equal the eager op's bit for bit.
+    op = getattr(_lib_ops(), fwd)
+    k, v, td, tf, gy = (x.to(DEV) for x in O.make_inputs(3, 150, 192, seed=43, dtype=dtype))
+
+    def f(k_, v_, td_, tf_):
+        return op(k_, v_, td_, tf_) * 2.0
+
+    cf = torch.compile(f, backend="aot_eager", fullgraph=True)
+    eager, compiled = _grads(f, k, v, td, tf, gy), _grads(cf, k, v, td, tf, gy)
+    for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), eager, compiled):
+        assert a.dtype == b.dtype and torch.equal(a, b), name
+    torch._dynamo.reset()
