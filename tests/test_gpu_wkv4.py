@@ -407,6 +407,22 @@ def test_split_over_time_matches_oracle(dtype, b, t, c, seed, monkeypatch):
         _close(got, r, what=f"split training path {name}", **tol(name))
 
 
+@pytest.mark.parametrize("split", ["0", "1"])
+def test_very_long_single_row(split, monkeypatch):
+    # One row of 16,384 steps (256 split segments, 128 one-row segments): the
+    # look-back chain and the one-row kernel's segment loop over a sequence
+    # five times the long-context recipe's, through the training path.
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    monkeypatch.setenv("WKV_SPLIT", split)
+    print(f"very long row B=1 T=16384 C=64 bf16 split={split}", flush=True)
+    k, v, td, tf, gy = O.make_inputs(1, 16384, 64, seed=37, dtype=torch.bfloat16)
+    got = _grads(weighted_key_value_hip_bf16io, *(x.to(DEV) for x in (k, v, td, tf, gy)))
+    ref = _oracle64_fast(k, v, td, tf, gy)
+    for g, r, name in zip(got, ref, ("y", "gk", "gv", "gtd", "gtf")):
+        _close(g, r, what=f"long row split={split} {name}", **_bf16_tol(name))
+
+
 @pytest.mark.parametrize("fcfg,bcfg", [("1,8,8", "1,8,8"), ("1,8,16", "1,16,4"),
                                        ("1,16,4", "1,8,16"), ("2,8,8", "2,8,8"),
                                        ("1,4,16", "2,4,16"), ("2,4,16", "1,4,16")])
