@@ -42,12 +42,22 @@ struct LifParams {
   float decay, threshold, reset, slope;
 };
 
-// Arctan surrogate derivative ds/dh = slope * 0.5 / (1 + (pi/2 c)^2) at
-// c = slope (h - threshold), with the hardware reciprocal (1 ulp) in place
-// of an IEEE division (~9 instructions on this recurrence's critical path).
-__device__ __forceinline__ float lif_surrogate(float cc, float slope) {
+// One reverse step of the LIF backward: dL/dh_t for the incoming gradient
+// g of s_t and the carried gradient gm (dL/dm_t), at h = h_t and
+// c = slope (h_t - threshold), with the arctan surrogate derivative
+// ds/dh = slope * 0.5 / (1 + (pi/2 c)^2):
+//   dL/dh = g ds/dh + gm ((1 - s) + (reset - h) ds/dh)
+//         = (slope/2) rcp(1 + q^2) (g + gm (reset - h)) + (s ? 0 : gm)
+// with q = (pi/2) c, the hardware reciprocal (1 ulp) in place of an IEEE
+// division, and fused multiply-adds (9 instructions instead of 14).  lif_bwd_scale gives (slope/2) rcp(1 + q^2) and
+// lif_bwd_dh the rest, so that two carries at one step share the scale.
+__device__ __forceinline__ float lif_bwd_scale(float cc, float slope) {
   const float q = 1.5707963267948966f * cc;
-  return (0.5f * slope) * __builtin_amdgcn_rcpf(fmaf(q, q, 1.f));
+  return __builtin_amdgcn_rcpf(fmaf(q, q, 1.f)) * (0.5f * slope);
+}
+__device__ __forceinline__ float lif_bwd_dh(float g, float gm, float h, float cc, float scale,
+                                            float reset) {
+  return fmaf(scale, fmaf(gm, reset - h, g), cc >= 0.f ? 0.f : gm);
 }
 
 // Loads S steps starting at t0 for the lane (buffer descriptor based at the
@@ -172,9 +182,8 @@ __device__ __forceinline__ void lif_bwd_block(const Pack<E, VEC> (&xb)[kLifBlock
     for (int c = 0; c < VEC; ++c) {
       const float hh = h[i][c];
       const float cc = P.slope * (hh - P.threshold);
-      const float s = cc >= 0.f ? 1.f : 0.f;
-      const float dsdh = lif_surrogate(cc, P.slope);
-      const float gh = gb[i].get(c) * dsdh + gm[c] * ((1.f - s) + (P.reset - hh) * dsdh);
+      const float gh = lif_bwd_dh(gb[i].get(c), gm[c], hh, cc, lif_bwd_scale(cc, P.slope),
+                                  P.reset);
       gv[c] = gh;
       gm[c] = P.decay * gh;
     }
@@ -688,9 +697,8 @@ __global__ __launch_bounds__(64) void lif_bwd_staged_kernel(const typename E::ra
 #pragma unroll
     for (int s = kLifBlock - 1; s >= 0; --s) {
       const float cc = cs[s];
-      const float sp = cc >= 0.f ? 1.f : 0.f;
-      const float dsdh = lif_surrogate(cc, P.slope);
-      const float gh = SG::get(gl, s, lane) * dsdh + gm * ((1.f - sp) + (P.reset - h[s]) * dsdh);
+      const float gh = lif_bwd_dh(SG::get(gl, s, lane), gm, h[s], cc,
+                                  lif_bwd_scale(cc, P.slope), P.reset);
       gm = P.decay * gh;
       S::put(os, s, lane, gh);
     }
@@ -789,11 +797,9 @@ __global__ __launch_bounds__(64) void lif_bwd_fixup_kernel(const typename E::raw
         const int t = t0 + s;
         const bool live = todo && t < T;
         const float cc = P.slope * (h[s] - P.threshold);
-        const float sp = cc >= 0.f ? 1.f : 0.f;
-        const float dsdh = lif_surrogate(cc, P.slope);
-        const float a = (1.f - sp) + (P.reset - h[s]) * dsdh;
-        const float gh = gv[s] * dsdh + gm * a;
-        const float ghs = gv[s] * dsdh + gms * a;
+        const float scale = lif_bwd_scale(cc, P.slope);
+        const float gh = lif_bwd_dh(gv[s], gm, h[s], cc, scale, P.reset);
+        const float ghs = lif_bwd_dh(gv[s], gms, h[s], cc, scale, P.reset);
         if (live && __float_as_uint(gh) != __float_as_uint(ghs))
           store_scalar<E>(gx + (size_t(b) * T + size_t(t)) * C + size_t(c), gh);
         if (t < T) {
