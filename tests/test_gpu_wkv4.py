@@ -195,12 +195,14 @@ def test_fp32_op_with_bf16_inputs_returns_bf16_like_reference():
     assert torch.equal(y, ref)
 
 
-def test_bf16_benchmark_shape_full_size():
-    # B=64, T=1024, C=512 bf16 (the headline workload) against the fp64 oracle,
-    # plus size-independent gradient invariants.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_bf16_benchmark_shape_full_size(dtype):
+    # B=64, T=1024, C=512 (the headline workload; bf16, and fp16 through the
+    # same op) against the fp64 oracle, plus size-independent gradient
+    # invariants.
     ops = _lib_ops()
     b, t, c = 64, 1024, 512
-    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=1, dtype=torch.bfloat16)
+    k, v, td, tf, gy = O.make_inputs(b, t, c, seed=1, dtype=dtype)
     kd, vd, tdd, tfd, gyd = (x.to(DEV) for x in (k, v, td, tf, gy))
     y = ops.wkv_forward_bf16io(kd, vd, tdd, tfd)
     gk, gv, gtd, gtf = ops.wkv_backward_bf16io(gyd, -torch.exp(tdd), tfd, kd, vd)
