@@ -183,7 +183,7 @@ def _ln_shift_mix_backward(grads: list[Tensor], x: Tensor, weight: Tensor, bias:
     xs = _lib.aligned(x)
     w, bb, mx = (_lib.aligned(p.float()) for p in (weight, bias, mix))
     gx = torch.empty_like(xs)
-    gp = torch.zeros((n + 2, c), dtype=torch.float32, device=x.device)
+    gp = torch.empty((n + 2, c), dtype=torch.float32, device=x.device)  # every entry written
     lib = _lib.load()
     ws = torch.empty(max(int(lib.layer_norm_shift_mix_workspace_bytes(n, b, t, c)), 16),
                      dtype=torch.uint8, device=x.device)
