@@ -782,3 +782,31 @@ def test_public_ops_compile_fullgraph_with_backward(fwd, dtype):
     for name, a, b in zip(("y", "gk", "gv", "gtd", "gtf"), eager, compiled):
         assert a.dtype == b.dtype and torch.equal(a, b), name
     torch._dynamo.reset()
+
+
+def test_past_2_to_the_31_elements():
+    # B*T*C = 2064*1024*1024 > 2^31: the last batch entry starts past element
+    # 2^31, so every offset into it needs 64-bit arithmetic (row bases,
+    # record rows, the batch-sum partials).  Training path (forward with
+    # records, backward from them); that entry against the fp64 oracle.
+    from spikegpt_myelin_amd import weighted_key_value_hip_bf16io
+
+    b, t, c = 2064, 1024, 1024
+    assert b * t * c > 2 ** 31 and (b - 1) * t * c > 2 ** 31
+    print(f"past 2^31 elements: B={b} T={t} C={c} bf16", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(47)
+    k = torch.randn(b, t, c, device=DEV, generator=g).clamp_(-30, 30).to(torch.bfloat16)
+    v = torch.randn(b, t, c, device=DEV, generator=g).to(torch.bfloat16)
+    gy = torch.randn(b, t, c, device=DEV, generator=g).to(torch.bfloat16)
+    _, _, td, tf, _ = O.make_inputs(1, 1, c, seed=47, dtype=torch.bfloat16)
+    leaves = [x.requires_grad_(True) for x in (k, v, td.to(DEV), tf.to(DEV))]
+    y = weighted_key_value_hip_bf16io(*leaves)
+    y.backward(gy)
+    last = b - 1
+    got = (y[last:].detach(), leaves[0].grad[last:], leaves[1].grad[last:])
+    assert all(bool(torch.isfinite(x.grad).all()) for x in leaves[2:])
+    ref = _oracle64_fast(k[last:].detach(), v[last:].detach(), td, tf, gy[last:])
+    for gt, r, name in zip(got, ref, ("y", "gk", "gv")):
+        _close(gt, r, what=f"past 2^31 {name}", **_bf16_tol(name))
+    del k, v, gy, leaves, y, got
+    torch.cuda.empty_cache()
